@@ -1,0 +1,169 @@
+/*
+ * C ABI of the MI355X (gfx950) TriFusion-FP inference kernels.
+ *
+ * Every entry point takes plain pointers, element counts and element strides,
+ * enqueues its kernels on the given HIP stream (a hipStream_t passed as void*;
+ * NULL is the legacy default stream) and returns a tf_status. Nothing is
+ * allocated, nothing is synchronised and no host memory is read after the
+ * call returns, so every entry point may be recorded into a HIP graph.
+ * Concurrent calls on different streams are independent; the library keeps no
+ * mutable global state besides a once-initialised device-property cache.
+ *
+ * Strides are in elements (not bytes) and may be 0 (broadcast) or any other
+ * value; dtypes are tf_dtype codes.
+ */
+#ifndef TRIFUSION_AMD_H
+#define TRIFUSION_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum tf_dtype {
+  TF_FLOAT32 = 0,
+  TF_BFLOAT16 = 1,
+  TF_FLOAT16 = 2,
+} tf_dtype;
+
+typedef enum tf_status {
+  TF_OK = 0,
+  TF_ERR_NULL = 1,        /* a required pointer is NULL */
+  TF_ERR_SHAPE = 2,       /* unsupported or inconsistent dimensions */
+  TF_ERR_DTYPE = 3,       /* unsupported dtype code or combination */
+  TF_ERR_STRIDE = 4,      /* layout the selected kernel cannot read */
+  TF_ERR_VARIANT = 5,     /* requested kernel variant cannot run these arguments */
+  TF_ERR_LAUNCH = 6,      /* the HIP runtime rejected the launch */
+} tf_status;
+
+/* Kernel selection for tf_fused_mamba. */
+typedef enum tf_mamba_variant {
+  TF_MAMBA_AUTO = 0,      /* chunked MFMA kernel when supported, else generic */
+  TF_MAMBA_GENERIC = 1,   /* fp32-FMA kernel: any dtype, N <= 128, P <= 64 */
+  TF_MAMBA_MFMA = 2,      /* bf16 MFMA chunked-scan kernel (gfx950) */
+} tf_mamba_variant;
+
+/*
+ * Operands of the fused Mamba-3 SISO recurrence. Shapes (reference
+ * src/trifusion_l4/mamba_fused.py:155-191 and docs/api.md:61-74):
+ *   q, k          [B, T, Hq, N]   C and B projections (H % Hq == 0)
+ *   v, z          [B, T, H, P]    x and gate
+ *   adt, dt, trap [B, H, T]       signed decay*dt, softplus(dt), pre-sigmoid trap
+ *   qb, kb        [H, N]          fp32, contiguous (C and B biases)
+ *   angles        [B, T, H, R]    raw pre-tanh rotary controls, R <= N/2
+ *   d             [H]             fp32, contiguous (skip D)
+ *   out           [B, T, H, P]
+ *   lengths       [B] int64 or NULL: rows t >= lengths[b] are written as 0 and
+ *                 chunks wholly past the length are skipped (extension; NULL
+ *                 reproduces the reference exactly).
+ * Stride arrays follow the dimension order above.
+ */
+typedef struct tf_mamba_args {
+  const void *q, *k, *v, *adt, *dt, *trap, *angles, *z;
+  const float *qb, *kb, *d;
+  void *out;
+  const int64_t *lengths;
+  int32_t q_dtype, k_dtype, v_dtype, z_dtype;
+  int32_t adt_dtype, dt_dtype, trap_dtype, angles_dtype, out_dtype;
+  int32_t variant;
+  int64_t q_stride[4], k_stride[4], v_stride[4], z_stride[4];
+  int64_t angles_stride[4], out_stride[4];
+  int64_t adt_stride[3], dt_stride[3], trap_stride[3];
+  int64_t batch, time, heads, qk_heads, state, head_dim, rotary;
+} tf_mamba_args;
+
+/*
+ * Fused recurrence forward. Replaces the Triton launch of `_fused` in
+ * src/trifusion_l4/mamba_fused.py:155-191 (shape check :159-160, launch
+ * :162-190), generalised to N in {16,32,64,128}, P in {32,64}, R <= N/2.
+ */
+int tf_fused_mamba(const tf_mamba_args *args, void *stream);
+
+/* Which kernel TF_MAMBA_AUTO would run for these arguments (1 or 2), or a
+ * negative tf_status if no kernel can run them. */
+int tf_fused_mamba_variant(const tf_mamba_args *args);
+
+/*
+ * Row RMSNorm: y[r,:] = x[r,:] * rsqrt(mean(x[r,:]^2) + eps) * w, fp32
+ * statistics. Row r of x starts at x + r * x_row_stride (elements; the row
+ * itself is contiguous, so strided column slices of a projection need no
+ * copy); y is contiguous [rows, d]; w fp32 [d]; d <= 4096.
+ * Replaces `_norm` MODE 0 / `rms` (src/trifusion_l4/kernels/native.py:8-39,
+ * 42-70) and RMSNorm.forward (src/trifusion_l4/kernels/__init__.py:15-28).
+ */
+int tf_rmsnorm(const void *x, int32_t x_dtype, int64_t x_row_stride, const float *w,
+               void *y, int32_t y_dtype, int64_t rows, int64_t d, float eps,
+               void *stream);
+
+/*
+ * Residual add fused with the following RMSNorm:
+ *   s = (a + b) * mask[row]   (fp32 math, stored as s_dtype)
+ *   y = rmsnorm(s) * w        (stored as y_dtype)
+ * mask is uint8 [rows] or NULL; all tensors contiguous [rows, d], d <= 4096.
+ * The norm reads s as stored. Combines `add` (native.py:81-100) and the next
+ * block's `_norm` MODE 0 (native.py:8-39) in one pass over the rows.
+ */
+int tf_add_rmsnorm(const void *a, int32_t a_dtype, const void *b, int32_t b_dtype,
+                   const uint8_t *mask, const float *w, void *s, int32_t s_dtype,
+                   void *y, int32_t y_dtype, int64_t rows, int64_t d, float eps,
+                   void *stream);
+
+/*
+ * SwiGLU: y[r, j] = silu(x[r, j]) * x[r, d + j], fp32 math. x contiguous
+ * [rows, 2d], y contiguous [rows, d]. Replaces `swiglu`/`_swiglu`
+ * (src/trifusion_l4/kernels/__init__.py:31-41, kernels/primitives.py:25-37).
+ */
+int tf_swiglu(const void *x, void *y, int32_t dtype, int64_t rows, int64_t d,
+              void *stream);
+
+/*
+ * Row mask: y[r,:] = mask[r] ? x[r,:] : 0 over contiguous [rows, d].
+ * Replaces `mask_buffer`/`_mask` (src/trifusion_l4/kernels/buffers.py:6-10,
+ * kernels/primitives.py:65-70).
+ */
+int tf_mask_rows(const void *x, void *y, int32_t dtype, const uint8_t *mask,
+                 int64_t rows, int64_t d, void *stream);
+
+/*
+ * y = a + b in fp32 (rows with mask[r] == 0 give 0 when mask is non-NULL),
+ * stored as y_dtype; contiguous [rows, d]. Replaces `add`/`_add`
+ * (src/trifusion_l4/kernels/native.py:81-100).
+ */
+int tf_add(const void *a, int32_t a_dtype, const void *b, int32_t b_dtype,
+           const uint8_t *mask, void *y, int32_t y_dtype, int64_t rows, int64_t d,
+           void *stream);
+
+/*
+ * Mamba-3 controls: for a, ddt read as [B, T, H] with strides (sb, st, 1):
+ *   dt  = softplus(ddt + bias[h])  (linear above 20)
+ *   adt = -max(relu(a) + 1/(1 - min(a, 0)), floor) * dt
+ * written as contiguous fp32 [B, H, T]. Replaces `mamba_controls`/`_controls`
+ * (src/trifusion_l4/kernels/buffers.py:82-101, kernels/primitives.py:190-216).
+ */
+int tf_mamba_controls(const void *a, const void *ddt, int32_t dtype, int64_t sb,
+                      int64_t st, const float *bias, float *adt, float *dt,
+                      int64_t batch, int64_t time, int64_t heads, float floor_,
+                      void *stream);
+
+/*
+ * Masked mean over time: y[b, :] = sum_{t < lengths[b]} x[b, t, :] / lengths[b]
+ * in fp32; x contiguous [B, T, D], y fp32 [B, D]. Replaces the global-feature
+ * pooling of src/trifusion_l4/decoder.py:60-62.
+ */
+int tf_masked_mean(const void *x, int32_t dtype, const int64_t *lengths, float *y,
+                   int64_t batch, int64_t time, int64_t d, void *stream);
+
+/* Row mask from lengths: mask[b*T + t] = t < lengths[b] (uint8). Replaces
+ * time_mask (src/trifusion_l4/masking.py:6-7) on the device. */
+int tf_time_mask(const int64_t *lengths, uint8_t *mask, int64_t batch, int64_t time,
+                 void *stream);
+
+/* Library version string (static storage). */
+const char *tf_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TRIFUSION_AMD_H */

@@ -1,0 +1,76 @@
+"""CPU restatements of the bandwidth-bound ops around the recurrence (oracle).
+
+Test infrastructure only (see ``oracle/__init__.py``). Each function restates
+one reference formula in fp32 PyTorch on the CPU.
+
+Pinning (tests/test_oracle_elementwise.py): ``rms_norm`` against
+``torch.nn.functional.rms_norm``; ``swiglu`` against ``F.silu(g) * u`` on an
+independently split tensor; ``mamba_controls`` against ``F.softplus`` (same
+threshold 20) and hand-evaluated special cases of the decay control;
+``masked_mean`` against a Python loop over valid frames; ``mask_rows`` and
+``add`` against explicit ``torch.where`` forms.
+"""
+
+import torch
+import torch.nn.functional as F
+
+
+def rms_norm(x, weight, eps=1e-5):
+    """``y = x * rsqrt(mean(x^2) + eps) * w`` with fp32 statistics, output in x's dtype.
+
+    Reference: ``src/trifusion_l4/kernels/__init__.py:10-12`` (``rms_reference``) and
+    the MODE-0 row kernel ``src/trifusion_l4/kernels/native.py:8-39,42-70``.
+    """
+    xf = x.float()
+    return (xf * torch.rsqrt(xf.square().mean(-1, keepdim=True) + eps) * weight.float()).to(x.dtype)
+
+
+def swiglu(x):
+    """``silu(g) * u`` over the two halves of the last dim, fp32 math.
+
+    Reference: ``src/trifusion_l4/kernels/__init__.py:31-34``;
+    ``src/trifusion_l4/kernels/primitives.py:25-37``.
+    """
+    gate, up = x.float().chunk(2, -1)
+    return (F.silu(gate) * up).to(x.dtype)
+
+
+def time_mask(lengths, time):
+    """``mask[b, t] = t < lengths[b]`` (``src/trifusion_l4/masking.py:6-7``)."""
+    return torch.arange(time, device=lengths.device)[None, :] < lengths[:, None]
+
+
+def mask_rows(x, mask):
+    """Zero rows whose mask is false (``masking.py:10-11``; ``primitives.py:65-70``)."""
+    return x.masked_fill(~mask[..., None], 0)
+
+
+def add(a, b, mask=None, bf16=False):
+    """``a + b`` in fp32, rows with a false mask set to 0 (``native.py:81-100``)."""
+    y = a.float() + b.float()
+    if mask is not None:
+        y = y.masked_fill(~mask.reshape(*y.shape[:-1], 1), 0)
+    dtype = torch.bfloat16 if bf16 else torch.promote_types(a.dtype, b.dtype)
+    return y.to(dtype)
+
+
+def mamba_controls(a, ddt, dt_bias, floor=1e-4):
+    """Discretisation controls of the Mamba-3 block.
+
+    ``dt = softplus(ddt + dt_bias)`` (threshold 20) and
+    ``adt = -max(relu(a) + 1/(1 - min(a, 0)), floor) * dt``, both returned as
+    contiguous ``[B,H,T]`` fp32. Reference: ``src/trifusion_l4/mamba.py:58-63`` and
+    ``src/trifusion_l4/kernels/primitives.py:190-216``.
+    """
+    af = a.float()
+    v = ddt.float() + dt_bias.float()
+    control = torch.clamp_max(-(af.clamp_min(0) + 1 / (1 - af.clamp_max(0))), -floor)
+    dt = torch.where(v > 20, v, torch.log1p(torch.exp(v)))
+    adt = control * dt
+    return adt.transpose(1, 2).contiguous(), dt.transpose(1, 2).contiguous()
+
+
+def masked_mean(x, lengths):
+    """Masked mean over time, ``sum_t x*mask / length`` in fp32 (``decoder.py:60-62``)."""
+    mask = time_mask(lengths, x.shape[1])
+    return (x.float() * mask[..., None]).sum(1) / lengths[:, None]

@@ -1,0 +1,121 @@
+"""Parity of the HIP bandwidth kernels against the CPU oracle (MI355X)."""
+
+import pytest
+import torch
+
+from oracle import elementwise as E
+from trifusion_amd.kernels import RMSNorm, swiglu
+from trifusion_amd.kernels.buffers import mamba_controls, mask_buffer
+from trifusion_amd.kernels.native import add, add_rms, rms
+from trifusion_amd.masking import masked_mean, time_mask
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("rows,d", [(6400, 512), (7, 64), (33, 1365), (5, 4096), (1, 1)])
+def test_rmsnorm(dtype, rows, d):
+    g = gen(rows + d)
+    x = torch.randn(rows, d, generator=g).to(dtype)
+    w = torch.rand(d, generator=g) + 0.5
+    y = rms(x.to(DEV), w.to(DEV)).cpu()
+    ref = E.rms_norm(x, w)
+    assert y.dtype == dtype
+    if dtype == torch.float32:
+        torch.testing.assert_close(y, ref, rtol=1e-5, atol=1e-5)
+    else:  # at most one bf16 ulp apart
+        torch.testing.assert_close(y.float(), ref.float(), rtol=2 ** -7, atol=1e-6)
+
+
+def test_rmsnorm_strided_rows_no_copy():
+    g = gen(3)
+    proj = torch.randn(4, 50, 300, generator=g).to(torch.bfloat16)
+    x = proj[..., 100:164].reshape(4, 50, 1, 64)
+    w = torch.rand(64, generator=g) + 0.5
+    dx = proj.to(DEV)[..., 100:164].reshape(4, 50, 1, 64)
+    assert not dx.is_contiguous()
+    norm = RMSNorm(64).to(DEV)
+    with torch.no_grad():
+        norm.weight.copy_(w)
+    y = norm(dx).cpu()
+    torch.testing.assert_close(y.float(), E.rms_norm(x, w).float(), rtol=2 ** -7, atol=1e-6)
+
+
+@pytest.mark.parametrize("bdtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("ydtype", [torch.float32, torch.bfloat16])
+def test_add_rmsnorm(bdtype, ydtype):
+    g = gen(4)
+    a = torch.randn(16, 400, 512, generator=g)
+    b = torch.randn(16, 400, 512, generator=g).to(bdtype)
+    mask = E.time_mask(torch.randint(1, 401, (16,), generator=g), 400)
+    w = torch.rand(512, generator=g) + 0.5
+    s, y = add_rms(a.to(DEV), b.to(DEV), w.to(DEV), mask.to(DEV), out_dtype=ydtype)
+    s_ref = E.add(a, b, mask)
+    torch.testing.assert_close(s.cpu(), s_ref, rtol=0, atol=0)
+    y_ref = E.rms_norm(s_ref, w).to(ydtype)
+    tol = 1e-5 if ydtype == torch.float32 else 2 ** -7
+    torch.testing.assert_close(y.cpu().float(), y_ref.float(), rtol=tol, atol=1e-5)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(6400, 2730), (3, 8), (1, 2)])
+def test_swiglu(dtype, shape):
+    x = torch.randn(*shape, generator=gen(5)).to(dtype)
+    y = swiglu(x.to(DEV)).cpu()
+    ref = E.swiglu(x)
+    tol = 1e-6 if dtype == torch.float32 else 2 ** -7
+    torch.testing.assert_close(y.float(), ref.float(), rtol=tol, atol=1e-6)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_mask_and_time_mask(dtype):
+    g = gen(6)
+    lengths = torch.tensor([400, 1, 0, 217])
+    x = torch.randn(4, 400, 96, generator=g).to(dtype)
+    m = time_mask(lengths.to(DEV), 400)
+    assert torch.equal(m.cpu(), E.time_mask(lengths, 400))
+    y = mask_buffer(x.to(DEV), m).cpu()
+    assert torch.equal(y, E.mask_rows(x, E.time_mask(lengths, 400)))
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_add_masked(bf16):
+    g = gen(7)
+    a = torch.randn(8, 33, 512, generator=g)
+    b = torch.randn(8, 33, 512, generator=g).to(torch.bfloat16)
+    mask = torch.rand(8, 33, generator=g) > 0.3
+    y = add(a.to(DEV), b.to(DEV), mask.to(DEV), bf16=bf16).cpu()
+    assert torch.equal(y, E.add(a, b, mask, bf16=bf16))
+    y = add(a.to(DEV), b.to(DEV)).cpu()
+    assert torch.equal(y, E.add(a, b))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_mamba_controls(dtype):
+    g = gen(8)
+    b, t, h = 16, 400, 16
+    proj = (torch.randn(b, t, 3 * h + 7, generator=g) * 3).to(dtype)
+    proj[0, 0, :h] = 30.0  # softplus linear branch
+    ddt, a = proj[..., :h], proj[..., h : 2 * h]
+    bias = torch.full((h,), -4.0) + torch.randn(h, generator=g)
+    dproj = proj.to(DEV)
+    adt, dt = mamba_controls(dproj[..., h : 2 * h], dproj[..., :h], bias.to(DEV), 1e-4)
+    adt_ref, dt_ref = E.mamba_controls(a, ddt, bias)
+    assert adt.is_contiguous() and adt.shape == (b, h, t)
+    torch.testing.assert_close(dt.cpu(), dt_ref, rtol=2e-6, atol=1e-7)
+    torch.testing.assert_close(adt.cpu(), adt_ref, rtol=2e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_masked_mean(dtype):
+    g = gen(9)
+    x = torch.randn(16, 400, 512, generator=g).to(dtype)
+    lengths = torch.randint(1, 401, (16,), generator=g)
+    lengths[0] = 400
+    y = masked_mean(x.to(DEV), lengths.to(DEV)).cpu()
+    torch.testing.assert_close(y, E.masked_mean(x, lengths), rtol=1e-5, atol=1e-6)

@@ -1,0 +1,132 @@
+// Device helpers shared by the gfx950 kernels: dtype-generic loads/stores,
+// round-to-nearest-even conversions, wave64 reductions and scans, and the
+// fast transcendentals used by the recurrence.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "trifusion_amd.h"
+
+namespace tf {
+
+constexpr float kLog2e = 1.44269504089f;  // rounded log2(e) the recurrence scales adt by
+constexpr float kPi = 3.141592653589793f;
+constexpr float kTwoPi = 6.283185307179586f;
+constexpr float kInvTwoPi = 0.15915494309189535f;
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// fp32 -> bf16 bits, round to nearest even (NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16(float x) {
+  uint32_t u = __float_as_uint(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float round_bf16(float x) { return bf16_to_f32(f32_to_bf16(x)); }
+
+__device__ __forceinline__ float round_f16(float x) {
+  return static_cast<float>(static_cast<_Float16>(x));
+}
+
+// Round an fp32 value to `dtype` and back (identity for fp32).
+__device__ __forceinline__ float round_to(float x, int dtype) {
+  if (dtype == TF_BFLOAT16) return round_bf16(x);
+  if (dtype == TF_FLOAT16) return round_f16(x);
+  return x;
+}
+
+__device__ __forceinline__ float load_f32(const void* p, int dtype, int64_t i) {
+  if (dtype == TF_BFLOAT16) return bf16_to_f32(static_cast<const uint16_t*>(p)[i]);
+  if (dtype == TF_FLOAT16) return static_cast<float>(static_cast<const _Float16*>(p)[i]);
+  return static_cast<const float*>(p)[i];
+}
+
+__device__ __forceinline__ void store_f32(void* p, int dtype, int64_t i, float x) {
+  if (dtype == TF_BFLOAT16) {
+    static_cast<uint16_t*>(p)[i] = f32_to_bf16(x);
+  } else if (dtype == TF_FLOAT16) {
+    static_cast<_Float16*>(p)[i] = static_cast<_Float16>(x);
+  } else {
+    static_cast<float*>(p)[i] = x;
+  }
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float sigmoidf(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+// x - 2pi*floor(x/2pi), the reduction the reference applies to phases.
+__device__ __forceinline__ float mod_two_pi(float x) {
+  return x - kTwoPi * floorf(x / kTwoPi);
+}
+
+// Wave64 sum via xor shuffles (every lane receives the total).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// Inclusive prefix sum across the 64 lanes of a wave (Hillis-Steele).
+__device__ __forceinline__ float wave_inclusive_scan(float v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    float o = __shfl_up(v, off, 64);
+    if (lane >= off) v += o;
+  }
+  return v;
+}
+
+// Typed element wrappers for the bandwidth kernels.
+struct bf16_t {
+  uint16_t bits;
+};
+using f16_t = _Float16;
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(bf16_t x) { return bf16_to_f32(x.bits); }
+__device__ __forceinline__ float to_f32(f16_t x) { return static_cast<float>(x); }
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float x);
+template <>
+__device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <>
+__device__ __forceinline__ bf16_t from_f32<bf16_t>(float x) { return bf16_t{f32_to_bf16(x)}; }
+template <>
+__device__ __forceinline__ f16_t from_f32<f16_t>(float x) { return static_cast<f16_t>(x); }
+
+// Calls BODY with `T` bound to the element type of dtype code `code`.
+#define TF_DISPATCH(code, T, ...)                       \
+  switch (code) {                                       \
+    case TF_FLOAT32: {                                  \
+      using T = float;                                  \
+      __VA_ARGS__;                                      \
+    } break;                                            \
+    case TF_BFLOAT16: {                                 \
+      using T = ::tf::bf16_t;                           \
+      __VA_ARGS__;                                      \
+    } break;                                            \
+    case TF_FLOAT16: {                                  \
+      using T = ::tf::f16_t;                            \
+      __VA_ARGS__;                                      \
+    } break;                                            \
+    default:                                            \
+      return TF_ERR_DTYPE;                              \
+  }
+
+inline bool dtype_ok(int d) { return d == TF_FLOAT32 || d == TF_BFLOAT16 || d == TF_FLOAT16; }
+
+inline int dtype_size(int d) { return d == TF_FLOAT32 ? 4 : 2; }
+
+inline int launch_status() {
+  return hipGetLastError() == hipSuccess ? TF_OK : TF_ERR_LAUNCH;
+}
+
+}  // namespace tf

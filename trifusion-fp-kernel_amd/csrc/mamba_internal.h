@@ -1,0 +1,24 @@
+// Shared declarations of the fused-recurrence kernels.
+#pragma once
+
+#include "common.h"
+
+namespace tf {
+
+constexpr int kChunk = 64;  // recurrence chunk length (mamba_fused.py:63)
+
+// Valid prefix of batch row b: lengths[b] clamped to [0, T], or T.
+__device__ __forceinline__ int valid_length(const tf_mamba_args& a, int b) {
+  const int T = static_cast<int>(a.time);
+  if (a.lengths == nullptr) return T;
+  const int64_t l = a.lengths[b];
+  return l < 0 ? 0 : (l > T ? T : static_cast<int>(l));
+}
+
+bool generic_supported(const tf_mamba_args& a);
+int launch_generic(const tf_mamba_args& a, hipStream_t stream);
+
+bool mfma_supported(const tf_mamba_args& a);
+int launch_mfma(const tf_mamba_args& a, hipStream_t stream);
+
+}  // namespace tf

@@ -1,0 +1,133 @@
+"""One-pass Mamba-3 SISO inference recurrence on MI355X (gfx950).
+
+Drop-in for the reference's ``fused_mamba`` (``src/trifusion_l4/mamba_fused.py:155-191``):
+same name, positional order and ``warps`` keyword, output allocated like
+``torch.empty_like(v, memory_format=torch.contiguous_format)`` (``:161``), launch
+on the current stream, forward only. Shapes are generalised from the
+reference's fixed N=128, P=64, R=32 (``:159-160``) to N in {16, 32, 64, 128},
+P in {32, 64} and any R <= N/2; other dims raise ``ValueError`` as the reference
+does. Two keyword-only extensions: ``out=`` (write into a caller tensor, e.g. an
+fp32 one) and ``lengths=`` (per-row valid lengths: rows past the length are 0
+and fully padded chunks are skipped).
+"""
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+SUPPORTED_STATE = (16, 32, 64, 128)
+SUPPORTED_HEAD = (32, 64)
+
+
+def _shape_error(message):
+    return ValueError(f"fused_mamba: {message}")
+
+
+def build_args(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths=None, variant="auto"):
+    """Validate the operands and pack them into a ``tf_mamba_args`` struct."""
+    what = "fused_mamba"
+    for name, t in (("q", q), ("k", k), ("v", v), ("z", z), ("angles", angles)):
+        if t.dim() != 4:
+            raise _shape_error(f"{name} must be 4-D, got {tuple(t.shape)}")
+    for name, t in (("adt", adt), ("dt", dt), ("trap", trap)):
+        if t.dim() != 3:
+            raise _shape_error(f"{name} must be [B, H, T], got {tuple(t.shape)}")
+    b, t, h, p = v.shape
+    hq, n = q.shape[2], q.shape[3]
+    r = angles.shape[-1]
+    if n not in SUPPORTED_STATE or p not in SUPPORTED_HEAD or not 0 <= r <= n // 2:
+        raise _shape_error(
+            f"recurrence requires state in {SUPPORTED_STATE}, head in {SUPPORTED_HEAD} and "
+            f"rotary <= state/2 (got state={n}, head={p}, rotary={r})"
+        )
+    if tuple(q.shape) != (b, t, hq, n) or tuple(k.shape) != (b, t, hq, n):
+        raise _shape_error(f"q/k must be [B, T, Hq, N] = {(b, t, hq, n)}")
+    if hq < 1 or h % hq:
+        raise _shape_error(f"heads {h} must be divisible by q/k heads {hq}")
+    if tuple(z.shape) != (b, t, h, p):
+        raise _shape_error("z must match v")
+    for name, ten in (("adt", adt), ("dt", dt), ("trap", trap)):
+        if tuple(ten.shape) != (b, h, t):
+            raise _shape_error(f"{name} must be [B, H, T] = {(b, h, t)}")
+    if tuple(angles.shape[:3]) != (b, t, h):
+        raise _shape_error("angles must be [B, T, H, R]")
+    for name, ten, shape in (("qb", qb, (h, n)), ("kb", kb, (h, n)), ("d", d, (h,))):
+        if tuple(ten.shape) != shape or ten.dtype != torch.float32 or not ten.is_contiguous():
+            raise _shape_error(f"{name} must be a contiguous float32 tensor of shape {shape}")
+    if tuple(out.shape) != (b, t, h, p):
+        raise _shape_error("out must be [B, T, H, P]")
+    if lengths is not None:
+        if tuple(lengths.shape) != (b,) or lengths.dtype != torch.int64 or not lengths.is_contiguous():
+            raise _shape_error("lengths must be a contiguous int64 tensor of shape [B]")
+    _lib.require_cuda(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths, what=what)
+
+    a = _lib.MambaArgs()
+    for name, ten in (
+        ("q", q),
+        ("k", k),
+        ("v", v),
+        ("adt", adt),
+        ("dt", dt),
+        ("trap", trap),
+        ("angles", angles),
+        ("z", z),
+        ("qb", qb),
+        ("kb", kb),
+        ("d", d),
+        ("out", out),
+    ):
+        setattr(a, name, ten.data_ptr())
+    a.lengths = lengths.data_ptr() if lengths is not None else None
+    for name, ten in (
+        ("q", q),
+        ("k", k),
+        ("v", v),
+        ("z", z),
+        ("adt", adt),
+        ("dt", dt),
+        ("trap", trap),
+        ("angles", angles),
+        ("out", out),
+    ):
+        setattr(a, name + "_dtype", _lib.dtype_code(ten, what))
+    for name, ten in (("q", q), ("k", k), ("v", v), ("z", z), ("angles", angles), ("out", out)):
+        getattr(a, name + "_stride")[:] = ten.stride()
+    for name, ten in (("adt", adt), ("dt", dt), ("trap", trap)):
+        getattr(a, name + "_stride")[:] = ten.stride()
+    a.batch, a.time, a.heads, a.qk_heads = b, t, h, hq
+    a.state, a.head_dim, a.rotary = n, p, r
+    try:
+        a.variant = _lib.VARIANTS[variant]
+    except KeyError:
+        raise ValueError(f"fused_mamba: unknown variant {variant!r}") from None
+    return a
+
+
+def fused_mamba(q, k, v, adt, dt, trap, qb, kb, angles, d, z, warps=8, *, out=None, lengths=None, variant="auto"):
+    """Fused Mamba-3 recurrence forward; returns ``out`` ``[B, T, H, P]``.
+
+    ``warps`` is accepted for signature compatibility; gfx950 launch shapes are
+    chosen by the library. ``variant`` selects ``"auto"`` (MFMA chunked scan
+    where supported), ``"mfma"`` or ``"generic"``.
+    """
+    del warps
+    lib = _lib.load()
+    if out is None:
+        out = torch.empty_like(v, memory_format=torch.contiguous_format)
+    args = build_args(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths, variant)
+    _lib.check(lib.tf_fused_mamba(ctypes.byref(args), _lib.stream_of(v)), "fused_mamba")
+    return out
+
+
+def selected_variant(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out=None, lengths=None, variant="auto"):
+    """Name of the kernel ``fused_mamba`` would launch for these operands."""
+    lib = _lib.load()
+    if out is None:
+        out = torch.empty_like(v, memory_format=torch.contiguous_format)
+    args = build_args(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths, variant)
+    code = lib.tf_fused_mamba_variant(ctypes.byref(args))
+    if code < 0:
+        _lib.check(-code, "fused_mamba")
+    return {1: "generic", 2: "mfma"}[code]
