@@ -71,23 +71,31 @@ def step_controls(dt, trap):
 def phase_chunked(angles, dt, pairs, chunk=CHUNK):
     """Rotary phase ``(cumsum_t pi*tanh(theta)*dt) mod 2pi`` with a per-chunk carry.
 
-    Follows ``src/trifusion_l4/angle.py:103-144`` and ``mamba_fused.py:102-111``:
-    inside a chunk the phase is the inclusive cumsum plus the carried state, reduced
-    with ``x - 2pi*floor(x/2pi)``; the carry adds the chunk sum and is reduced the
-    same way. ``angles`` is ``[B,T,H,R]`` (raw, pre-tanh), ``dt`` is ``[B,H,T]``.
-    Returns ``[B,T,H,pairs]`` fp32; pairs ``r >= R`` have phase 0 (no rotation).
+    Follows the structure of ``src/trifusion_l4/angle.py:103-144`` and
+    ``mamba_fused.py:102-111``: inside a chunk the phase is the inclusive cumsum
+    plus the carried state, reduced with ``x - 2pi*floor(x/2pi)``; the carry adds
+    the chunk sum and is reduced the same way. ``angles`` is ``[B,T,H,R]`` (raw,
+    pre-tanh), ``dt`` is ``[B,H,T]``. Returns ``[B,T,H,pairs]`` fp32; pairs
+    ``r >= R`` have phase 0 (no rotation).
+
+    The arithmetic (tanh, products, sums, carry, reduction) is done in float64 and
+    only the final phase is rounded to fp32. An fp32 carry accumulates ~1e-6 rad
+    of rounding noise over long clips; after the bf16 rounding of the rotated
+    q/k that noise alone moves outputs by up to ~6e-4 of max|y|, so the oracle
+    keeps the phase exact to fp32 resolution and so do the HIP kernels.
     """
     b, t, h, r = angles.shape
-    vals = (torch.tanh(angles.float()) * math.pi) * dt.float().transpose(1, 2)[..., None]
+    vals = (torch.tanh(angles.double()) * math.pi) * dt.double().transpose(1, 2)[..., None]
     out = torch.empty_like(vals)
     state = vals.new_zeros(b, h, r)
+    two_pi = 2 * math.pi
     for c0 in range(0, t, chunk):
         blk = vals[:, c0 : c0 + chunk]
         ph = torch.cumsum(blk, 1) + state[:, None]
-        out[:, c0 : c0 + chunk] = ph - TWO_PI * torch.floor(ph / TWO_PI)
+        out[:, c0 : c0 + chunk] = ph - two_pi * torch.floor(ph / two_pi)
         state = state + blk.sum(1)
-        state = state - TWO_PI * torch.floor(state / TWO_PI)
-    return F.pad(out, (0, pairs - r))
+        state = state - two_pi * torch.floor(state / two_pi)
+    return F.pad(out.float(), (0, pairs - r))
 
 
 def rotate_pairs(x, cos, sin):

@@ -65,6 +65,13 @@ __device__ __forceinline__ float mod_two_pi(float x) {
   return x - kTwoPi * floorf(x / kTwoPi);
 }
 
+constexpr double kPiD = 3.141592653589793;
+constexpr double kTwoPiD = 6.283185307179586;
+
+__device__ __forceinline__ double mod_two_pi_d(double x) {
+  return x - kTwoPiD * floor(x / kTwoPiD);
+}
+
 // Wave64 sum via xor shuffles (every lane receives the total).
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

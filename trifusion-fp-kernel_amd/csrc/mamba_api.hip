@@ -8,11 +8,10 @@
 namespace tf {
 namespace {
 
+bool empty(const tf_mamba_args* a) { return a->batch == 0 || a->time == 0; }
+
 int validate(const tf_mamba_args* a) {
   if (a == nullptr) return TF_ERR_NULL;
-  if (!a->q || !a->k || !a->v || !a->adt || !a->dt || !a->trap || !a->angles || !a->z || !a->qb ||
-      !a->kb || !a->d || !a->out)
-    return TF_ERR_NULL;
   const int dts[] = {a->q_dtype,    a->k_dtype,     a->v_dtype,     a->z_dtype,     a->adt_dtype,
                      a->dt_dtype,   a->trap_dtype,  a->angles_dtype, a->out_dtype};
   for (int d : dts)
@@ -23,6 +22,10 @@ int validate(const tf_mamba_args* a) {
   if (a->rotary < 0 || a->rotary > a->state / 2) return TF_ERR_SHAPE;
   if (a->batch > 65535 || a->heads > 65535 || a->time > (int64_t(1) << 30)) return TF_ERR_SHAPE;
   if (a->variant < TF_MAMBA_AUTO || a->variant > TF_MAMBA_MFMA) return TF_ERR_VARIANT;
+  // empty tensors may carry NULL data pointers
+  if (!empty(a) && (!a->q || !a->k || !a->v || !a->adt || !a->dt || !a->trap || !a->angles ||
+                    !a->z || !a->qb || !a->kb || !a->d || !a->out))
+    return TF_ERR_NULL;
   return TF_OK;
 }
 
@@ -44,7 +47,7 @@ extern "C" int tf_fused_mamba_variant(const tf_mamba_args* a) { return tf::selec
 extern "C" int tf_fused_mamba(const tf_mamba_args* a, void* stream) {
   const int which = tf::select(a);
   if (which < 0) return -which;
-  if (a->batch == 0 || a->time == 0) return TF_OK;
+  if (tf::empty(a)) return TF_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
   return which == TF_MAMBA_MFMA ? tf::launch_mfma(*a, s) : tf::launch_generic(*a, s);
 }

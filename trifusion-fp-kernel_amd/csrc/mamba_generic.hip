@@ -58,7 +58,7 @@ __global__ __launch_bounds__(kThreads) void mamba_generic_kernel(const tf_mamba_
 #pragma unroll
   for (int j = 0; j < kStatePerThread; ++j) state[j] = 0.f;
   for (int e = tid; e < kPMax * (kNMax + 1); e += kThreads) (&sh.sr[0][0])[e] = 0.f;
-  float carry = 0.f;  // phase carry of pair `tid` (tid < N/2)
+  double carry = 0.0;  // phase carry of pair `tid` (tid < N/2), kept in fp64
   const float skip = a.d[h];
   const int nchunks = (L + kChunk - 1) / kChunk;
 
@@ -103,10 +103,12 @@ __global__ __launch_bounds__(kThreads) void mamba_generic_kernel(const tf_mamba_
       sh.qk[tid] = s * sh.gamma[tid];
     }
     __syncthreads();
-    // phase scan + rotary + scale + rounding, one thread per pair (mamba_fused.py:102-135)
+    // phase scan + rotary + scale + rounding, one thread per pair (mamba_fused.py:102-135).
+    // The phase is accumulated in fp64 and rounded to fp32 once, so it carries no
+    // fp32 summation noise into the bf16 rounding of qr/kr.
     if (tid < n_state / 2) {
       const int i = tid;
-      float cum = 0.f;
+      double cum = 0.0;
       for (int r = 0; r < kChunk; ++r) {
         const int t = t0 + r;
         const bool valid = t < L;
@@ -115,8 +117,8 @@ __global__ __launch_bounds__(kThreads) void mamba_generic_kernel(const tf_mamba_
           const float th =
               valid ? load_f32(a.angles, a.angles_dtype, go + t * a.angles_stride[1] + i * a.angles_stride[3])
                     : 0.f;
-          cum += (tanhf(th) * kPi) * sh.dt[r];
-          const float ph = mod_two_pi(cum + carry);
+          cum += tanh(static_cast<double>(th)) * kPiD * static_cast<double>(sh.dt[r]);
+          const float ph = static_cast<float>(mod_two_pi_d(cum + carry));
           co = cosf(ph);
           si = sinf(ph);
         }
@@ -128,7 +130,7 @@ __global__ __launch_bounds__(kThreads) void mamba_generic_kernel(const tf_mamba_
         sh.kr[r][2 * i] = valid ? round_to((k0 * co - k1 * si) * s, a.k_dtype) : 0.f;
         sh.kr[r][2 * i + 1] = valid ? round_to((k0 * si + k1 * co) * s, a.k_dtype) : 0.f;
       }
-      if (i < rot) carry = mod_two_pi(carry + cum);
+      if (i < rot) carry = mod_two_pi_d(carry + cum);
     }
     __syncthreads();
     // strictly causal decayed scores, rounded to v's dtype (mamba_fused.py:144-146)

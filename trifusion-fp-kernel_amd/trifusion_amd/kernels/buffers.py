@@ -22,7 +22,7 @@ def mask_buffer(x, mask):
         raise ValueError("mask_buffer: mask must be bool with one entry per row")
     mask = mask.contiguous()
     status = lib.tf_mask_rows(
-        x.data_ptr(), _lib.dtype_code(x, "mask_buffer"), y.data_ptr(), mask.data_ptr(), rows, d, _lib.stream_of(x)
+        x.data_ptr(), y.data_ptr(), _lib.dtype_code(x, "mask_buffer"), mask.data_ptr(), rows, d, _lib.stream_of(x)
     )
     _lib.check(status, "mask_buffer")
     return y
