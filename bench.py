@@ -1,0 +1,244 @@
+"""Benchmark of the fused Mamba-3 inference hot path on one MI355X.
+
+Default workload: ``fused_mamba`` at the 4 s clip shape B=16, L=400, H=16, P=64,
+N=64 (R=16, Hq=1; bf16 x/B/C/z, fp32 dt/adt/trap/angles), synthetic seeded
+inputs resident in HBM. A step is one call over the batch; the timed region
+replays a HIP graph holding ``--steps`` back-to-back calls so host dispatch does
+not stall the GPU between calls, bracketed by device synchronisation and timed
+with HIP events on the launch stream.
+
+Printed as one JSON line: ``value`` is the algorithmic GB/s (unique input bytes +
+output bytes per call / average call time), ``roofline`` compares it with the
+8 TB/s HBM peak, ``cpu_baseline`` times the CPU oracle (chunked fp32 PyTorch) on
+the same workload on the host cores, and ``encoder`` reports the ms per forward
+of the 8-block encoder at 4 s mono x 16 with graph replay (``--no-encoder`` to
+skip).
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "trifusion-fp-kernel_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+HBM_PEAK_GBS = 8000.0
+WORKLOAD = dict(batch=16, time=400, heads=16, head_dim=64, state=64, rotary=16, qk_heads=1)
+METRIC = "fused_mamba GB/s & %HBM peak; ms/forward 4s mono×16 encoder, 1 MI355X"
+TRAFFIC_FILE = ROOT / "profiles" / "fused_mamba_clip_b16_l400_pmc.txt"
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline time budget")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-encoder", action="store_true")
+    p.add_argument("--variant", default="auto", choices=["auto", "mfma", "generic"])
+    p.add_argument("--eager", action="store_true", help="time Python-dispatched calls instead of graph replay")
+    p.add_argument(
+        "--calibrate-copy",
+        type=int,
+        default=0,
+        metavar="MIB",
+        help="only run 20 device-to-device copies of MIB MiB (HBM counter calibration) and exit",
+    )
+    return p.parse_args()
+
+
+def calibrate_copy(torch, mib):
+    """Plain copy of known size: reads and writes exactly mib MiB per copy."""
+    n = mib * (1 << 20) // 4
+    src = torch.randn(n, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(20):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calibration_copy_bytes": n * 4, "copies": 20}), flush=True)
+
+
+def traffic_bytes():
+    """HBM bytes per call from the committed rocprofv3 --pmc summary, if any."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_call:"):
+            return int(line.split(":", 1)[1].strip())
+    return None
+
+
+def time_fused_mamba(args, torch, fused_mamba, dargs, steps, warmup, variant, eager):
+    stream = torch.cuda.current_stream()
+    with torch.inference_mode():
+        out = torch.empty_like(dargs[2])
+        for _ in range(warmup):
+            fused_mamba(*dargs, out=out, variant=variant)
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        if eager:
+            torch.cuda.synchronize()
+            start.record(stream)
+            for _ in range(steps):
+                fused_mamba(*dargs, out=out, variant=variant)
+            end.record(stream)
+            torch.cuda.synchronize()
+            return start.elapsed_time(end) / steps
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(graph, stream=side):
+                for _ in range(steps):
+                    fused_mamba(*dargs, out=out, variant=variant)
+        stream.wait_stream(side)
+        graph.replay()  # warm replay
+        torch.cuda.synchronize()
+        start.record(stream)
+        graph.replay()
+        end.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / steps
+
+
+def cpu_baseline(torch, budget_s):
+    from oracle.recurrence import fused_mamba_chunked
+    from trifusion_amd.synthetic import algorithmic_bytes, clip_inputs
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    args = clip_inputs(WORKLOAD["batch"], WORKLOAD["time"], heads=WORKLOAD["heads"], head_dim=WORKLOAD["head_dim"],
+                       state=WORKLOAD["state"], rotary=WORKLOAD["rotary"], seed=1)
+    nbytes = algorithmic_bytes(args)
+    fused_mamba_chunked(*args)  # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        fused_mamba_chunked(*args)
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    med = times[len(times) // 2]
+    model = ""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {
+        "value": round(nbytes / med / 1e9, 4),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"full clip workload B16 L400 H16 P64 N64, CPU oracle (chunked fp32 PyTorch), "
+        f"median of {len(times)} calls ({med * 1e3:.1f} ms/call), {model}",
+    }
+
+
+def encoder_ms(torch):
+    from trifusion_amd.runtime import InferenceEngine
+    from trifusion_amd.model import Encoder, ModelConfig
+    from trifusion_amd.runtime import prepare_static_weights
+
+    torch.manual_seed(0)
+    model = Encoder(ModelConfig()).eval().requires_grad_(False)
+    prepare_static_weights(model)
+    model = model.cuda()
+    g = torch.Generator().manual_seed(551)
+    audio = (torch.randint(-32768, 32768, (16, 1, 64000), generator=g).float() / 32768).cuda()
+    lengths = torch.full((16,), 64000, dtype=torch.int64, device="cuda")
+    channels = torch.ones(16, dtype=torch.int64, device="cuda")
+    engine = InferenceEngine(model, graphs=True, max_graphs=1)
+    engine(audio, lengths, channels)
+    for _ in range(3):
+        engine(audio, lengths, channels)
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(11):
+        t0 = time.perf_counter()
+        engine(audio, lengths, channels)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return {"ms_per_forward": round(times[len(times) // 2] * 1e3, 4), "graph_hits": engine.graph_hits,
+            "protocol": "3 warm-ups, median of 11, perf_counter + synchronize, graph replay"}
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(
+            f"bench.py runs on one GPU only: --gpus {args.gpus} is not supported "
+            "(the fused recurrence shards over (batch, head) units without collectives; see DESIGN.md)",
+            file=sys.stderr,
+        )
+        sys.exit(2)
+    import torch
+
+    from trifusion_amd.mamba_fused import fused_mamba, selected_variant
+    from trifusion_amd.synthetic import algorithmic_bytes, clip_inputs
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        sys.exit(1)
+    if args.calibrate_copy:
+        calibrate_copy(torch, args.calibrate_copy)
+        return
+    w = WORKLOAD
+    host = clip_inputs(w["batch"], w["time"], heads=w["heads"], head_dim=w["head_dim"], state=w["state"],
+                       rotary=w["rotary"], qk_heads=w["qk_heads"], seed=1)
+    dargs = tuple(x.cuda() for x in host)
+    nbytes = algorithmic_bytes(host)
+    kernel = selected_variant(*dargs, variant=args.variant)
+    ms = time_fused_mamba(args, torch, fused_mamba, dargs, args.steps, args.warmup, args.variant, args.eager)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    line = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded clip_inputs: x,B,C,z ~ N(0,1); dt = softplus(N(0,1)-2); A = -exp(U(0, ln16)))",
+        "config": {
+            "workload": "fused_mamba clip B16 L400 H16 P64 N64 R16 Hq1",
+            "kernel": kernel,
+            "timing": "eager calls" if args.eager else f"HIP graph of {args.steps} calls, HIP events on the launch stream",
+            "algorithmic_bytes_per_call": nbytes,
+            **w,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gbs, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "traffic": traffic_bytes(),
+        },
+    }
+    if not args.no_encoder:
+        try:
+            line["encoder"] = encoder_ms(torch)
+        except ImportError as err:  # encoder not built yet
+            line["encoder"] = {"error": str(err)}
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(torch, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

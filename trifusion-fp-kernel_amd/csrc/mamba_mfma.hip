@@ -60,8 +60,12 @@ __device__ __forceinline__ int kidx(int s, int hh, int j) {
   return 32 * (s >> 1) + 16 * (s & 1) + 8 * (j >> 2) + 4 * hh + (j & 3);
 }
 
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+
+// Two fp32 -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+  const bf16x2 v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+  return __builtin_bit_cast(uint32_t, v);
 }
 __device__ __forceinline__ float lo_f(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float hi_f(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
@@ -123,60 +127,75 @@ __device__ __forceinline__ u32x4 load_row8(const uint16_t* row, int k0) {
   return r;
 }
 
-// Raw angles of rows [t0, t0+64) -> phs[row*rs + pair] as fp32 (0 past L). One
-// wave-uniform dtype branch around coalesced loops.
-__device__ __forceinline__ void stage_angles(const tf_mamba_args& a, int64_t go, int t0, int L, int rs, float* phs) {
-  const int R = static_cast<int>(a.rotary);
-  const int lane = threadIdx.x & 63;
-  const int total = kChunk * R;
-  const int64_t st = a.angles_stride[1], sc = a.angles_stride[3];
-  if (a.angles_dtype == TF_BFLOAT16) {
-    const uint16_t* p = static_cast<const uint16_t*>(a.angles) + go;
-    for (int i = lane; i < total; i += 64) {
-      const int row = i / R, pr = i - row * R;
-      const int t = t0 + row;
-      phs[row * rs + pr] = t < L ? bf16_to_f32(p[t * st + pr * sc]) : 0.f;
-    }
-  } else if (a.angles_dtype == TF_FLOAT32) {
-    const float* p = static_cast<const float*>(a.angles) + go;
-    for (int i = lane; i < total; i += 64) {
-      const int row = i / R, pr = i - row * R;
-      const int t = t0 + row;
-      phs[row * rs + pr] = t < L ? p[t * st + pr * sc] : 0.f;
-    }
-  } else {
-    const _Float16* p = static_cast<const _Float16*>(a.angles) + go;
-    for (int i = lane; i < total; i += 64) {
-      const int row = i / R, pr = i - row * R;
-      const int t = t0 + row;
-      phs[row * rs + pr] = t < L ? static_cast<float>(p[t * st + pr * sc]) : 0.f;
-    }
+// tanh for |x| < 0.625 by the odd polynomial of the Cephes single-precision
+// tanhf (S. L. Moshier, Cephes Math Library), else 1 - 2/(exp(2|x|) + 1) with
+// the hardware exp2/rcp; a few ulp, no branches.
+__device__ __forceinline__ float tanh_fast(float x) {
+  const float ax = fabsf(x);
+  const float z = x * x;
+  const float poly =
+      ((((-5.70498872745e-3f * z + 2.06390887954e-2f) * z - 5.37397155531e-2f) * z + 1.33314422036e-1f) * z -
+       3.33332819422e-1f) * z * ax + ax;
+  const float e = __builtin_amdgcn_exp2f(2.f * kLog2e * fminf(ax, 40.f));
+  const float big = 1.f - 2.f * __builtin_amdgcn_rcpf(e + 1.f);
+  return copysignf(ax < 0.625f ? poly : big, x);
+}
+
+// Raw angles of rows [seg*rp, seg*rp + rp) of pair pp, all loads issued before
+// use (0 past L or for pp >= R).
+template <int RPMAX, typename E>
+__device__ __forceinline__ void load_angles(const E* p, int64_t st, int t0, int L, int seg, int rp, bool on,
+                                            float (&th)[RPMAX]) {
+#pragma unroll
+  for (int r = 0; r < RPMAX; ++r) {
+    const int t = t0 + seg * rp + r;
+    th[r] = (on && r < rp && t < L) ? to_f32(p[t * st]) : 0.f;
   }
 }
 
-// Sum over rows [seg*rp, seg*rp + rp) of pi*tanh(theta)*dt for pair pp (fp64).
-__device__ __forceinline__ double segment_phase_sum(int pp, int seg, int rp, int R, int rs, const float* dtw,
-                                                   const float* phs) {
+// Pass 1: increments pi*tanh(theta)*dt of the lane's rows -> phs[row*rs + pp]
+// (fp32); returns their fp64 sum.
+template <int RPMAX>
+__device__ __forceinline__ double phase_pass1(const tf_mamba_args& a, int64_t go, int t0, int L, int pp, int seg,
+                                              int rp, int R, int rs, const float* dtw, float* phs) {
+  float th[RPMAX];
+  const bool on = pp < R;
+  const int64_t st = a.angles_stride[1];
+  const int64_t off = go + pp * a.angles_stride[3];
+  if (a.angles_dtype == TF_FLOAT32)
+    load_angles<RPMAX>(static_cast<const float*>(a.angles) + off, st, t0, L, seg, rp, on, th);
+  else if (a.angles_dtype == TF_BFLOAT16)
+    load_angles<RPMAX>(static_cast<const bf16_t*>(a.angles) + off, st, t0, L, seg, rp, on, th);
+  else
+    load_angles<RPMAX>(static_cast<const f16_t*>(a.angles) + off, st, t0, L, seg, rp, on, th);
   double sum = 0.0;
-  if (pp >= R) return sum;
-  for (int r = 0; r < rp; ++r) {
-    const int row = seg * rp + r;
-    sum += static_cast<double>(tanhf(phs[row * rs + pp])) * kPiD * static_cast<double>(dtw[row]);
+#pragma unroll
+  for (int r = 0; r < RPMAX; ++r) {
+    if (r < rp) {
+      const int row = seg * rp + r;
+      const float om = tanh_fast(th[r]) * kPi * dtw[row];
+      if (on) phs[row * rs + pp] = om;
+      sum += static_cast<double>(om);
+    }
   }
   return sum;
 }
 
-// Serial fp64 cumsum from `start` over the lane's rows, replacing the staged
-// raw angle with (phase mod 2pi) as fp32.
-__device__ __forceinline__ void segment_phase_write(int pp, int seg, int rp, int R, int rs, const float* dtw,
-                                                    double start, float* phs) {
+// Pass 2: fp64 cumsum of the increments from `start`, replacing each with its
+// phase reduced to [0, 2pi) as fp32.
+template <int RPMAX>
+__device__ __forceinline__ void phase_pass2(int pp, int seg, int rp, int R, int rs, double start, float* phs) {
   if (pp >= R) return;
+  float om[RPMAX];
+#pragma unroll
+  for (int r = 0; r < RPMAX; ++r) om[r] = r < rp ? phs[(seg * rp + r) * rs + pp] : 0.f;
   double cum = start;
-  for (int r = 0; r < rp; ++r) {
-    const int row = seg * rp + r;
-    float* cell = phs + row * rs + pp;
-    cum += static_cast<double>(tanhf(*cell)) * kPiD * static_cast<double>(dtw[row]);
-    *cell = static_cast<float>(mod_two_pi_d(cum));
+#pragma unroll
+  for (int r = 0; r < RPMAX; ++r) {
+    if (r < rp) {
+      cum += static_cast<double>(om[r]);
+      phs[(seg * rp + r) * rs + pp] = static_cast<float>(cum - kTwoPiD * floor(cum * (1.0 / kTwoPiD)));
+    }
   }
 }
 
@@ -307,12 +326,11 @@ __global__ __launch_bounds__(W * 64) void mamba_mfma_kernel(const tf_mamba_args 
       }
       const float chunk_tot = half_last(cs1);  // shuffle with every lane active
       if (lane == 0) sh.tot[w] = chunk_tot;
-      stage_angles(a, go, t0, L, rs, phs);
       wave_sync();
     }
     // rotary phase increments pi*tanh(theta)*dt: lane (pair pp, segment seg) sums
     // rows [seg*rp, seg*rp + rp) in fp64; the chunk sum per pair goes to LDS
-    const double seg_part = segment_phase_sum(pp, seg, rp, R, rs, sh.dt[w], phs);
+    const double seg_part = phase_pass1<16 * NT>(a, go, t0, L, pp, seg, rp, R, rs, sh.dt[w], phs);
     {
       double sum = seg_part;
       for (int off = rp; off < 64; off <<= 1) sum += __shfl_xor(sum, off);
@@ -322,20 +340,9 @@ __global__ __launch_bounds__(W * 64) void mamba_mfma_kernel(const tf_mamba_args 
 
     f32x16 yacc[PT][2];  // y^T tiles (pt, tt): lane = t, elements = p
     {
-      float delta[2];
-      // skip term: gamma * (q + qb).(k + kb), unrotated (mamba_fused.py:124)
-#pragma unroll
-      for (int rt = 0; rt < 2; ++rt) {
-        float part = 0.f;
-#pragma unroll
-        for (int s = 0; s < KS; ++s)
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const int n = kidx(s, hh, j);
-            part += (slot_f(qrow[rt][s], j) + sh.qb[n]) * (slot_f(krow[rt][s], j) + sh.kb[n]);
-          }
-        delta[rt] = gam[rt] * (part + __shfl_xor(part, 32));
-      }
+      // skip-term partial sums gamma * (q + qb).(k + kb) over this lane's n, from
+      // the unrotated biased values inside the rotation loop (mamba_fused.py:124)
+      float part[2] = {0.f, 0.f};
       // rotary phase: carry of the preceding chunks + exclusive segment prefix +
       // serial fp64 cumsum, reduced mod 2pi and staged as fp32 [row][pair] in this
       // wave's state slot (free until dS is written)
@@ -343,14 +350,14 @@ __global__ __launch_bounds__(W * 64) void mamba_mfma_kernel(const tf_mamba_args 
         double carry = 0.0;
         if (pp < R) {
           carry = sh.carry[pp];
-          for (int j = 0; j < w; ++j) carry = mod_two_pi_d(carry + sh.wsum[j][pp]);
+          for (int j = 0; j < w; ++j) carry += sh.wsum[j][pp];
         }
         double pre = seg_part;  // inclusive scan over segments of the same pair
         for (int off = rp; off < 64; off <<= 1) {
           const double o = __shfl_up(pre, off);
           if (seg * rp >= off) pre += o;
         }
-        segment_phase_write(pp, seg, rp, R, rs, sh.dt[w], carry + pre - seg_part, phs);
+        phase_pass2<16 * NT>(pp, seg, rp, R, rs, carry + pre - seg_part, phs);
       }
       wave_sync();
 #pragma unroll
@@ -393,6 +400,7 @@ __global__ __launch_bounds__(W * 64) void mamba_mfma_kernel(const tf_mamba_args 
             const uint32_t kw = krow[rt][s][q4];
             const float q0 = lo_f(qw) + qb0, q1 = hi_f(qw) + qb1;
             const float k0 = lo_f(kw) + kb0, k1 = hi_f(kw) + kb1;
+            part[rt] += q0 * k0 + q1 * k1;
             const float c = co[rt][q4], sn = si[rt][q4], sc = scl[rt];
             const uint32_t qn = pack2(q0 * c - q1 * sn, q0 * sn + q1 * c);
             const uint32_t kn = pack2((k0 * c - k1 * sn) * sc, (k0 * sn + k1 * c) * sc);
@@ -401,6 +409,10 @@ __global__ __launch_bounds__(W * 64) void mamba_mfma_kernel(const tf_mamba_args 
           }
         }
       }
+
+      float delta[2];
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) delta[rt] = gam[rt] * (part[rt] + __shfl_xor(part[rt], 32));
 
       // scores^T[u][t] = kr_u . qr_t on tiles (ut, tt) with ut <= tt, then the
       // strictly causal decay mask, rounded to bf16 (mamba_fused.py:144-146)
@@ -545,8 +557,8 @@ __global__ __launch_bounds__(W * 64) void mamba_mfma_kernel(const tf_mamba_args 
       }
       if (threadIdx.x < R) {
         double cr = sh.carry[threadIdx.x];
-        for (int j = 0; j < nact; ++j) cr = mod_two_pi_d(cr + sh.wsum[j][threadIdx.x]);
-        sh.carry[threadIdx.x] = cr;
+        for (int j = 0; j < nact; ++j) cr += sh.wsum[j][threadIdx.x];
+        sh.carry[threadIdx.x] = cr - kTwoPiD * floor(cr * (1.0 / kTwoPiD));
       }
     }
     __syncthreads();  // barrier 3: exclusive states in LDS
