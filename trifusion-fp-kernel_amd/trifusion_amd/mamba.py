@@ -1,0 +1,85 @@
+"""Frozen Mamba-3 SISO block on the MI355X kernels.
+
+Mirrors ``Mamba3Inference`` of the reference (``src/trifusion_l4/mamba.py:14-102``):
+the same parameter names and in-projection layout ``z, x, B, C, dt, a, trap,
+angles`` (``:26-30,43-55``), B/C RMSNorm over the state dim with one B/C head
+(``:21,56-57``), the discretisation controls (``:58-65``), rotary angles shared by
+all heads as a stride-0 view (``:66``) and the fused recurrence called on
+strided column slices of the projection, no copies (``:70-82``). The controls,
+norms and recurrence are gfx950 HIP kernels; the two projections are torch
+GEMMs (hipBLASLt).
+"""
+
+import torch
+from torch import nn
+
+from .kernels import RMSNorm
+from .kernels.buffers import mamba_controls
+from .mamba_fused import fused_mamba
+
+
+class Mamba3Inference(nn.Module):
+    def __init__(self, config):
+        super().__init__()
+        self.d_inner = config.dim * 2
+        self.headdim = config.head_dim
+        self.nheads = self.d_inner // self.headdim
+        self.d_state = config.state_dim
+        self.num_bc_heads = 1
+        self.num_rope_angles = self.d_state // 4
+        self.A_floor = 1e-4
+        self.chunk_size = 64
+        self.in_proj = nn.Linear(
+            config.dim,
+            2 * self.d_inner + 2 * self.d_state + 3 * self.nheads + self.num_rope_angles,
+            bias=False,
+        )
+        self.out_proj = nn.Linear(self.d_inner, config.dim, bias=False)
+        self.dt_bias = nn.Parameter(torch.full((self.nheads,), -4.0))
+        self.B_bias = nn.Parameter(torch.ones(self.nheads, 1, self.d_state))
+        self.C_bias = nn.Parameter(torch.ones_like(self.B_bias))
+        self.D = nn.Parameter(torch.ones(self.nheads))
+        self.B_norm = RMSNorm(self.d_state)
+        self.C_norm = RMSNorm(self.d_state)
+        # "mfma" (chunked MFMA scan), "generic" (fp32-FMA kernel) or "auto"
+        self.variant = "auto"
+
+    def split(self, p):
+        return p.split(
+            [
+                self.d_inner,
+                self.d_inner,
+                self.d_state,
+                self.d_state,
+                self.nheads,
+                self.nheads,
+                self.nheads,
+                self.num_rope_angles,
+            ],
+            -1,
+        )
+
+    def forward(self, u, lengths=None):
+        b, t, _ = u.shape
+        p = self.in_proj(u)
+        z, v, k, q, ddt, a, trap, angles = self.split(p)
+        q = self.C_norm(q.reshape(b, t, 1, self.d_state))
+        k = self.B_norm(k.reshape(b, t, 1, self.d_state))
+        adt, dt = mamba_controls(a, ddt, self.dt_bias, self.A_floor)
+        angles = angles.unsqueeze(2).expand(b, t, self.nheads, self.num_rope_angles)
+        y = fused_mamba(
+            q,
+            k,
+            v.reshape(b, t, self.nheads, self.headdim),
+            adt,
+            dt,
+            trap.transpose(1, 2),
+            self.C_bias[:, 0],
+            self.B_bias[:, 0],
+            angles,
+            self.D,
+            z.reshape(b, t, self.nheads, self.headdim),
+            lengths=lengths,
+            variant=self.variant,
+        )
+        return self.out_proj(y.reshape(b, t, self.d_inner))

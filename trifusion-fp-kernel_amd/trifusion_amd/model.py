@@ -1,0 +1,119 @@
+"""Synthetic 8-block audio encoder built from the hot-path primitives.
+
+The benchmark encoder for 4 s mono x 16 clips: a Conv1d stem (kernel 400,
+stride 160, 1 -> 512 channels, padded so a 4 s clip gives 400 frames at a 10 ms
+hop), ``depth`` blocks of
+
+    RMSNorm -> Mamba-3 (in-proj 512 -> 2240, fused recurrence with SiLU(z) gate,
+    out-proj 1024 -> 512) -> masked residual -> RMSNorm -> SwiGLU 512 -> 1365 ->
+    512 -> masked residual
+
+and a masked mean-pool over valid frames followed by a 512 -> 5 linear head.
+``forward(audio, lengths, channels)`` returns ``{"logits": [B, 5]}``, the contract
+``InferenceEngine`` relies on (reference ``src/trifusion_l4/runtime.py:82``,
+``src/trifusion_l4/model.py:259-260``). The residual stream is fp32; each residual
+add is fused with the RMSNorm that follows it (reference ``native.add`` +
+``_norm``, ``src/trifusion_l4/kernels/native.py:8-39,81-100``). Rows past a clip's
+length are zero after every residual (``src/trifusion_l4/model.py:143-147,199``).
+"""
+
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from .kernels import RMSNorm, swiglu
+from .kernels.native import add, add_rms, rms
+from .mamba import Mamba3Inference
+from .masking import masked, masked_mean, time_mask
+
+
+@dataclass
+class ModelConfig:
+    dim: int = 512
+    depth: int = 8
+    ffn_dim: int = 1365
+    state_dim: int = 64
+    head_dim: int = 64
+    num_outputs: int = 5
+    stem_kernel: int = 400
+    stem_stride: int = 160
+    stem_padding: int = 120
+    norm_eps: float = 1e-5
+    init_std: float = 0.02
+
+
+class EncoderBlock(nn.Module):
+    def __init__(self, c):
+        super().__init__()
+        self.pre = RMSNorm(c.dim, c.norm_eps)
+        self.mamba = Mamba3Inference(c)
+        self.ff_norm = RMSNorm(c.dim, c.norm_eps)
+        self.gate_up = nn.Linear(c.dim, 2 * c.ffn_dim, bias=False)
+        self.down = nn.Linear(c.ffn_dim, c.dim, bias=False)
+
+    def ffn(self, h):
+        return self.down(swiglu(self.gate_up(h)))
+
+
+class Encoder(nn.Module):
+    def __init__(self, config=None):
+        super().__init__()
+        self.config = c = config or ModelConfig()
+        self.stem = nn.Conv1d(1, c.dim, c.stem_kernel, stride=c.stem_stride, padding=c.stem_padding, bias=False)
+        self.blocks = nn.ModuleList([EncoderBlock(c) for _ in range(c.depth)])
+        self.head = nn.Linear(c.dim, c.num_outputs)
+        self.reset_parameters()
+
+    def reset_parameters(self):
+        for m in self.modules():
+            if isinstance(m, (nn.Linear, nn.Conv1d)):
+                nn.init.normal_(m.weight, std=self.config.init_std)
+                if m.bias is not None:
+                    nn.init.zeros_(m.bias)
+
+    def set_variant(self, variant):
+        """Select the recurrence kernel ("auto", "mfma" or "generic") of every block."""
+        for blk in self.blocks:
+            blk.mamba.variant = variant
+
+    def frames(self, lengths, time):
+        """Valid frames per clip: floor(len / stride) for the padded stem, in [1, time]."""
+        return (lengths // self.config.stem_stride).clamp(1, time)
+
+    def stem_forward(self, audio, channels):
+        """Channel mix then the strided Conv1d stem as one GEMM over framed audio."""
+        b, c, n = audio.shape
+        chan = torch.arange(c, device=audio.device)[None, :] < channels[:, None]
+        mono = (audio * chan[..., None]).sum(1) / channels[:, None].to(audio.dtype)
+        cfg = self.config
+        pad = F.pad(mono, (cfg.stem_padding, cfg.stem_padding))
+        framed = pad.unfold(1, cfg.stem_kernel, cfg.stem_stride)  # [B, T, K] view
+        w = self.stem.weight.reshape(cfg.dim, cfg.stem_kernel)
+        return F.linear(framed.to(w.dtype), w)  # [B, T, dim]
+
+    def encode(self, audio, lengths, channels):
+        x = self.stem_forward(audio, channels)
+        b, t, _ = x.shape
+        frames = self.frames(lengths, t)
+        mask = time_mask(frames, t)
+        x = masked(x.float().contiguous(), mask)
+        blocks = self.blocks
+        h = rms(x, blocks[0].pre.weight, blocks[0].pre.eps, out_dtype=torch.bfloat16)
+        for i, blk in enumerate(blocks):
+            m = blk.mamba(h, frames)
+            x, h = add_rms(x, m, blk.ff_norm.weight, mask, blk.ff_norm.eps)
+            d = blk.ffn(h)
+            if i + 1 < len(blocks):
+                nxt = blocks[i + 1].pre
+                x, h = add_rms(x, d, nxt.weight, mask, nxt.eps)
+            else:
+                x = add(x, d, mask)
+        return x, frames
+
+    def forward(self, audio, lengths, channels):
+        x, frames = self.encode(audio, lengths, channels)
+        pooled = masked_mean(x, frames)
+        logits = self.head(pooled.to(self.head.weight.dtype)).float()
+        return {"logits": logits, "embedding": pooled}
