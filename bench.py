@@ -41,6 +41,7 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline time budget")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-encoder", action="store_true")
+    p.add_argument("--encoder-only", action="store_true", help="only time the encoder forward (profiling aid)")
     p.add_argument("--variant", default="auto", choices=["auto", "mfma", "generic"])
     p.add_argument("--eager", action="store_true", help="time Python-dispatched calls instead of graph replay")
     p.add_argument(
@@ -192,6 +193,9 @@ def main():
         sys.exit(1)
     if args.calibrate_copy:
         calibrate_copy(torch, args.calibrate_copy)
+        return
+    if args.encoder_only:
+        print(json.dumps({"encoder": encoder_ms(torch)}), flush=True)
         return
     w = WORKLOAD
     host = clip_inputs(w["batch"], w["time"], heads=w["heads"], head_dim=w["head_dim"], state=w["state"],
