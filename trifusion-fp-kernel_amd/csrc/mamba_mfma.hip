@@ -3,19 +3,26 @@
 // Same arithmetic and bf16 rounding points as the reference kernel
 // (src/trifusion_l4/mamba_fused.py:72-152), reorganised for CDNA4:
 //
-//   * One workgroup per (batch, head) unit, W waves. The sequence is walked in
-//     "super-chunks" of W chunks of 64 steps; wave w owns chunk g*W + w, so the
-//     chunk-local work of W chunks (loads, controls, phase scan, rotary, the
-//     intra-chunk C.B^T score, score.v and the chunk's state contribution dS)
-//     runs on all SIMDs at once instead of one chunk after another.
+//   * One workgroup per (batch, head) unit. The sequence is walked in
+//     "super-chunks" of CW chunks of 64 steps. Each chunk is split over two
+//     waves, one per 32-step half, so a workgroup runs 2*CW waves (two per SIMD
+//     for CW = 4): every wave works on one 32-row MFMA tile, which keeps its
+//     working set inside the 256 registers a wave gets at two waves per SIMD,
+//     and the second wave on each SIMD hides the first one's memory and
+//     dependency latency.
+//   * Chunk semantics are unchanged: the cumulative decay, the causal score
+//     mask, the state contribution dS and the bf16 rounding of the state all
+//     follow 64-step chunks. The half-1 wave receives the half-0 wave's rotated
+//     k rows and v^T tile through LDS for its off-diagonal score tile and y
+//     term; each half writes its share of dS, and the state scan adds the two.
 //   * The only serial dependency, the fp32 state S <- S*2^tot + dS, is a
-//     prefix scan over the W chunk contributions held in LDS: every thread of
-//     the workgroup owns a slice of the P x N state and walks the W slots,
-//     replacing each dS_c with the exclusive state S_c entering chunk c. Wave w
-//     then adds 2^cs * qr . bf16(S_c)^T to its outputs.
+//     prefix scan over the CW chunk contributions held in LDS: every thread of
+//     the workgroup owns a slice of the P x N state and walks the CW chunks,
+//     replacing each chunk's dS with the exclusive state S_c entering it. Each
+//     wave then adds 2^cs * qr . bf16(S_c)^T to its outputs.
 //   * All contractions run on v_mfma_f32_32x32x16_bf16. Operands come straight
 //     from global memory in MFMA register layout (8-byte loads of four
-//     consecutive elements); the two transposes the contractions over time need
+//     consecutive elements); the transposes the contractions over time need
 //     (v^T and kr^T) are products with an identity tile on the matrix core,
 //     which is exact for bf16 values.
 //   * The rotary phase is accumulated in fp64 and rounded to fp32 once.
@@ -90,7 +97,8 @@ __device__ __forceinline__ F half_last(F v) {
   return __shfl(v, 31, 32);
 }
 
-// Orders this wave's LDS writes before its later LDS reads of other lanes' data.
+// Orders this wave's LDS accesses: earlier writes before later reads of other
+// lanes' data, earlier reads before later writes to the same cells.
 __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -126,6 +134,9 @@ __device__ __forceinline__ u32x4 load_row8(const uint16_t* row, int k0) {
   r[3] = y[1];
   return r;
 }
+
+__device__ __forceinline__ u32x4 as_u4(const float4& f) { return __builtin_bit_cast(u32x4, f); }
+__device__ __forceinline__ float4 as_f4(const u32x4& u) { return __builtin_bit_cast(float4, u); }
 
 // tanh for |x| < 0.625 by the odd polynomial of the Cephes single-precision
 // tanhf (S. L. Moshier, Cephes Math Library), else 1 - 2/(exp(2|x|) + 1) with the
@@ -172,101 +183,67 @@ struct MfmaParams {
   int out_f32, trap_bf16, angles_dtype;
 };
 
-// Global inputs of one wave's chunk, loaded ahead of use (rows c32 and c32+32 of
-// the chunk in MFMA row form; phase lane (pp, seg) raw angles of its rows).
-template <int KS, int PS, int RPMAX>
-struct ChunkInputs {
-  u32x4 q[2][KS], k[2][KS], v[2][PS];
-  float dt[2], dn[2], tr[2], tn[2], adt[2];
-  float th[RPMAX];
-};
-
-template <int RPMAX, typename E>
-__device__ __forceinline__ void load_angles(const E* p, int st, int t0, int L, int seg, int rp, bool on,
-                                            float (&th)[RPMAX]) {
-  const int first = t0 + seg * rp;
-  const E* row = p + first * st;
-#pragma unroll
-  for (int r = 0; r < RPMAX; ++r) {
-    th[r] = (on && r < rp && first + r < L) ? to_f32(*row) : 0.f;
-    row += st;
-  }
-}
-
-template <int KS, int PS, int RPMAX>
-__device__ __forceinline__ void load_chunk(const MfmaParams& P, ChunkInputs<KS, PS, RPMAX>& in, int b, int h, int qh,
-                                           int t0, int L, int c32, int hh, int pp, int seg, int rp) {
-  const float* dtp = P.dt + b * P.d_sb + h * P.d_sh;
-  const float* adtp = P.adt + b * P.a_sb + h * P.a_sh;
-  const int tro = b * P.r_sb + h * P.r_sh;
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
-    const int t = t0 + 32 * rt + c32;
-    const bool valid = t < L;
-    const bool next = t + 1 < P.T;
-    in.dt[rt] = valid ? dtp[t * P.d_st] : 0.f;
-    in.dn[rt] = next ? dtp[(t + 1) * P.d_st] : 0.f;
-    in.adt[rt] = valid ? adtp[t * P.a_st] : 0.f;
-    if (P.trap_bf16) {
-      const bf16_t* tp = static_cast<const bf16_t*>(P.trap) + tro;
-      in.tr[rt] = valid ? to_f32(tp[t * P.r_st]) : 0.f;
-      in.tn[rt] = next ? to_f32(tp[(t + 1) * P.r_st]) : 0.f;
-    } else {
-      const float* tp = static_cast<const float*>(P.trap) + tro;
-      in.tr[rt] = valid ? tp[t * P.r_st] : 0.f;
-      in.tn[rt] = next ? tp[(t + 1) * P.r_st] : 0.f;
-    }
-    // rows past L read row t0 (in bounds) and never reach the outputs or the state
-    const int tl = valid ? t : t0;
-    const uint16_t* q_row = P.q + b * P.q_sb + qh * P.q_sh + tl * P.q_st;
-    const uint16_t* k_row = P.k + b * P.k_sb + qh * P.k_sh + tl * P.k_st;
-    const uint16_t* v_row = P.v + b * P.v_sb + h * P.v_sh + tl * P.v_st;
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      in.q[rt][s] = load_row8(q_row, kidx(s, hh, 0));
-      in.k[rt][s] = load_row8(k_row, kidx(s, hh, 0));
-    }
-#pragma unroll
-    for (int s = 0; s < PS; ++s) in.v[rt][s] = load_row8(v_row, kidx(s, hh, 0));
-  }
-  const bool on = pp < P.R;
-  const int go = b * P.g_sb + h * P.g_sh + (on ? pp : 0) * P.g_sr;
-  if (P.angles_dtype == TF_FLOAT32)
-    load_angles<RPMAX>(static_cast<const float*>(P.angles) + go, P.g_st, t0, L, seg, rp, on, in.th);
-  else
-    load_angles<RPMAX>(static_cast<const bf16_t*>(P.angles) + go, P.g_st, t0, L, seg, rp, on, in.th);
-}
-
-template <int NT, int PT, int W>
+template <int NT, int PT, int CW>
 struct Smem {
-  static constexpr int kTiles = NT * PT;
-  static constexpr int kF4 = kTiles * 4 * 64;  // float4 per chunk state
-  float4 state[W][kF4];  // [slot][tile][g][lane] = D elements 4g..4g+3 of tile (nt, pt)
-  float cs[W][kChunk];   // cumulative log2 decay of each wave's chunk
-  float dt[W][kChunk];   // dt of each wave's chunk rows
-  float wv[W][kChunk];   // 2^(tot - cs): decay from each row to the chunk end
-  float tot[W];
-  double wsum[W][64];    // phase increment of each chunk per rotary pair
-  double carry[64];      // phase carry entering the super-chunk
+  static constexpr int kF4 = NT * PT * 256;  // float4 per chunk state ([tile][g][lane])
+  // Per chunk slot, in the order of use within a super-chunk:
+  //   a: half-0 -> half-1 exchange (kr rows, v^T tile), then half 1's dS, then
+  //      the exclusive state S_c read by the output phase;
+  //   b: rotary phase staging [row][pair], then half 0's dS.
+  float4 a[CW][kF4];
+  float4 b[CW][kF4];
+  float cs[CW][kChunk];  // cumulative log2 decay over the chunk
+  float dt[CW][kChunk];  // dt of the chunk rows
+  float wv[CW][kChunk];  // 2^(tot - cs): decay from each row to the chunk end
+  float htot[2 * CW];    // log2 decay of each half (wave) on its own
+  double wsum[2 * CW][64];  // phase increment of each half per rotary pair
+  double carry[64];         // phase carry entering the super-chunk
   float qb[32 * NT];
   float kb[32 * NT];
 };
 
-template <int NT, int PT, int W>
-__global__ __launch_bounds__(W * 64) void mamba_mfma_kernel(const MfmaParams P) {
+// Scores^T[u][t] = kr_u . qr_t of one 32x32 tile times the decay
+// 2^min(cs_t - cs_u, 0), strictly causal on a diagonal tile, rounded to bf16 as
+// the Y operand of the score . v product (rows t, K = u; mamba_fused.py:144-146).
+__device__ __forceinline__ void score_tile(const f32x16& acc, float cst, const float* csu_base, bool diag, int c32,
+                                           int hh, u32x4 (&out)[2]) {
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const float4 csu = *reinterpret_cast<const float4*>(csu_base + 8 * g + 4 * hh);
+    const float cu[4] = {csu.x, csu.y, csu.z, csu.w};
+    float vals[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int e = 4 * g + q;
+      const float x = acc[e] * fast_exp2(fminf(cst - cu[q], 0.f));
+      vals[q] = (!diag || c32 > drow(e, hh)) ? x : 0.f;
+    }
+    out[g >> 1][2 * (g & 1)] = pack2(vals[0], vals[1]);
+    out[g >> 1][2 * (g & 1) + 1] = pack2(vals[2], vals[3]);
+  }
+}
+
+// WIDE: R in (N/4, N/2], else R <= N/4. The phase lanes of a wave take pair
+// pp = lane % RP over RPL consecutive rows of the wave's half, segment
+// seg = lane / RP (64 / RP segments of RPL rows cover the 32 rows).
+template <int NT, int PT, int CW, bool WIDE>
+__global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P) {
+  constexpr int W = 2 * CW;         // waves: two per chunk
   constexpr int N = 32 * NT;
   constexpr int KS = N / 16;        // k-steps over the state dim
   constexpr int PS = PT * 2;        // k-steps over the head dim
-  constexpr int RPMAX = N / 2;      // rows per phase lane at most (R <= N/2)
-  using Sm = Smem<NT, PT, W>;
+  constexpr int RPL = WIDE ? N / 4 : N / 8;  // phase rows per lane
+  constexpr int RP = 2 * RPL;                // pairs covered by the phase lanes (>= R)
+  using Sm = Smem<NT, PT, CW>;
   constexpr int kF4 = Sm::kF4;
   constexpr int SPT = (kF4 + W * 64 - 1) / (W * 64);  // float4 of the running state per thread
+  static_assert((KS + 2 * PT) * 64 <= kF4, "exchange tile does not fit its slot");
   __shared__ Sm sh;
 
-  const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
-  const int c32 = lane & 31;
-  const int hh = lane >> 5;
+  const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int cw = w % CW;        // chunk slot
+  const int hf = w / CW;        // half: rows 32*hf .. 32*hf + 31 of the chunk
+  const int sub = 2 * cw + hf;  // time order of the wave's rows within the super-chunk
   const int unit = P.xcd_per > 0 ? (blockIdx.x & 7) * P.xcd_per + (blockIdx.x >> 3) : static_cast<int>(blockIdx.x);
   const int b = unit / P.H;
   const int h = unit - b * P.H;
@@ -279,13 +256,19 @@ __global__ __launch_bounds__(W * 64) void mamba_mfma_kernel(const MfmaParams P) 
     L = l < 0 ? 0 : (l > T ? T : static_cast<int>(l));
   }
   const int nvalid = (L + kChunk - 1) / kChunk;
-  // phase lanes: pair pp = lane % rp over rows [seg*rp, seg*rp + rp), rp = pow2 >= R
-  int rp = 1;
-  while (rp < R) rp <<= 1;
-  const int pp = lane & (rp - 1);
-  const int seg = lane / rp;
   const int rs = (R + 1) & ~1;  // row stride of the staged phases (even: 8-byte pair reads)
   const float skip = P.d[h];
+
+  // per-unit bases
+  const uint16_t* qbase = P.q + b * P.q_sb + qh * P.q_sh;
+  const uint16_t* kbase = P.k + b * P.k_sb + qh * P.k_sh;
+  const uint16_t* vbase = P.v + b * P.v_sb + h * P.v_sh;
+  const uint16_t* zbase = P.z + b * P.z_sb + h * P.z_sh;
+  const float* dtb = P.dt + b * P.d_sb + h * P.d_sh;
+  const float* adtb = P.adt + b * P.a_sb + h * P.a_sh;
+  const int trb = b * P.r_sb + h * P.r_sh;
+  const int gbase = b * P.g_sb + h * P.g_sh;
+  const int obase = b * P.o_sb + h * P.o_sh;
 
   for (int i = threadIdx.x; i < 64; i += W * 64) sh.carry[i] = 0.0;
   for (int i = threadIdx.x; i < N; i += W * 64) {
@@ -295,100 +278,136 @@ __global__ __launch_bounds__(W * 64) void mamba_mfma_kernel(const MfmaParams P) 
   float4 run[SPT];
 #pragma unroll
   for (int r = 0; r < SPT; ++r) run[r] = make_float4(0.f, 0.f, 0.f, 0.f);
-  const u32x4 ident0 = identity_rows(0, hh, c32);
-  const u32x4 ident1 = identity_rows(1, hh, c32);
+  const u32x4 ident0 = identity_rows(0, (threadIdx.x >> 5) & 1, threadIdx.x & 31);
+  const u32x4 ident1 = identity_rows(1, (threadIdx.x >> 5) & 1, threadIdx.x & 31);
 
   __syncthreads();
 
-  for (int g0 = 0; g0 < nvalid; g0 += W) {
-    const bool active = g0 + w < nvalid;  // wave-uniform; idle waves recompute the last chunk
-    const int c = active ? g0 + w : nvalid - 1;
-    const int nact = min(W, nvalid - g0);
-    const int t0 = c * kChunk;
-    float* phs = reinterpret_cast<float*>(&sh.state[w][0]);  // [row][pair] staging, free until dS
-    ChunkInputs<KS, PS, RPMAX> cur;
-    load_chunk(P, cur, b, h, qh, t0, L, c32, hh, pp, seg, rp);
+  for (int g0 = 0; g0 < nvalid; g0 += CW) {
+    // Lane-derived indices are rebuilt from an index the compiler cannot see
+    // through each iteration: hoisted out of the loop, the dozens of per-lane
+    // addresses they feed would stay live across it and spill.
+    int tid = static_cast<int>(threadIdx.x);
+    asm volatile("" : "+v"(tid));
+    const int lane = tid & 63;
+    const int c32 = lane & 31;
+    const int hh = lane >> 5;
+    const int pp = lane & (RP - 1);
+    const int seg = lane / RP;
+    const bool pair_on = pp < R;
+    const int nact = min(CW, nvalid - g0);
+    const bool active = cw < nact;  // wave-uniform; idle waves only join the barriers
+    const int t0 = (g0 + cw) * kChunk;
+    const int t = t0 + 32 * hf + c32;  // row of this lane in the row-form tiles
+    float* stg = reinterpret_cast<float*>(&sh.b[cw][0]);  // [64][rs] phase staging
 
-    // ---------------- phase A: chunk-local work ----------------
-    float csr[2], gam[2], scl[2];
-    {
-      float da[2];
-#pragma unroll
-      for (int rt = 0; rt < 2; ++rt) {
-        const float tr = sigmoid_fast(cur.tr[rt]);
-        const float tn = sigmoid_fast(cur.tn[rt]);
-        gam[rt] = cur.dt[rt] * tr;
-        scl[rt] = cur.dn[rt] * (1.f - tn) + gam[rt];
-        da[rt] = cur.adt[rt] * kLog2e;
-      }
-      // cumulative log2 decay over the chunk; both lane halves hold all 64 rows
-      const float cs0 = half_scan(da[0], c32);
-      const float cs1 = half_scan(da[1], c32) + half_last(cs0);
-      const float tot = half_last(cs1);  // shuffle with every lane active
-      csr[0] = cs0;
-      csr[1] = cs1;
-      if (hh == 0) {
-        sh.cs[w][c32] = cs0;
-        sh.cs[w][32 + c32] = cs1;
-        sh.dt[w][c32] = cur.dt[0];
-        sh.dt[w][32 + c32] = cur.dt[1];
-        sh.wv[w][c32] = fast_exp2(tot - cs0);
-        sh.wv[w][32 + c32] = fast_exp2(tot - cs1);
-      }
-      if (lane == 0) sh.tot[w] = tot;
-      wave_sync();
-    }
-    // rotary phase, pass 1: increments pi*tanh(theta)*dt of the lane's rows to the
-    // staging area and their fp64 sum; the chunk sum per pair goes to LDS
+    // Values carried from one "if (active)" region to a later one are given a
+    // definition on the idle path too: left undefined there, the compiler
+    // carries them around the loop and holds their registers through every phase.
+    u32x4 q[KS] = {}, k[KS] = {}, v[PS] = {};
+    float th[RPL] = {};
+    float csr = 0.f, gam = 0.f, scl = 0.f;
     double seg_part = 0.0;
-    if (pp < R) {
-      float* cell = phs + seg * rp * rs + pp;
-      const float* dtr = &sh.dt[w][seg * rp];
+    // ---------------- loads, controls, phase pass 1 ----------------
+    if (active) {
+      const bool valid = t < L;
+      const bool next = t + 1 < T;
+      // rows past L read row t0 (valid) and never reach the outputs or the state
+      const int tl = valid ? t : t0;
+      const uint16_t* q_row = qbase + tl * P.q_st;
+      const uint16_t* k_row = kbase + tl * P.k_st;
+      const uint16_t* v_row = vbase + tl * P.v_st;
 #pragma unroll
-      for (int r = 0; r < RPMAX; ++r) {
-        if (r < rp) {
-          const float om = tanh_fast(cur.th[r]) * kPi * dtr[r];
-          *cell = om;
-          seg_part += static_cast<double>(om);
-        }
-        cell += rs;
+      for (int s = 0; s < KS; ++s) {
+        q[s] = load_row8(q_row, kidx(s, hh, 0));
+        k[s] = load_row8(k_row, kidx(s, hh, 0));
       }
-    }
-    {
-      double sum = seg_part;
-      for (int off = rp; off < 64; off <<= 1) sum += __shfl_xor(sum, off);
-      if (seg == 0 && pp < R) sh.wsum[w][pp] = sum;
-    }
-    __syncthreads();  // barrier 1: chunk phase sums visible
+#pragma unroll
+      for (int s = 0; s < PS; ++s) v[s] = load_row8(v_row, kidx(s, hh, 0));
+      const float dtv = valid ? dtb[t * P.d_st] : 0.f;
+      const float dnv = next ? dtb[(t + 1) * P.d_st] : 0.f;
+      const float adv = valid ? adtb[t * P.a_st] : 0.f;
+      float trv, tnv;
+      if (P.trap_bf16) {
+        const bf16_t* tp = static_cast<const bf16_t*>(P.trap) + trb;
+        trv = valid ? to_f32(tp[t * P.r_st]) : 0.f;
+        tnv = next ? to_f32(tp[(t + 1) * P.r_st]) : 0.f;
+      } else {
+        const float* tp = static_cast<const float*>(P.trap) + trb;
+        trv = valid ? tp[t * P.r_st] : 0.f;
+        tnv = next ? tp[(t + 1) * P.r_st] : 0.f;
+      }
+      // raw angles of the phase lane's rows (clamped to a valid row; their dt is 0)
+      const int first = t0 + 32 * hf + seg * RPL;
+      if (P.angles_dtype == TF_FLOAT32) {
+        const float* ap = static_cast<const float*>(P.angles) + gbase + (pair_on ? pp : 0) * P.g_sr;
+#pragma unroll
+        for (int r = 0; r < RPL; ++r)
+          th[r] = ap[min(first + r, L - 1) * P.g_st];
+      } else {
+        const bf16_t* ap = static_cast<const bf16_t*>(P.angles) + gbase + (pair_on ? pp : 0) * P.g_sr;
+#pragma unroll
+        for (int r = 0; r < RPL; ++r)
+          th[r] = to_f32(ap[min(first + r, L - 1) * P.g_st]);
+      }
 
-    f32x16 yacc[PT][2];  // y^T tiles (pt, tt): lane = t, elements = p
-    u32x4 qrow[2][KS];   // rotated q rows (Y operand over n)
-    {
-      // pass 2: carry of the preceding chunks + exclusive segment prefix + serial
+      // controls (mamba_fused.py:98-110) and the half's cumulative log2 decay
+      gam = dtv * sigmoid_fast(trv);
+      scl = dnv * (1.f - sigmoid_fast(tnv)) + gam;
+      csr = half_scan(adv * kLog2e, c32);
+      const float ltot = half_last(csr);
+      if (hh == 0) {
+        sh.dt[cw][32 * hf + c32] = dtv;
+        if (hf == 0) sh.cs[cw][c32] = csr;  // final for half 0
+      }
+      if (lane == 0) sh.htot[w] = ltot;
+      wave_sync();
+
+      // rotary phase, pass 1: increments pi*tanh(theta)*dt of the lane's rows
+      // (kept in th[]) and their fp64 sum; the half's sum per pair goes to LDS
+      const float* dtr = &sh.dt[cw][32 * hf + seg * RPL];
+#pragma unroll
+      for (int r = 0; r < RPL; ++r) {
+        th[r] = tanh_fast(th[r]) * kPi * dtr[r];
+        seg_part += static_cast<double>(th[r]);
+      }
+      if (!pair_on) seg_part = 0.0;
+      double sum = seg_part;
+      for (int off = RP; off < 64; off <<= 1) sum += __shfl_xor(sum, off);
+      if (seg == 0 && pair_on) sh.wsum[sub][pp] = sum;
+    }
+    __syncthreads();  // barrier 1: half sums of decay and phase visible
+
+    u32x4 qrow[KS] = {};  // rotated q rows (Y operand over n)
+    u32x4 scy_d[2] = {};  // diagonal score tile (Y rows t, K = u of this half)
+    u32x4 ktx[NT][2] = {}, vtx[PT][2] = {}, vsy[PT][2] = {};
+    float csf = 0.f, delta = 0.f;
+    // ---------------- phase pass 2, rotary, own-half products ----------------
+    if (active) {
+      const float tot = sh.htot[CW + cw] + sh.htot[cw];  // chunk total, same sum as half 1's last cs
+      csf = hf ? csr + sh.htot[cw] : csr;
+      if (hh == 0) {
+        if (hf) sh.cs[cw][32 + c32] = csf;
+        sh.wv[cw][32 * hf + c32] = fast_exp2(tot - csf);
+      }
+      // pass 2: carry of the preceding halves + exclusive segment prefix + serial
       // fp64 cumsum, reduced to [0, 2pi) and staged as fp32 [row][pair]
       {
-        double carry = 0.0;
-        if (pp < R) {
-          carry = sh.carry[pp];
-          for (int j = 0; j < w; ++j) carry += sh.wsum[j][pp];
-        }
-        double pre = seg_part;  // inclusive scan over segments of the same pair
-        for (int off = rp; off < 64; off <<= 1) {
+        const int ppc = pair_on ? pp : 0;
+        double carry = sh.carry[ppc];
+        for (int j = 0; j < sub; ++j) carry += sh.wsum[j][ppc];
+        double pre = seg_part;  // inclusive scan over the segments of the same pair
+        for (int off = RP; off < 64; off <<= 1) {
           const double o = __shfl_up(pre, off);
-          if (seg * rp >= off) pre += o;
+          if (lane >= off) pre += o;
         }
-        if (pp < R) {
-          float* base = phs + seg * rp * rs + pp;
-          float om[RPMAX];
+        double cum = carry + pre - seg_part;
+        float* cell = stg + (32 * hf + seg * RPL) * rs + pp;
+        if (pair_on) {
 #pragma unroll
-          for (int r = 0; r < RPMAX; ++r) om[r] = r < rp ? base[r * rs] : 0.f;
-          double cum = carry + pre - seg_part;
-#pragma unroll
-          for (int r = 0; r < RPMAX; ++r) {
-            if (r < rp) {
-              cum += static_cast<double>(om[r]);
-              base[r * rs] = static_cast<float>(cum - kTwoPiD * floor(cum * (1.0 / kTwoPiD)));
-            }
+          for (int r = 0; r < RPL; ++r) {
+            cum += static_cast<double>(th[r]);
+            cell[r * rs] = static_cast<float>(cum - kTwoPiD * floor(cum * (1.0 / kTwoPiD)));
           }
         }
       }
@@ -397,256 +416,236 @@ __global__ __launch_bounds__(W * 64) void mamba_mfma_kernel(const MfmaParams P) 
       // bias + rotary + scale + bf16 rounding of q and k (mamba_fused.py:112-135),
       // with the skip-term partial sums gamma * (q + qb).(k + kb) over this lane's n
       // from the unrotated biased values (mamba_fused.py:124)
-      u32x4 krow[2][KS];
-      float part[2] = {0.f, 0.f};
+      u32x4 krow[KS];
+      float part = 0.f;
+      // zero the compiler cannot see through: keeps the bias reads inside the
+      // loop instead of 4*N registers held across it
+      int bias_off = 0;
+      asm volatile("" : "+v"(bias_off));
+      const float* prow = stg + (32 * hf + c32) * rs;
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        float co[2][4], si[2][4];
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            co[rt][u] = 1.f;
-            si[rt][u] = 0.f;
-          }
+        float co[4] = {1.f, 1.f, 1.f, 1.f}, si[4] = {0.f, 0.f, 0.f, 0.f};
         const bool rot = 8 * s < R;  // wave-uniform: pairs >= R are not rotated
         if (rot) {
 #pragma unroll
-          for (int rt = 0; rt < 2; ++rt) {
-            const float* row = phs + (32 * rt + c32) * rs;
+          for (int half = 0; half < 2; ++half) {
+            const int pr = 8 * s + 2 * hh + 4 * half;
+            const float2 ph = *reinterpret_cast<const float2*>(prow + min(pr, rs - 2));
 #pragma unroll
-            for (int half = 0; half < 2; ++half) {
-              const int pr = 8 * s + 2 * hh + 4 * half;
-              const float2 ph = *reinterpret_cast<const float2*>(row + pr);
-#pragma unroll
-              for (int u = 0; u < 2; ++u) {
-                const float x = u ? ph.y : ph.x;
-                if (pr + u < R) {
-                  co[rt][2 * half + u] = __builtin_amdgcn_cosf(x * kInvTwoPi);
-                  si[rt][2 * half + u] = __builtin_amdgcn_sinf(x * kInvTwoPi);
-                }
+            for (int u = 0; u < 2; ++u) {
+              const float x = u ? ph.y : ph.x;
+              if (pr + u < R) {
+                co[2 * half + u] = __builtin_amdgcn_cosf(x * kInvTwoPi);
+                si[2 * half + u] = __builtin_amdgcn_sinf(x * kInvTwoPi);
               }
             }
           }
         }
+        // biases of the lane's 8 state indices (two 16-byte LDS reads each)
+        const float4 qbl = *reinterpret_cast<const float4*>(&sh.qb[kidx(s, hh, 0) + bias_off]);
+        const float4 qbh = *reinterpret_cast<const float4*>(&sh.qb[kidx(s, hh, 4) + bias_off]);
+        const float4 kbl = *reinterpret_cast<const float4*>(&sh.kb[kidx(s, hh, 0) + bias_off]);
+        const float4 kbh = *reinterpret_cast<const float4*>(&sh.kb[kidx(s, hh, 4) + bias_off]);
+        const float qbs[8] = {qbl.x, qbl.y, qbl.z, qbl.w, qbh.x, qbh.y, qbh.z, qbh.w};
+        const float kbs[8] = {kbl.x, kbl.y, kbl.z, kbl.w, kbh.x, kbh.y, kbh.z, kbh.w};
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {
-          const int j = 2 * q4;
-          const float qb0 = sh.qb[kidx(s, hh, j)], qb1 = sh.qb[kidx(s, hh, j + 1)];
-          const float kb0 = sh.kb[kidx(s, hh, j)], kb1 = sh.kb[kidx(s, hh, j + 1)];
-#pragma unroll
-          for (int rt = 0; rt < 2; ++rt) {
-            const uint32_t qw = cur.q[rt][s][q4];
-            const uint32_t kw = cur.k[rt][s][q4];
-            const float q0 = lo_f(qw) + qb0, q1 = hi_f(qw) + qb1;
-            const float k0 = lo_f(kw) + kb0, k1 = hi_f(kw) + kb1;
-            part[rt] += q0 * k0 + q1 * k1;
-            const float sc = scl[rt];
-            if (rot) {
-              const float c = co[rt][q4], sn = si[rt][q4];
-              qrow[rt][s][q4] = pack2(q0 * c - q1 * sn, q0 * sn + q1 * c);
-              krow[rt][s][q4] = pack2((k0 * c - k1 * sn) * sc, (k0 * sn + k1 * c) * sc);
-            } else {
-              qrow[rt][s][q4] = pack2(q0, q1);
-              krow[rt][s][q4] = pack2(k0 * sc, k1 * sc);
-            }
+          const float qb0 = qbs[2 * q4], qb1 = qbs[2 * q4 + 1];
+          const float kb0 = kbs[2 * q4], kb1 = kbs[2 * q4 + 1];
+          const uint32_t qw = q[s][q4];
+          const uint32_t kw = k[s][q4];
+          const float q0 = lo_f(qw) + qb0, q1 = hi_f(qw) + qb1;
+          const float k0 = lo_f(kw) + kb0, k1 = hi_f(kw) + kb1;
+          part += q0 * k0 + q1 * k1;
+          if (rot) {
+            const float c = co[q4], sn = si[q4];
+            qrow[s][q4] = pack2(q0 * c - q1 * sn, q0 * sn + q1 * c);
+            krow[s][q4] = pack2((k0 * c - k1 * sn) * scl, (k0 * sn + k1 * c) * scl);
+          } else {
+            qrow[s][q4] = pack2(q0, q1);
+            krow[s][q4] = pack2(k0 * scl, k1 * scl);
           }
         }
       }
-      float delta[2];
-#pragma unroll
-      for (int rt = 0; rt < 2; ++rt) delta[rt] = gam[rt] * (part[rt] + __shfl_xor(part[rt], 32));
+      delta = gam * (part + __shfl_xor(part, 32));
 
-      // scores^T[u][t] = kr_u . qr_t on tiles (ut, tt) with ut <= tt, then the
-      // strictly causal decay mask, rounded to bf16 (mamba_fused.py:144-146)
-      u32x4 scy[2][4];  // Y rows t, K = u
+      float4* ex = &sh.a[cw][0];
+      if (hf == 0) {
+#pragma unroll
+        for (int s = 0; s < KS; ++s) ex[s * 64 + lane] = as_f4(krow[s]);
+      }
+      // diagonal score tile of this half
       {
-        f32x16 sacc[3] = {zero16(), zero16(), zero16()};
+        f32x16 sacc = zero16();
 #pragma unroll
-        for (int s = 0; s < KS; ++s) {
-          sacc[0] = mfma(krow[0][s], qrow[0][s], sacc[0]);
-          sacc[1] = mfma(krow[0][s], qrow[1][s], sacc[1]);
-          sacc[2] = mfma(krow[1][s], qrow[1][s], sacc[2]);
-        }
-#pragma unroll
-        for (int tile = 0; tile < 3; ++tile) {
-          const int ut = tile == 2 ? 1 : 0;
-          const int tt = tile == 0 ? 0 : 1;
-          const float cst = csr[tt];
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const float4 csu = *reinterpret_cast<const float4*>(&sh.cs[w][32 * ut + 8 * g + 4 * hh]);
-            const float cu[4] = {csu.x, csu.y, csu.z, csu.w};
-            float vals[4];
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const int e = 4 * g + q;
-              const float x = sacc[tile][e] * fast_exp2(fminf(cst - cu[q], 0.f));
-              // the off-diagonal tile (u < 32 <= t) is entirely below the diagonal
-              vals[q] = (tile == 1 || c32 > drow(e, hh)) ? x : 0.f;
-            }
-            scy[tt][2 * ut + (g >> 1)][2 * (g & 1)] = pack2(vals[0], vals[1]);
-            scy[tt][2 * ut + (g >> 1)][2 * (g & 1) + 1] = pack2(vals[2], vals[3]);
-          }
-        }
+        for (int s = 0; s < KS; ++s) sacc = mfma(krow[s], qrow[s], sacc);
+        score_tile(sacc, csf, &sh.cs[cw][32 * hf], true, c32, hh, scy_d);
       }
-
       // kr^T via the identity tile: D[u][n] = kr[u][n] -> X rows n, K = u
-      u32x4 ktx[NT][4];
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt)
+      for (int nt = 0; nt < NT; ++nt) {
+        f32x16 d = mfma(krow[2 * nt], ident0, zero16());
+        d = mfma(krow[2 * nt + 1], ident1, d);
 #pragma unroll
-        for (int ut = 0; ut < 2; ++ut) {
-          f32x16 d = mfma(krow[ut][2 * nt], ident0, zero16());
-          d = mfma(krow[ut][2 * nt + 1], ident1, d);
+        for (int sp = 0; sp < 2; ++sp)
 #pragma unroll
-          for (int sp = 0; sp < 2; ++sp)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) ktx[nt][2 * ut + sp][q] = pack2(d[8 * sp + 2 * q], d[8 * sp + 2 * q + 1]);
-        }
-
+          for (int q4 = 0; q4 < 4; ++q4) ktx[nt][sp][q4] = pack2(d[8 * sp + 2 * q4], d[8 * sp + 2 * q4 + 1]);
+      }
       // v^T via the identity tile: D[u][p] = v[u][p] -> X rows p, K = u; and the
       // decay-scaled copy rounded to bf16 (mamba_fused.py:151) -> Y rows p, K = u.
       // Rows past L carry v = 0, so they add nothing to the state.
+      if (t >= L) {
 #pragma unroll
-      for (int rt = 0; rt < 2; ++rt)
-        if (t0 + 32 * rt + c32 >= L)
-#pragma unroll
-          for (int s = 0; s < PS; ++s) cur.v[rt][s] = u32x4{0u, 0u, 0u, 0u};
-      u32x4 vtx[PT][4], vsy[PT][4];
-#pragma unroll
-      for (int ut = 0; ut < 2; ++ut) {
-        float sc16[16];
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const float4 wu = *reinterpret_cast<const float4*>(&sh.wv[w][32 * ut + 8 * g + 4 * hh]);
-          sc16[4 * g] = wu.x;
-          sc16[4 * g + 1] = wu.y;
-          sc16[4 * g + 2] = wu.z;
-          sc16[4 * g + 3] = wu.w;
-        }
-#pragma unroll
-        for (int pt = 0; pt < PT; ++pt) {
-          f32x16 d = mfma(cur.v[ut][2 * pt], ident0, zero16());
-          d = mfma(cur.v[ut][2 * pt + 1], ident1, d);
-#pragma unroll
-          for (int sp = 0; sp < 2; ++sp)
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const int e = 8 * sp + 2 * q;
-              vtx[pt][2 * ut + sp][q] = pack2(d[e], d[e + 1]);
-              vsy[pt][2 * ut + sp][q] = pack2(d[e] * sc16[e], d[e + 1] * sc16[e + 1]);
-            }
-        }
+        for (int s = 0; s < PS; ++s) v[s] = u32x4{0u, 0u, 0u, 0u};
       }
+      float sc16[16];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 wu = *reinterpret_cast<const float4*>(&sh.wv[cw][32 * hf + 8 * g + 4 * hh]);
+        sc16[4 * g] = wu.x;
+        sc16[4 * g + 1] = wu.y;
+        sc16[4 * g + 2] = wu.z;
+        sc16[4 * g + 3] = wu.w;
+      }
+#pragma unroll
+      for (int pt = 0; pt < PT; ++pt) {
+        f32x16 d = mfma(v[2 * pt], ident0, zero16());
+        d = mfma(v[2 * pt + 1], ident1, d);
+#pragma unroll
+        for (int sp = 0; sp < 2; ++sp)
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4) {
+            const int e = 8 * sp + 2 * q4;
+            vtx[pt][sp][q4] = pack2(d[e], d[e + 1]);
+            vsy[pt][sp][q4] = pack2(d[e] * sc16[e], d[e + 1] * sc16[e + 1]);
+          }
+      }
+      if (hf == 0) {
+#pragma unroll
+        for (int pt = 0; pt < PT; ++pt)
+#pragma unroll
+          for (int sp = 0; sp < 2; ++sp) ex[(KS + 2 * pt + sp) * 64 + lane] = as_f4(vtx[pt][sp]);
+      }
+    }
+    __syncthreads();  // barrier 2: exchange tiles visible, phase staging no longer read
 
-      // dS^T[n][p] = sum_u kr^T[n][u] vs[p][u] -> LDS slot w (lane = p, elements = n)
+    f32x16 yacc[PT] = {};  // y^T tiles: lane = t, elements = p
+    if (active) {
+      u32x4 scy_o[2];
+      u32x4 exv[PT][2];
+      const float4* ex = &sh.a[cw][0];
+      if (hf) {
+        // off-diagonal score tile: u in half 0, t in half 1 (entirely causal)
+        f32x16 sacc = zero16();
+#pragma unroll
+        for (int s = 0; s < KS; ++s) sacc = mfma(as_u4(ex[s * 64 + lane]), qrow[s], sacc);
+        score_tile(sacc, csf, &sh.cs[cw][0], false, c32, hh, scy_o);
+#pragma unroll
+        for (int pt = 0; pt < PT; ++pt)
+#pragma unroll
+          for (int sp = 0; sp < 2; ++sp) exv[pt][sp] = as_u4(ex[(KS + 2 * pt + sp) * 64 + lane]);
+        wave_sync();  // exchange reads before this wave's dS overwrites the slot
+      }
+      // this half's share of dS^T[n][p] = sum_u kr^T[n][u] vs[p][u] (lane = p, elements = n)
+      float4* dsl = hf ? &sh.a[cw][0] : &sh.b[cw][0];
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt)
 #pragma unroll
         for (int pt = 0; pt < PT; ++pt) {
-          f32x16 d = zero16();
-#pragma unroll
-          for (int k = 0; k < 4; ++k) d = mfma(ktx[nt][k], vsy[pt][k], d);
-          float4* dst = &sh.state[w][(nt * PT + pt) * 256];
+          f32x16 d = mfma(ktx[nt][0], vsy[pt][0], zero16());
+          d = mfma(ktx[nt][1], vsy[pt][1], d);
+          float4* dst = dsl + (nt * PT + pt) * 256;
 #pragma unroll
           for (int g = 0; g < 4; ++g)
             dst[g * 64 + lane] = make_float4(d[4 * g], d[4 * g + 1], d[4 * g + 2], d[4 * g + 3]);
         }
-    
-      // y_intra^T[p][t] = (D + delta_t) v[t][p] + sum_u v^T[p][u] score[t][u]
+      // y_intra^T[p][t] = (D + delta_t) v[t][p] + sum_{u < t} v^T[p][u] score[t][u]
+      const float coef = skip + delta;
 #pragma unroll
       for (int pt = 0; pt < PT; ++pt) {
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-          const float coef = skip + delta[tt];
-#pragma unroll
-          for (int e = 0; e < 16; ++e) yacc[pt][tt][e] = coef * slot_f(cur.v[tt][2 * pt + (e >> 3)], e & 7);
+        for (int e = 0; e < 16; ++e) yacc[pt][e] = coef * slot_f(v[2 * pt + (e >> 3)], e & 7);
+        if (hf) {
+          yacc[pt] = mfma(exv[pt][0], scy_o[0], yacc[pt]);
+          yacc[pt] = mfma(exv[pt][1], scy_o[1], yacc[pt]);
         }
-        yacc[pt][0] = mfma(vtx[pt][0], scy[0][0], yacc[pt][0]);
-        yacc[pt][0] = mfma(vtx[pt][1], scy[0][1], yacc[pt][0]);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) yacc[pt][1] = mfma(vtx[pt][k], scy[1][k], yacc[pt][1]);
+        yacc[pt] = mfma(vtx[pt][0], scy_d[0], yacc[pt]);
+        yacc[pt] = mfma(vtx[pt][1], scy_d[1], yacc[pt]);
       }
-
     }
-    __syncthreads();  // barrier 2: every dS in LDS
+    __syncthreads();  // barrier 3: every dS share in LDS
 
-    // gate operand of this chunk and all inputs of the next super-chunk, loaded
-    // while the state scan and the output phase run
-    u32x4 zrow[2][PS];
+    // gate operand of this half, loaded while the state scan runs
+    u32x4 zrow[PS] = {};
+    if (active) {
+      const uint16_t* z_row = zbase + (t < L ? t : t0) * P.z_st;
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-      const int t = t0 + 32 * rt + c32;
-      const uint16_t* z_row = P.z + b * P.z_sb + h * P.z_sh + (t < L ? t : t0) * P.z_st;
-#pragma unroll
-      for (int s = 0; s < PS; ++s) zrow[rt][s] = load_row8(z_row, kidx(s, hh, 0));
+      for (int s = 0; s < PS; ++s) zrow[s] = load_row8(z_row, kidx(s, hh, 0));
     }
 
-    // ---------------- phase B: state scan over the W chunks ----------------
+    // ---------------- state scan over the CW chunks ----------------
     {
-      float dec[W];
+      float dec[CW];
 #pragma unroll
-      for (int j = 0; j < W; ++j) dec[j] = j < nact ? fast_exp2(sh.tot[j]) : 1.f;
+      for (int j = 0; j < CW; ++j) dec[j] = j < nact ? fast_exp2(sh.htot[CW + j] + sh.htot[j]) : 1.f;
 #pragma unroll
       for (int r = 0; r < SPT; ++r) {
-        const int f = threadIdx.x + r * W * 64;
+        const int f = tid + r * W * 64;
         if (f >= kF4) break;
         float4 s = run[r];
 #pragma unroll
-        for (int j = 0; j < W; ++j) {
+        for (int j = 0; j < CW; ++j) {
           if (j < nact) {
-            const float4 d = sh.state[j][f];
-            sh.state[j][f] = s;
-            s = make_float4(s.x * dec[j] + d.x, s.y * dec[j] + d.y, s.z * dec[j] + d.z, s.w * dec[j] + d.w);
+            const float4 d0 = sh.b[j][f];
+            const float4 d1 = sh.a[j][f];
+            sh.a[j][f] = s;
+            s = make_float4(s.x * dec[j] + (d0.x + d1.x), s.y * dec[j] + (d0.y + d1.y),
+                            s.z * dec[j] + (d0.z + d1.z), s.w * dec[j] + (d0.w + d1.w));
           }
         }
         run[r] = s;
       }
-      if (threadIdx.x < R) {
-        double cr = sh.carry[threadIdx.x];
-        for (int j = 0; j < nact; ++j) cr += sh.wsum[j][threadIdx.x];
-        sh.carry[threadIdx.x] = cr - kTwoPiD * floor(cr * (1.0 / kTwoPiD));
+      if (tid < R) {
+        double cr = sh.carry[tid];
+        for (int j = 0; j < 2 * nact; ++j) cr += sh.wsum[j][tid];
+        sh.carry[tid] = cr - kTwoPiD * floor(cr * (1.0 / kTwoPiD));
       }
     }
-    __syncthreads();  // barrier 3: exclusive states in LDS
+    __syncthreads();  // barrier 4: exclusive states in LDS
 
-    // ---------------- phase C: inter-chunk term, gate, store ----------------
+    // ---------------- inter-chunk term, gate, store ----------------
+    if (active) {
+      const bool ok = t < L;
+      const float decay = fast_exp2(csf);
 #pragma unroll
-    for (int pt = 0; pt < PT; ++pt) {
-      f32x16 yi[2] = {zero16(), zero16()};
+      for (int pt = 0; pt < PT; ++pt) {
+        f32x16 yi = zero16();
 #pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        // X rows p, K = n: D elements 8*(s&1) .. +7 of tile (s>>1, pt)
-        const float4* src = &sh.state[w][((s >> 1) * PT + pt) * 256];
-        const float4 lo = src[(2 * (s & 1)) * 64 + lane];
-        const float4 hi = src[(2 * (s & 1) + 1) * 64 + lane];
-        u32x4 sx;
-        sx[0] = pack2(lo.x, lo.y);
-        sx[1] = pack2(lo.z, lo.w);
-        sx[2] = pack2(hi.x, hi.y);
-        sx[3] = pack2(hi.z, hi.w);
-        yi[0] = mfma(sx, qrow[0][s], yi[0]);
-        yi[1] = mfma(sx, qrow[1][s], yi[1]);
-      }
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        const int t = t0 + 32 * tt + c32;
-        if (active && t < T) {
-          const bool ok = t < L;
-          const float decay = fast_exp2(csr[tt]);
+        for (int s = 0; s < KS; ++s) {
+          // X rows p, K = n: D elements 8*(s&1) .. +7 of tile (s>>1, pt)
+          const float4* src = &sh.a[cw][((s >> 1) * PT + pt) * 256];
+          const float4 lo = src[(2 * (s & 1)) * 64 + lane];
+          const float4 hi = src[(2 * (s & 1) + 1) * 64 + lane];
+          u32x4 sx;
+          sx[0] = pack2(lo.x, lo.y);
+          sx[1] = pack2(lo.z, lo.w);
+          sx[2] = pack2(hi.x, hi.y);
+          sx[3] = pack2(hi.z, hi.w);
+          yi = mfma(sx, qrow[s], yi);
+        }
+        if (t < T) {
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
             float y[4];
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const int e = 4 * g + q;
-              const float zz = slot_f(zrow[tt][2 * pt + (e >> 3)], e & 7);
-              const float acc = yacc[pt][tt][e] + yi[tt][e] * decay;
-              y[q] = ok ? acc * (zz * sigmoid_fast(zz)) : 0.f;
+            for (int q4 = 0; q4 < 4; ++q4) {
+              const int e = 4 * g + q4;
+              const float zz = slot_f(zrow[2 * pt + (e >> 3)], e & 7);
+              const float acc = yacc[pt][e] + yi[e] * decay;
+              y[q4] = ok ? acc * (zz * sigmoid_fast(zz)) : 0.f;
             }
-            const int p0 = 32 * pt + 8 * g + 4 * hh;
-            const int off = b * P.o_sb + h * P.o_sh + t * P.o_st + p0;
+            const int off = obase + t * P.o_st + 32 * pt + 8 * g + 4 * hh;
             if (P.out_f32) {
               *reinterpret_cast<float4*>(static_cast<float*>(P.out) + off) = make_float4(y[0], y[1], y[2], y[3]);
             } else {
@@ -663,8 +662,8 @@ __global__ __launch_bounds__(W * 64) void mamba_mfma_kernel(const MfmaParams P) 
   // rows past the last valid chunk (only when lengths < T)
   constexpr int PD = 32 * PT;
   for (int e = nvalid * kChunk * PD + threadIdx.x; e < T * PD; e += W * 64) {
-    const int t = e / PD, p = e - t * PD;
-    const int off = b * P.o_sb + h * P.o_sh + t * P.o_st + p;
+    const int tt = e / PD, p = e - tt * PD;
+    const int off = obase + tt * P.o_st + p;
     if (P.out_f32)
       static_cast<float*>(P.out)[off] = 0.f;
     else
@@ -739,20 +738,15 @@ MfmaParams make_params(const tf_mamba_args& a) {
   return P;
 }
 
-template <int NT, int PT, int W>
+template <int NT, int PT, int CW>
 int launch_shape(const tf_mamba_args& a, hipStream_t stream) {
   const int64_t units = a.batch * a.heads;
-  hipLaunchKernelGGL((mamba_mfma_kernel<NT, PT, W>), dim3(static_cast<uint32_t>(units)), dim3(W * 64), 0, stream,
-                     make_params(a));
+  const dim3 grid(static_cast<uint32_t>(units)), block(CW * 128);
+  if (a.rotary > a.state / 4)
+    hipLaunchKernelGGL((mamba_mfma_kernel<NT, PT, CW, true>), grid, block, 0, stream, make_params(a));
+  else
+    hipLaunchKernelGGL((mamba_mfma_kernel<NT, PT, CW, false>), grid, block, 0, stream, make_params(a));
   return launch_status();
-}
-
-// Four waves (one per SIMD, up to 512 registers each): the chunk-local working
-// set of a 64-step chunk does not fit the 256 registers a wave gets at two
-// waves per SIMD without spilling.
-template <int NT, int PT>
-int launch_waves(const tf_mamba_args& a, hipStream_t stream) {
-  return launch_shape<NT, PT, 4>(a, stream);
 }
 
 }  // namespace
@@ -766,6 +760,7 @@ bool mfma_supported(const tf_mamba_args& a) {
   if (a.out_dtype != TF_BFLOAT16 && a.out_dtype != TF_FLOAT32) return false;
   if (!(a.state == 32 || a.state == 64 || a.state == 128)) return false;
   if (!(a.head_dim == 32 || a.head_dim == 64)) return false;
+  if (a.rotary < 0 || a.rotary > a.state / 2) return false;
   // the phase staging area [64 rows][R rounded up to even] lives in a state slot
   if (64 * ((a.rotary + 1) & ~int64_t(1)) > (a.state / 32) * (a.head_dim / 32) * 1024) return false;
   if (a.batch * a.heads > 0x7fffffff) return false;
@@ -777,15 +772,18 @@ bool mfma_supported(const tf_mamba_args& a) {
   return offsets_fit(a);
 }
 
+// Four chunks (eight waves, two per SIMD) per super-chunk. N=128 keeps two
+// chunks (four waves, one per SIMD): its working set needs the 512 registers a
+// lone wave gets, and with P=64 its two LDS slots per chunk would not fit four.
 int launch_mfma(const tf_mamba_args& a, hipStream_t stream) {
   const int nt = static_cast<int>(a.state / 32);
   const int pt = static_cast<int>(a.head_dim / 32);
-  if (nt == 1 && pt == 1) return launch_waves<1, 1>(a, stream);
-  if (nt == 1 && pt == 2) return launch_waves<1, 2>(a, stream);
-  if (nt == 2 && pt == 1) return launch_waves<2, 1>(a, stream);
-  if (nt == 2 && pt == 2) return launch_waves<2, 2>(a, stream);
-  if (nt == 4 && pt == 1) return launch_waves<4, 1>(a, stream);
-  if (nt == 4 && pt == 2) return launch_waves<4, 2>(a, stream);
+  if (nt == 1 && pt == 1) return launch_shape<1, 1, 4>(a, stream);
+  if (nt == 1 && pt == 2) return launch_shape<1, 2, 4>(a, stream);
+  if (nt == 2 && pt == 1) return launch_shape<2, 1, 4>(a, stream);
+  if (nt == 2 && pt == 2) return launch_shape<2, 2, 4>(a, stream);
+  if (nt == 4 && pt == 1) return launch_shape<4, 1, 2>(a, stream);
+  if (nt == 4 && pt == 2) return launch_shape<4, 2, 2>(a, stream);
   return TF_ERR_SHAPE;
 }
 
