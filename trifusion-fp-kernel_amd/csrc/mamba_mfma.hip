@@ -105,6 +105,15 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Workgroup barrier ordering LDS accesses only. Waves exchange data through LDS
+// alone, so global loads in flight (the next super-chunk's inputs) stay
+// outstanding across it instead of being drained as a full fence would.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 __device__ __forceinline__ float sigmoid_fast(float x) {
   return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-x * kLog2e));
 }
@@ -140,7 +149,9 @@ __device__ __forceinline__ float4 as_f4(const u32x4& u) { return __builtin_bit_c
 
 // tanh for |x| < 0.625 by the odd polynomial of the Cephes single-precision
 // tanhf (S. L. Moshier, Cephes Math Library), else 1 - 2/(exp(2|x|) + 1) with the
-// hardware exp2/rcp, evaluated only when some lane of the wave needs it.
+// hardware exp2/rcp, evaluated only when some lane of the wave needs it. (The
+// exp form alone is biased by ~1e-7 near 0, which the phase cumsum carries
+// into a visible error after a few thousand steps.)
 __device__ __forceinline__ float tanh_fast(float x) {
   const float ax = fabsf(x);
   const float z = x * x;
@@ -223,6 +234,58 @@ __device__ __forceinline__ void score_tile(const f32x16& acc, float cst, const f
   }
 }
 
+// Global inputs of one wave's 32 rows: row t of the lane in MFMA row form
+// (q, k, v and the controls), and for the phase lane rows first .. first+RPL-1
+// of its rotary pair (column offset gcol). Rows past L read a valid row; their
+// dt is 0, so they reach neither the outputs nor the state.
+template <int KS, int PS, int RPL>
+struct HalfIn {
+  u32x4 q[KS], k[KS], v[PS];
+  float th[RPL];
+  float dt, dn, adt, tr, tn;
+};
+
+template <int KS, int PS, int RPL>
+__device__ __forceinline__ void load_half(const MfmaParams& P, HalfIn<KS, PS, RPL>& in, const uint16_t* qbase,
+                                          const uint16_t* kbase, const uint16_t* vbase, const float* dtb,
+                                          const float* adtb, int trb, int gcol, int t0, int t, int first, int L,
+                                          int hh) {
+  const bool valid = t < L;
+  const bool next = t + 1 < P.T;
+  const int tl = valid ? t : t0;
+  const uint16_t* q_row = qbase + tl * P.q_st;
+  const uint16_t* k_row = kbase + tl * P.k_st;
+  const uint16_t* v_row = vbase + tl * P.v_st;
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    in.q[s] = load_row8(q_row, kidx(s, hh, 0));
+    in.k[s] = load_row8(k_row, kidx(s, hh, 0));
+  }
+#pragma unroll
+  for (int s = 0; s < PS; ++s) in.v[s] = load_row8(v_row, kidx(s, hh, 0));
+  in.dt = valid ? dtb[t * P.d_st] : 0.f;
+  in.dn = next ? dtb[(t + 1) * P.d_st] : 0.f;
+  in.adt = valid ? adtb[t * P.a_st] : 0.f;
+  if (P.trap_bf16) {
+    const bf16_t* tp = static_cast<const bf16_t*>(P.trap) + trb;
+    in.tr = valid ? to_f32(tp[t * P.r_st]) : 0.f;
+    in.tn = next ? to_f32(tp[(t + 1) * P.r_st]) : 0.f;
+  } else {
+    const float* tp = static_cast<const float*>(P.trap) + trb;
+    in.tr = valid ? tp[t * P.r_st] : 0.f;
+    in.tn = next ? tp[(t + 1) * P.r_st] : 0.f;
+  }
+  if (P.angles_dtype == TF_FLOAT32) {
+    const float* ap = static_cast<const float*>(P.angles) + gcol;
+#pragma unroll
+    for (int r = 0; r < RPL; ++r) in.th[r] = ap[min(first + r, L - 1) * P.g_st];
+  } else {
+    const bf16_t* ap = static_cast<const bf16_t*>(P.angles) + gcol;
+#pragma unroll
+    for (int r = 0; r < RPL; ++r) in.th[r] = to_f32(ap[min(first + r, L - 1) * P.g_st]);
+  }
+}
+
 // WIDE: R in (N/4, N/2], else R <= N/4. The phase lanes of a wave take pair
 // pp = lane % RP over RPL consecutive rows of the wave's half, segment
 // seg = lane / RP (64 / RP segments of RPL rows cover the 32 rows).
@@ -281,7 +344,19 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
   const u32x4 ident0 = identity_rows(0, (threadIdx.x >> 5) & 1, threadIdx.x & 31);
   const u32x4 ident1 = identity_rows(1, (threadIdx.x >> 5) & 1, threadIdx.x & 31);
 
-  __syncthreads();
+  // inputs of the first super-chunk; later ones are prefetched one super-chunk
+  // ahead, while the state scan and the output phase run
+  using In = HalfIn<KS, PS, RPL>;
+  In cur = {};
+  if (cw < min(CW, nvalid)) {
+    const int ln = threadIdx.x & 63;
+    const int p0 = ln & (RP - 1);
+    const int r0 = 32 * hf;
+    load_half(P, cur, qbase, kbase, vbase, dtb, adtb, trb, gbase + (p0 < R ? p0 : 0) * P.g_sr, cw * kChunk,
+              cw * kChunk + r0 + (ln & 31), cw * kChunk + r0 + (ln / RP) * RPL, L, ln >> 5);
+  }
+
+  lds_barrier();
 
   for (int g0 = 0; g0 < nvalid; g0 += CW) {
     // Lane-derived indices are rebuilt from an index the compiler cannot see
@@ -304,57 +379,19 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
     // Values carried from one "if (active)" region to a later one are given a
     // definition on the idle path too: left undefined there, the compiler
     // carries them around the loop and holds their registers through every phase.
-    u32x4 q[KS] = {}, k[KS] = {}, v[PS] = {};
-    float th[RPL] = {};
+    u32x4 (&q)[KS] = cur.q;
+    u32x4 (&k)[KS] = cur.k;
+    u32x4 (&v)[PS] = cur.v;
+    float (&th)[RPL] = cur.th;
+    const float dtv = cur.dt;
     float csr = 0.f, gam = 0.f, scl = 0.f;
     double seg_part = 0.0;
-    // ---------------- loads, controls, phase pass 1 ----------------
+    // ---------------- controls, phase pass 1 ----------------
     if (active) {
-      const bool valid = t < L;
-      const bool next = t + 1 < T;
-      // rows past L read row t0 (valid) and never reach the outputs or the state
-      const int tl = valid ? t : t0;
-      const uint16_t* q_row = qbase + tl * P.q_st;
-      const uint16_t* k_row = kbase + tl * P.k_st;
-      const uint16_t* v_row = vbase + tl * P.v_st;
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        q[s] = load_row8(q_row, kidx(s, hh, 0));
-        k[s] = load_row8(k_row, kidx(s, hh, 0));
-      }
-#pragma unroll
-      for (int s = 0; s < PS; ++s) v[s] = load_row8(v_row, kidx(s, hh, 0));
-      const float dtv = valid ? dtb[t * P.d_st] : 0.f;
-      const float dnv = next ? dtb[(t + 1) * P.d_st] : 0.f;
-      const float adv = valid ? adtb[t * P.a_st] : 0.f;
-      float trv, tnv;
-      if (P.trap_bf16) {
-        const bf16_t* tp = static_cast<const bf16_t*>(P.trap) + trb;
-        trv = valid ? to_f32(tp[t * P.r_st]) : 0.f;
-        tnv = next ? to_f32(tp[(t + 1) * P.r_st]) : 0.f;
-      } else {
-        const float* tp = static_cast<const float*>(P.trap) + trb;
-        trv = valid ? tp[t * P.r_st] : 0.f;
-        tnv = next ? tp[(t + 1) * P.r_st] : 0.f;
-      }
-      // raw angles of the phase lane's rows (clamped to a valid row; their dt is 0)
-      const int first = t0 + 32 * hf + seg * RPL;
-      if (P.angles_dtype == TF_FLOAT32) {
-        const float* ap = static_cast<const float*>(P.angles) + gbase + (pair_on ? pp : 0) * P.g_sr;
-#pragma unroll
-        for (int r = 0; r < RPL; ++r)
-          th[r] = ap[min(first + r, L - 1) * P.g_st];
-      } else {
-        const bf16_t* ap = static_cast<const bf16_t*>(P.angles) + gbase + (pair_on ? pp : 0) * P.g_sr;
-#pragma unroll
-        for (int r = 0; r < RPL; ++r)
-          th[r] = to_f32(ap[min(first + r, L - 1) * P.g_st]);
-      }
-
       // controls (mamba_fused.py:98-110) and the half's cumulative log2 decay
-      gam = dtv * sigmoid_fast(trv);
-      scl = dnv * (1.f - sigmoid_fast(tnv)) + gam;
-      csr = half_scan(adv * kLog2e, c32);
+      gam = dtv * sigmoid_fast(cur.tr);
+      scl = cur.dn * (1.f - sigmoid_fast(cur.tn)) + gam;
+      csr = half_scan(cur.adt * kLog2e, c32);
       const float ltot = half_last(csr);
       if (hh == 0) {
         sh.dt[cw][32 * hf + c32] = dtv;
@@ -376,7 +413,7 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
       for (int off = RP; off < 64; off <<= 1) sum += __shfl_xor(sum, off);
       if (seg == 0 && pair_on) sh.wsum[sub][pp] = sum;
     }
-    __syncthreads();  // barrier 1: half sums of decay and phase visible
+    lds_barrier();  // barrier 1: half sums of decay and phase visible
 
     u32x4 qrow[KS] = {};  // rotated q rows (Y operand over n)
     u32x4 scy_d[2] = {};  // diagonal score tile (Y rows t, K = u of this half)
@@ -395,7 +432,11 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
       {
         const int ppc = pair_on ? pp : 0;
         double carry = sh.carry[ppc];
-        for (int j = 0; j < sub; ++j) carry += sh.wsum[j][ppc];
+#pragma unroll
+        for (int j = 0; j < 2 * CW; ++j) {  // independent reads, summed in order
+          const double x = sh.wsum[j][ppc];
+          carry += j < sub ? x : 0.0;
+        }
         double pre = seg_part;  // inclusive scan over the segments of the same pair
         for (int off = RP; off < 64; off <<= 1) {
           const double o = __shfl_up(pre, off);
@@ -528,7 +569,7 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
           for (int sp = 0; sp < 2; ++sp) ex[(KS + 2 * pt + sp) * 64 + lane] = as_f4(vtx[pt][sp]);
       }
     }
-    __syncthreads();  // barrier 2: exchange tiles visible, phase staging no longer read
+    lds_barrier();  // barrier 2: exchange tiles visible, phase staging no longer read
 
     f32x16 yacc[PT] = {};  // y^T tiles: lane = t, elements = p
     if (active) {
@@ -574,7 +615,7 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
         yacc[pt] = mfma(vtx[pt][1], scy_d[1], yacc[pt]);
       }
     }
-    __syncthreads();  // barrier 3: every dS share in LDS
+    lds_barrier();  // barrier 3: every dS share in LDS
 
     // gate operand of this half, loaded while the state scan runs
     u32x4 zrow[PS] = {};
@@ -582,6 +623,18 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
       const uint16_t* z_row = zbase + (t < L ? t : t0) * P.z_st;
 #pragma unroll
       for (int s = 0; s < PS; ++s) zrow[s] = load_row8(z_row, kidx(s, hh, 0));
+      // rows in [L, T) get z = 0, whose gate silu(0) = 0 writes them as zeros
+      if (t >= L) {
+#pragma unroll
+        for (int s = 0; s < PS; ++s) zrow[s] = u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+    // inputs of the same half of the next super-chunk
+    In nxt = {};
+    if (g0 + CW + cw < nvalid) {
+      const int tn = (g0 + CW + cw) * kChunk;
+      load_half(P, nxt, qbase, kbase, vbase, dtb, adtb, trb, gbase + (pair_on ? pp : 0) * P.g_sr, tn,
+                tn + 32 * hf + c32, tn + 32 * hf + seg * RPL, L, hh);
     }
 
     // ---------------- state scan over the CW chunks ----------------
@@ -612,11 +665,10 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
         sh.carry[tid] = cr - kTwoPiD * floor(cr * (1.0 / kTwoPiD));
       }
     }
-    __syncthreads();  // barrier 4: exclusive states in LDS
+    lds_barrier();  // barrier 4: exclusive states in LDS
 
     // ---------------- inter-chunk term, gate, store ----------------
     if (active) {
-      const bool ok = t < L;
       const float decay = fast_exp2(csf);
 #pragma unroll
       for (int pt = 0; pt < PT; ++pt) {
@@ -634,17 +686,16 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
           sx[3] = pack2(hi.z, hi.w);
           yi = mfma(sx, qrow[s], yi);
         }
+        float yv[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const float zz = slot_f(zrow[2 * pt + (e >> 3)], e & 7);
+          yv[e] = (yacc[pt][e] + yi[e] * decay) * (zz * sigmoid_fast(zz));
+        }
         if (t < T) {
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
-            float y[4];
-#pragma unroll
-            for (int q4 = 0; q4 < 4; ++q4) {
-              const int e = 4 * g + q4;
-              const float zz = slot_f(zrow[2 * pt + (e >> 3)], e & 7);
-              const float acc = yacc[pt][e] + yi[e] * decay;
-              y[q4] = ok ? acc * (zz * sigmoid_fast(zz)) : 0.f;
-            }
+            const float y[4] = {yv[4 * g], yv[4 * g + 1], yv[4 * g + 2], yv[4 * g + 3]};
             const int off = obase + t * P.o_st + 32 * pt + 8 * g + 4 * hh;
             if (P.out_f32) {
               *reinterpret_cast<float4*>(static_cast<float*>(P.out) + off) = make_float4(y[0], y[1], y[2], y[3]);
@@ -658,6 +709,7 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
         }
       }
     }
+    cur = nxt;
   }
   // rows past the last valid chunk (only when lengths < T)
   constexpr int PD = 32 * PT;
