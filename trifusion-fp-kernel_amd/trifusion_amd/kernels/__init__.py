@@ -8,6 +8,7 @@ import torch
 from torch import nn
 
 from .. import _lib
+from ..ops import ops
 from .native import rms
 
 
@@ -22,7 +23,12 @@ class RMSNorm(nn.Module):
 
 
 def swiglu(x):
-    """``silu(g) * u`` with ``g, u`` the halves of the last dim (fp32 math)."""
+    """``silu(g) * u`` with ``g, u`` the halves of the last dim (fp32 math)
+    (``trifusion_amd::swiglu``)."""
+    return ops.swiglu(x)
+
+
+def launch_swiglu(x):
     lib = _lib.load()
     _lib.require_cuda(x, what="swiglu")
     x = x.contiguous()

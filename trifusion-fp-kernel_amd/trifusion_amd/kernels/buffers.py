@@ -8,10 +8,16 @@ and ``mamba_controls`` replaces ``buffers.py:82-101`` (``_controls``,
 import torch
 
 from .. import _lib
+from ..ops import ops
 
 
 def mask_buffer(x, mask):
-    """Copy of ``x`` with rows whose ``mask`` entry is false set to zero."""
+    """Copy of ``x`` with rows whose ``mask`` entry is false set to zero
+    (``trifusion_amd::mask_rows``)."""
+    return ops.mask_rows(x, mask)
+
+
+def launch_mask_rows(x, mask):
     lib = _lib.load()
     _lib.require_cuda(x, mask, what="mask_buffer")
     x = x.contiguous()
@@ -33,7 +39,12 @@ def mamba_controls(a, dt, bias, floor):
 
     ``a`` and ``dt`` are column slices of one projection and share strides, the
     head dimension unit-strided (as at ``src/trifusion_l4/mamba.py:65``).
+    Dispatches through ``trifusion_amd::mamba_controls``.
     """
+    return ops.mamba_controls(a, dt, bias, float(floor))
+
+
+def launch_mamba_controls(a, dt, bias, floor):
     lib = _lib.load()
     _lib.require_cuda(a, dt, bias, what="mamba_controls")
     b, t, h = a.shape

@@ -9,6 +9,7 @@ its normalised copy in one pass.
 import torch
 
 from .. import _lib
+from ..ops import ops
 
 
 def _row_view(x):
@@ -32,7 +33,12 @@ def _row_view(x):
 
 
 def rms(x, weight, eps=1e-5, out_dtype=None):
-    """RMSNorm over the last dim with fp32 statistics; output dtype = x.dtype."""
+    """RMSNorm over the last dim with fp32 statistics; output dtype = x.dtype
+    (``trifusion_amd::rms_norm``)."""
+    return ops.rms_norm(x, weight, eps, out_dtype)
+
+
+def launch_rms(x, weight, eps=1e-5, out_dtype=None):
     lib = _lib.load()
     _lib.require_cuda(x, weight, what="rms")
     if weight.dtype != torch.float32 or not weight.is_contiguous():
@@ -60,7 +66,12 @@ def rms(x, weight, eps=1e-5, out_dtype=None):
 
 
 def add(a, b, mask=None, bf16=False):
-    """``a + b`` in fp32, zeroing rows whose mask is false; dtype as the reference."""
+    """``a + b`` in fp32, zeroing rows whose mask is false; dtype as the reference
+    (``trifusion_amd::add``)."""
+    return ops.add(a, b, mask, bf16)
+
+
+def launch_add(a, b, mask=None, bf16=False):
     lib = _lib.load()
     _lib.require_cuda(a, b, mask, what="add")
     a = a.contiguous()
@@ -89,7 +100,12 @@ def add(a, b, mask=None, bf16=False):
 
 
 def add_rms(a, b, weight, mask=None, eps=1e-5, out_dtype=torch.bfloat16):
-    """Fused ``s = add(a, b, mask)`` (fp32) and ``y = rms(s, weight)`` (``out_dtype``)."""
+    """Fused ``s = add(a, b, mask)`` (fp32) and ``y = rms(s, weight)`` (``out_dtype``)
+    (``trifusion_amd::add_rms_norm``)."""
+    return ops.add_rms_norm(a, b, weight, mask, eps, out_dtype)
+
+
+def launch_add_rms(a, b, weight, mask=None, eps=1e-5, out_dtype=torch.bfloat16):
     lib = _lib.load()
     _lib.require_cuda(a, b, mask, weight, what="add_rms")
     if a.dtype != torch.float32:

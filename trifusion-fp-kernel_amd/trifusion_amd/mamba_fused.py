@@ -16,6 +16,7 @@ import ctypes
 import torch
 
 from . import _lib
+from .ops import ops
 
 SUPPORTED_STATE = (16, 32, 64, 128)
 SUPPORTED_HEAD = (32, 64)
@@ -105,20 +106,27 @@ def build_args(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths=None, 
     return a
 
 
+def launch(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths=None, variant="auto"):
+    """Validate, then enqueue ``tf_fused_mamba`` on the current stream (the CUDA
+    kernel of the ``trifusion_amd::fused_mamba`` operator); returns ``out``."""
+    lib = _lib.load()
+    args = build_args(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths, variant)
+    _lib.check(lib.tf_fused_mamba(ctypes.byref(args), _lib.stream_of(v)), "fused_mamba")
+    return out
+
+
 def fused_mamba(q, k, v, adt, dt, trap, qb, kb, angles, d, z, warps=8, *, out=None, lengths=None, variant="auto"):
     """Fused Mamba-3 recurrence forward; returns ``out`` ``[B, T, H, P]``.
 
     ``warps`` is accepted for signature compatibility; gfx950 launch shapes are
     chosen by the library. ``variant`` selects ``"auto"`` (MFMA chunked scan
-    where supported), ``"mfma"`` or ``"generic"``.
+    where supported), ``"mfma"`` or ``"generic"``. Dispatches through the
+    ``trifusion_amd::fused_mamba`` operator (``fused_mamba.out`` with ``out=``).
     """
     del warps
-    lib = _lib.load()
     if out is None:
-        out = torch.empty_like(v, memory_format=torch.contiguous_format)
-    args = build_args(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths, variant)
-    _lib.check(lib.tf_fused_mamba(ctypes.byref(args), _lib.stream_of(v)), "fused_mamba")
-    return out
+        return ops.fused_mamba(q, k, v, adt, dt, trap, qb, kb, angles, d, z, lengths, variant)
+    return ops.fused_mamba.out(q, k, v, adt, dt, trap, qb, kb, angles, d, z, lengths, variant, out=out)
 
 
 def selected_variant(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out=None, lengths=None, variant="auto"):

@@ -4,11 +4,17 @@
 import torch
 
 from . import _lib
+from .ops import ops
 from .kernels.buffers import mask_buffer
 
 
 def time_mask(lengths, time):
-    """``mask[b, t] = t < lengths[b]`` as a bool ``[B, T]`` device tensor."""
+    """``mask[b, t] = t < lengths[b]`` as a bool ``[B, T]`` device tensor
+    (``trifusion_amd::time_mask``)."""
+    return ops.time_mask(lengths, int(time))
+
+
+def launch_time_mask(lengths, time):
     lib = _lib.load()
     _lib.require_cuda(lengths, what="time_mask")
     lengths = lengths.to(torch.int64).contiguous()
@@ -24,7 +30,12 @@ def masked(x, mask):
 
 
 def masked_mean(x, lengths):
-    """``sum_{t < len} x[b, t] / len`` in fp32, ``x`` ``[B, T, D]`` -> ``[B, D]``."""
+    """``sum_{t < len} x[b, t] / len`` in fp32, ``x`` ``[B, T, D]`` -> ``[B, D]``
+    (``trifusion_amd::masked_mean``)."""
+    return ops.masked_mean(x, lengths)
+
+
+def launch_masked_mean(x, lengths):
     lib = _lib.load()
     _lib.require_cuda(x, lengths, what="masked_mean")
     x = x.contiguous()

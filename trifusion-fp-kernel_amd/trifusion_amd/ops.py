@@ -1,0 +1,185 @@
+"""``trifusion_amd::*`` torch operators over the C-ABI library.
+
+Every compute entry point of ``include/trifusion_amd.h`` is registered with
+``torch.library`` in the ``trifusion_amd`` namespace:
+
+* a CUDA kernel (ROCm devices dispatch through the CUDA key) that validates
+  the operands and calls the C entry on the current stream;
+* a Meta kernel giving output shapes and dtypes, so the operators trace under
+  fake tensors (``torch.compile``, ``torch.export``) without a device;
+* a CPU kernel that raises: there is no CPU path by design.
+
+The public Python API (``fused_mamba``, ``kernels.rms``, ``kernels.swiglu``,
+...) calls these operators, so eager calls, graph capture and tracing all go
+through the same dispatcher entry. The reference launches its Triton kernels
+directly from Python (``src/trifusion_l4/mamba_fused.py:162-190``); the
+operator layer is the torch-native form of that launch.
+"""
+
+import torch
+
+NAMESPACE = "trifusion_amd"
+
+_SCHEMAS = {
+    "fused_mamba": "fused_mamba(Tensor q, Tensor k, Tensor v, Tensor adt, Tensor dt, Tensor trap, Tensor qb, "
+    "Tensor kb, Tensor angles, Tensor d, Tensor z, Tensor? lengths=None, str variant='auto') -> Tensor",
+    "fused_mamba.out": "fused_mamba.out(Tensor q, Tensor k, Tensor v, Tensor adt, Tensor dt, Tensor trap, "
+    "Tensor qb, Tensor kb, Tensor angles, Tensor d, Tensor z, Tensor? lengths=None, str variant='auto', *, "
+    "Tensor(a!) out) -> Tensor(a!)",
+    "rms_norm": "rms_norm(Tensor x, Tensor weight, float eps=1e-05, ScalarType? out_dtype=None) -> Tensor",
+    "add_rms_norm": "add_rms_norm(Tensor a, Tensor b, Tensor weight, Tensor? mask=None, float eps=1e-05, "
+    "ScalarType? out_dtype=None) -> (Tensor, Tensor)",
+    "add": "add(Tensor a, Tensor b, Tensor? mask=None, bool bf16=False) -> Tensor",
+    "swiglu": "swiglu(Tensor x) -> Tensor",
+    "mask_rows": "mask_rows(Tensor x, Tensor mask) -> Tensor",
+    "mamba_controls": "mamba_controls(Tensor a, Tensor dt, Tensor bias, float floor) -> (Tensor, Tensor)",
+    "masked_mean": "masked_mean(Tensor x, Tensor lengths) -> Tensor",
+    "time_mask": "time_mask(Tensor lengths, int time) -> Tensor",
+}
+
+OPERATORS = tuple(_SCHEMAS)
+
+
+# ---- CUDA kernels: the ctypes launches (imported lazily: those modules call these operators) ----
+
+
+def _cuda_fused_mamba(q, k, v, adt, dt, trap, qb, kb, angles, d, z, lengths=None, variant="auto"):
+    from .mamba_fused import launch
+
+    out = torch.empty_like(v, memory_format=torch.contiguous_format)
+    return launch(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths, variant)
+
+
+def _cuda_fused_mamba_out(q, k, v, adt, dt, trap, qb, kb, angles, d, z, lengths=None, variant="auto", *, out):
+    from .mamba_fused import launch
+
+    return launch(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths, variant)
+
+
+def _cuda_rms_norm(x, weight, eps=1e-5, out_dtype=None):
+    from .kernels.native import launch_rms
+
+    return launch_rms(x, weight, eps, out_dtype)
+
+
+def _cuda_add_rms_norm(a, b, weight, mask=None, eps=1e-5, out_dtype=None):
+    from .kernels.native import launch_add_rms
+
+    return launch_add_rms(a, b, weight, mask, eps, out_dtype or torch.bfloat16)
+
+
+def _cuda_add(a, b, mask=None, bf16=False):
+    from .kernels.native import launch_add
+
+    return launch_add(a, b, mask, bf16)
+
+
+def _cuda_swiglu(x):
+    from .kernels import launch_swiglu
+
+    return launch_swiglu(x)
+
+
+def _cuda_mask_rows(x, mask):
+    from .kernels.buffers import launch_mask_rows
+
+    return launch_mask_rows(x, mask)
+
+
+def _cuda_mamba_controls(a, dt, bias, floor):
+    from .kernels.buffers import launch_mamba_controls
+
+    return launch_mamba_controls(a, dt, bias, floor)
+
+
+def _cuda_masked_mean(x, lengths):
+    from .masking import launch_masked_mean
+
+    return launch_masked_mean(x, lengths)
+
+
+def _cuda_time_mask(lengths, time):
+    from .masking import launch_time_mask
+
+    return launch_time_mask(lengths, time)
+
+
+# ---- Meta kernels: output shapes and dtypes only ----
+
+
+def _meta_fused_mamba(q, k, v, adt, dt, trap, qb, kb, angles, d, z, lengths=None, variant="auto"):
+    return torch.empty_like(v, memory_format=torch.contiguous_format)
+
+
+def _meta_fused_mamba_out(q, k, v, adt, dt, trap, qb, kb, angles, d, z, lengths=None, variant="auto", *, out):
+    return out
+
+
+def _meta_rms_norm(x, weight, eps=1e-5, out_dtype=None):
+    return x.new_empty(x.shape, dtype=out_dtype or x.dtype)
+
+
+def _meta_add_rms_norm(a, b, weight, mask=None, eps=1e-5, out_dtype=None):
+    return a.new_empty(a.shape, dtype=torch.float32), a.new_empty(a.shape, dtype=out_dtype or torch.bfloat16)
+
+
+def _meta_add(a, b, mask=None, bf16=False):
+    return a.new_empty(a.shape, dtype=torch.bfloat16 if bf16 else torch.promote_types(a.dtype, b.dtype))
+
+
+def _meta_swiglu(x):
+    return x.new_empty((*x.shape[:-1], x.shape[-1] // 2))
+
+
+def _meta_mask_rows(x, mask):
+    return torch.empty_like(x, memory_format=torch.contiguous_format)
+
+
+def _meta_mamba_controls(a, dt, bias, floor):
+    b, t, h = a.shape
+    return a.new_empty((b, h, t), dtype=torch.float32), a.new_empty((b, h, t), dtype=torch.float32)
+
+
+def _meta_masked_mean(x, lengths):
+    return x.new_empty((x.shape[0], x.shape[2]), dtype=torch.float32)
+
+
+def _meta_time_mask(lengths, time):
+    return lengths.new_empty((lengths.shape[0], time), dtype=torch.bool)
+
+
+# ---- CPU kernels: loud failure, no fallback ----
+
+
+def _no_cpu(name):
+    def kernel(*args, **kwargs):
+        raise RuntimeError(
+            f"{NAMESPACE}::{name} runs only on a ROCm GPU (gfx950); there is no CPU path. "
+            "Move the operands to a cuda device."
+        )
+
+    return kernel
+
+
+_KERNELS = {
+    "fused_mamba": (_cuda_fused_mamba, _meta_fused_mamba),
+    "fused_mamba.out": (_cuda_fused_mamba_out, _meta_fused_mamba_out),
+    "rms_norm": (_cuda_rms_norm, _meta_rms_norm),
+    "add_rms_norm": (_cuda_add_rms_norm, _meta_add_rms_norm),
+    "add": (_cuda_add, _meta_add),
+    "swiglu": (_cuda_swiglu, _meta_swiglu),
+    "mask_rows": (_cuda_mask_rows, _meta_mask_rows),
+    "mamba_controls": (_cuda_mamba_controls, _meta_mamba_controls),
+    "masked_mean": (_cuda_masked_mean, _meta_masked_mean),
+    "time_mask": (_cuda_time_mask, _meta_time_mask),
+}
+
+_LIBRARY = torch.library.Library(NAMESPACE, "DEF")
+for _name, _schema in _SCHEMAS.items():
+    _LIBRARY.define(_schema)
+    _cuda, _meta = _KERNELS[_name]
+    _LIBRARY.impl(_name, _cuda, "CUDA")
+    _LIBRARY.impl(_name, _meta, "Meta")
+    _LIBRARY.impl(_name, _no_cpu(_name), "CPU")
+
+ops = getattr(torch.ops, NAMESPACE)
