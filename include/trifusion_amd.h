@@ -57,6 +57,12 @@ typedef enum tf_mamba_variant {
  *   lengths       [B] int64 or NULL: rows t >= lengths[b] are written as 0 and
  *                 chunks wholly past the length are skipped (extension; NULL
  *                 reproduces the reference exactly).
+ *   workspace     device scratch of workspace_bytes, or NULL/0 (extension).
+ *                 When it holds at least tf_fused_mamba_workspace_size(args)
+ *                 bytes (> 0), long sequences over few (batch, head) units run
+ *                 chunk-parallel: the time axis is cut into segments that run
+ *                 on separate workgroups, joined by a scan of their states.
+ *                 Otherwise each unit is walked by one workgroup.
  * Stride arrays follow the dimension order above.
  */
 typedef struct tf_mamba_args {
@@ -71,6 +77,8 @@ typedef struct tf_mamba_args {
   int64_t angles_stride[4], out_stride[4];
   int64_t adt_stride[3], dt_stride[3], trap_stride[3];
   int64_t batch, time, heads, qk_heads, state, head_dim, rotary;
+  void *workspace;
+  int64_t workspace_bytes;
 } tf_mamba_args;
 
 /*
@@ -79,6 +87,15 @@ typedef struct tf_mamba_args {
  * :162-190), generalised to N in {16,32,64,128}, P in {32,64}, R <= N/2.
  */
 int tf_fused_mamba(const tf_mamba_args *args, void *stream);
+
+/*
+ * Scratch bytes the chunk-parallel path wants for these arguments, or 0 when
+ * one workgroup per unit is used (short sequences, many units, or a kernel
+ * without a segmented form). The reference has no counterpart: its Triton
+ * kernel always walks a unit serially (src/trifusion_l4/mamba_fused.py:93-152).
+ * Negative: a tf_status for invalid arguments.
+ */
+int64_t tf_fused_mamba_workspace_size(const tf_mamba_args *args);
 
 /* Which kernel TF_MAMBA_AUTO would run for these arguments (1 or 2), or a
  * negative tf_status if no kernel can run them. */

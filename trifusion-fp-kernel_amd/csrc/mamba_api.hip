@@ -52,4 +52,11 @@ extern "C" int tf_fused_mamba(const tf_mamba_args* a, void* stream) {
   return which == TF_MAMBA_MFMA ? tf::launch_mfma(*a, s) : tf::launch_generic(*a, s);
 }
 
+extern "C" int64_t tf_fused_mamba_workspace_size(const tf_mamba_args* a) {
+  const int which = tf::select(a);
+  if (which < 0) return which;
+  if (tf::empty(a) || which != TF_MAMBA_MFMA) return 0;
+  return tf::mfma_workspace_bytes(*a);
+}
+
 extern "C" const char* tf_version(void) { return "trifusion_amd 0.1.0 (gfx950)"; }

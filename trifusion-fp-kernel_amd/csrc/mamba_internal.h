@@ -20,5 +20,8 @@ int launch_generic(const tf_mamba_args& a, hipStream_t stream);
 
 bool mfma_supported(const tf_mamba_args& a);
 int launch_mfma(const tf_mamba_args& a, hipStream_t stream);
+// Scratch bytes of the MFMA kernel's chunk-parallel form for these arguments
+// (0: one workgroup per unit).
+int64_t mfma_workspace_bytes(const tf_mamba_args& a);
 
 }  // namespace tf

@@ -192,6 +192,17 @@ struct MfmaParams {
   int r_sb, r_sh, r_st;
   int T, H, group, R, xcd_per;
   int out_f32, trap_bf16, angles_dtype;
+  // Chunk-parallel form: the time axis of each of the `units` (batch, head)
+  // units is cut into G segments of SC chunks, one workgroup per (segment,
+  // unit). Scratch: per (unit, chunk) the phase sum per pair ([NC][64] fp64,
+  // from the phase pre-pass); per record rec = unit * G + segment the state
+  // ([kF4] float4 in kernel layout: the contribution from zero written by the
+  // summary pass, replaced by the state entering the segment by the segment
+  // scan) and the log2 decay. G = 1: no scratch.
+  float4* seg_state;
+  double* chunk_phase;
+  float* seg_decay;
+  int units, G, SC, NC;
 };
 
 template <int NT, int PT, int CW>
@@ -245,7 +256,7 @@ struct HalfIn {
   float dt, dn, adt, tr, tn;
 };
 
-template <int KS, int PS, int RPL>
+template <bool WITH_Q, int KS, int PS, int RPL>
 __device__ __forceinline__ void load_half(const MfmaParams& P, HalfIn<KS, PS, RPL>& in, const uint16_t* qbase,
                                           const uint16_t* kbase, const uint16_t* vbase, const float* dtb,
                                           const float* adtb, int trb, int gcol, int t0, int t, int first, int L,
@@ -258,7 +269,7 @@ __device__ __forceinline__ void load_half(const MfmaParams& P, HalfIn<KS, PS, RP
   const uint16_t* v_row = vbase + tl * P.v_st;
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
-    in.q[s] = load_row8(q_row, kidx(s, hh, 0));
+    if constexpr (WITH_Q) in.q[s] = load_row8(q_row, kidx(s, hh, 0));
     in.k[s] = load_row8(k_row, kidx(s, hh, 0));
   }
 #pragma unroll
@@ -289,7 +300,12 @@ __device__ __forceinline__ void load_half(const MfmaParams& P, HalfIn<KS, PS, RP
 // WIDE: R in (N/4, N/2], else R <= N/4. The phase lanes of a wave take pair
 // pp = lane % RP over RPL consecutive rows of the wave's half, segment
 // seg = lane / RP (64 / RP segments of RPL rows cover the 32 rows).
-template <int NT, int PT, int CW, bool WIDE>
+// MODE 0 computes the outputs of the workgroup's chunks, starting from the
+// state and phase carry entering its time segment (zero, or the segment
+// scan's record). MODE 1 is the summary pass of the chunk-parallel form: from
+// zero it computes only the segment's state contribution, log2 decay and phase
+// sum (no q, z, scores or outputs) and writes them to the segment's record.
+template <int NT, int PT, int CW, bool WIDE, int MODE>
 __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P) {
   constexpr int W = 2 * CW;         // waves: two per chunk
   constexpr int N = 32 * NT;
@@ -307,7 +323,12 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
   const int cw = w % CW;        // chunk slot
   const int hf = w / CW;        // half: rows 32*hf .. 32*hf + 31 of the chunk
   const int sub = 2 * cw + hf;  // time order of the wave's rows within the super-chunk
-  const int unit = P.xcd_per > 0 ? (blockIdx.x & 7) * P.xcd_per + (blockIdx.x >> 3) : static_cast<int>(blockIdx.x);
+  // work item = (time segment, unit), units fastest, so the units sharing a
+  // segment's q/k rows sit next to each other and land on one XCD
+  const int item = P.xcd_per > 0 ? (blockIdx.x & 7) * P.xcd_per + (blockIdx.x >> 3) : static_cast<int>(blockIdx.x);
+  const int tseg = item / P.units;
+  const int unit = item - tseg * P.units;
+  const int rec = unit * P.G + tseg;
   const int b = unit / P.H;
   const int h = unit - b * P.H;
   const int qh = h / P.group;
@@ -319,6 +340,10 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
     L = l < 0 ? 0 : (l > T ? T : static_cast<int>(l));
   }
   const int nvalid = (L + kChunk - 1) / kChunk;
+  // chunks [c_begin, c_end) are this workgroup's; those below c_stop are valid
+  const int c_begin = tseg * P.SC;
+  const int c_end = min(c_begin + P.SC, (T + kChunk - 1) / kChunk);
+  const int c_stop = min(c_end, nvalid);
   const int rs = (R + 1) & ~1;  // row stride of the staged phases (even: 8-byte pair reads)
   const float skip = P.d[h];
 
@@ -333,14 +358,32 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
   const int gbase = b * P.g_sb + h * P.g_sh;
   const int obase = b * P.o_sb + h * P.o_sh;
 
-  for (int i = threadIdx.x; i < 64; i += W * 64) sh.carry[i] = 0.0;
+  // Phase carry entering the segment (both passes): the fp64 sum of the
+  // preceding chunks' phase sums, reduced mod 2pi. kr depends on the absolute
+  // phase, so even the summary pass needs it. State entering the segment
+  // (output pass only): the segment scan's record.
+  const bool seeded = MODE == 0 && P.G > 1;
+  for (int i = threadIdx.x; i < 64; i += W * 64) {
+    double acc = 0.0;
+    if (P.G > 1 && i < R) {
+      const double* cp = P.chunk_phase + static_cast<size_t>(unit) * P.NC * 64 + i;
+#pragma unroll 8
+      for (int c = 0; c < c_begin; ++c) acc += cp[c * 64];
+      acc -= kTwoPiD * floor(acc * (1.0 / kTwoPiD));
+    }
+    sh.carry[i] = acc;
+  }
   for (int i = threadIdx.x; i < N; i += W * 64) {
     sh.qb[i] = P.qb[h * N + i];
     sh.kb[i] = P.kb[h * N + i];
   }
   float4 run[SPT];
 #pragma unroll
-  for (int r = 0; r < SPT; ++r) run[r] = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int r = 0; r < SPT; ++r) {
+    const int f = threadIdx.x + r * W * 64;
+    run[r] = (seeded && f < kF4) ? P.seg_state[static_cast<size_t>(rec) * kF4 + f] : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  float seg_log2 = 0.f;  // log2 decay over the segment (summary pass)
   const u32x4 ident0 = identity_rows(0, (threadIdx.x >> 5) & 1, threadIdx.x & 31);
   const u32x4 ident1 = identity_rows(1, (threadIdx.x >> 5) & 1, threadIdx.x & 31);
 
@@ -348,17 +391,17 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
   // ahead, while the state scan and the output phase run
   using In = HalfIn<KS, PS, RPL>;
   In cur = {};
-  if (cw < min(CW, nvalid)) {
+  if (c_begin + cw < c_stop) {
     const int ln = threadIdx.x & 63;
     const int p0 = ln & (RP - 1);
-    const int r0 = 32 * hf;
-    load_half(P, cur, qbase, kbase, vbase, dtb, adtb, trb, gbase + (p0 < R ? p0 : 0) * P.g_sr, cw * kChunk,
-              cw * kChunk + r0 + (ln & 31), cw * kChunk + r0 + (ln / RP) * RPL, L, ln >> 5);
+    const int r0 = (c_begin + cw) * kChunk + 32 * hf;
+    load_half<MODE == 0>(P, cur, qbase, kbase, vbase, dtb, adtb, trb, gbase + (p0 < R ? p0 : 0) * P.g_sr,
+                         (c_begin + cw) * kChunk, r0 + (ln & 31), r0 + (ln / RP) * RPL, L, ln >> 5);
   }
 
   lds_barrier();
 
-  for (int g0 = 0; g0 < nvalid; g0 += CW) {
+  for (int g0 = c_begin; g0 < c_stop; g0 += CW) {
     // Lane-derived indices are rebuilt from an index the compiler cannot see
     // through each iteration: hoisted out of the loop, the dozens of per-lane
     // addresses they feed would stay live across it and spill.
@@ -370,7 +413,7 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
     const int pp = lane & (RP - 1);
     const int seg = lane / RP;
     const bool pair_on = pp < R;
-    const int nact = min(CW, nvalid - g0);
+    const int nact = min(CW, c_stop - g0);
     const bool active = cw < nact;  // wave-uniform; idle waves only join the barriers
     const int t0 = (g0 + cw) * kChunk;
     const int t = t0 + 32 * hf + c32;  // row of this lane in the row-form tiles
@@ -498,26 +541,25 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
           const uint32_t kw = k[s][q4];
           const float q0 = lo_f(qw) + qb0, q1 = hi_f(qw) + qb1;
           const float k0 = lo_f(kw) + kb0, k1 = hi_f(kw) + kb1;
-          part += q0 * k0 + q1 * k1;
+          if constexpr (MODE == 0) part += q0 * k0 + q1 * k1;
           if (rot) {
             const float c = co[q4], sn = si[q4];
-            qrow[s][q4] = pack2(q0 * c - q1 * sn, q0 * sn + q1 * c);
+            if constexpr (MODE == 0) qrow[s][q4] = pack2(q0 * c - q1 * sn, q0 * sn + q1 * c);
             krow[s][q4] = pack2((k0 * c - k1 * sn) * scl, (k0 * sn + k1 * c) * scl);
           } else {
-            qrow[s][q4] = pack2(q0, q1);
+            if constexpr (MODE == 0) qrow[s][q4] = pack2(q0, q1);
             krow[s][q4] = pack2(k0 * scl, k1 * scl);
           }
         }
       }
-      delta = gam * (part + __shfl_xor(part, 32));
-
       float4* ex = &sh.a[cw][0];
-      if (hf == 0) {
+      if constexpr (MODE == 0) {
+        delta = gam * (part + __shfl_xor(part, 32));
+        if (hf == 0) {
 #pragma unroll
-        for (int s = 0; s < KS; ++s) ex[s * 64 + lane] = as_f4(krow[s]);
-      }
-      // diagonal score tile of this half
-      {
+          for (int s = 0; s < KS; ++s) ex[s * 64 + lane] = as_f4(krow[s]);
+        }
+        // diagonal score tile of this half
         f32x16 sacc = zero16();
 #pragma unroll
         for (int s = 0; s < KS; ++s) sacc = mfma(krow[s], qrow[s], sacc);
@@ -558,11 +600,11 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
 #pragma unroll
           for (int q4 = 0; q4 < 4; ++q4) {
             const int e = 8 * sp + 2 * q4;
-            vtx[pt][sp][q4] = pack2(d[e], d[e + 1]);
+            if constexpr (MODE == 0) vtx[pt][sp][q4] = pack2(d[e], d[e + 1]);
             vsy[pt][sp][q4] = pack2(d[e] * sc16[e], d[e + 1] * sc16[e + 1]);
           }
       }
-      if (hf == 0) {
+      if (MODE == 0 && hf == 0) {
 #pragma unroll
         for (int pt = 0; pt < PT; ++pt)
 #pragma unroll
@@ -576,7 +618,7 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
       u32x4 scy_o[2];
       u32x4 exv[PT][2];
       const float4* ex = &sh.a[cw][0];
-      if (hf) {
+      if (MODE == 0 && hf) {
         // off-diagonal score tile: u in half 0, t in half 1 (entirely causal)
         f32x16 sacc = zero16();
 #pragma unroll
@@ -602,24 +644,26 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
             dst[g * 64 + lane] = make_float4(d[4 * g], d[4 * g + 1], d[4 * g + 2], d[4 * g + 3]);
         }
       // y_intra^T[p][t] = (D + delta_t) v[t][p] + sum_{u < t} v^T[p][u] score[t][u]
-      const float coef = skip + delta;
+      if constexpr (MODE == 0) {
+        const float coef = skip + delta;
 #pragma unroll
-      for (int pt = 0; pt < PT; ++pt) {
+        for (int pt = 0; pt < PT; ++pt) {
 #pragma unroll
-        for (int e = 0; e < 16; ++e) yacc[pt][e] = coef * slot_f(v[2 * pt + (e >> 3)], e & 7);
-        if (hf) {
-          yacc[pt] = mfma(exv[pt][0], scy_o[0], yacc[pt]);
-          yacc[pt] = mfma(exv[pt][1], scy_o[1], yacc[pt]);
+          for (int e = 0; e < 16; ++e) yacc[pt][e] = coef * slot_f(v[2 * pt + (e >> 3)], e & 7);
+          if (hf) {
+            yacc[pt] = mfma(exv[pt][0], scy_o[0], yacc[pt]);
+            yacc[pt] = mfma(exv[pt][1], scy_o[1], yacc[pt]);
+          }
+          yacc[pt] = mfma(vtx[pt][0], scy_d[0], yacc[pt]);
+          yacc[pt] = mfma(vtx[pt][1], scy_d[1], yacc[pt]);
         }
-        yacc[pt] = mfma(vtx[pt][0], scy_d[0], yacc[pt]);
-        yacc[pt] = mfma(vtx[pt][1], scy_d[1], yacc[pt]);
       }
     }
     lds_barrier();  // barrier 3: every dS share in LDS
 
     // gate operand of this half, loaded while the state scan runs
     u32x4 zrow[PS] = {};
-    if (active) {
+    if (MODE == 0 && active) {
       const uint16_t* z_row = zbase + (t < L ? t : t0) * P.z_st;
 #pragma unroll
       for (int s = 0; s < PS; ++s) zrow[s] = load_row8(z_row, kidx(s, hh, 0));
@@ -631,17 +675,21 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
     }
     // inputs of the same half of the next super-chunk
     In nxt = {};
-    if (g0 + CW + cw < nvalid) {
+    if (g0 + CW + cw < c_stop) {
       const int tn = (g0 + CW + cw) * kChunk;
-      load_half(P, nxt, qbase, kbase, vbase, dtb, adtb, trb, gbase + (pair_on ? pp : 0) * P.g_sr, tn,
-                tn + 32 * hf + c32, tn + 32 * hf + seg * RPL, L, hh);
+      load_half<MODE == 0>(P, nxt, qbase, kbase, vbase, dtb, adtb, trb, gbase + (pair_on ? pp : 0) * P.g_sr, tn,
+                           tn + 32 * hf + c32, tn + 32 * hf + seg * RPL, L, hh);
     }
 
     // ---------------- state scan over the CW chunks ----------------
     {
       float dec[CW];
 #pragma unroll
-      for (int j = 0; j < CW; ++j) dec[j] = j < nact ? fast_exp2(sh.htot[CW + j] + sh.htot[j]) : 1.f;
+      for (int j = 0; j < CW; ++j) {
+        const float tj = sh.htot[CW + j] + sh.htot[j];
+        dec[j] = j < nact ? fast_exp2(tj) : 1.f;
+        if (MODE == 1 && j < nact) seg_log2 += tj;
+      }
 #pragma unroll
       for (int r = 0; r < SPT; ++r) {
         const int f = tid + r * W * 64;
@@ -652,7 +700,7 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
           if (j < nact) {
             const float4 d0 = sh.b[j][f];
             const float4 d1 = sh.a[j][f];
-            sh.a[j][f] = s;
+            if constexpr (MODE == 0) sh.a[j][f] = s;
             s = make_float4(s.x * dec[j] + (d0.x + d1.x), s.y * dec[j] + (d0.y + d1.y),
                             s.z * dec[j] + (d0.z + d1.z), s.w * dec[j] + (d0.w + d1.w));
           }
@@ -668,7 +716,7 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
     lds_barrier();  // barrier 4: exclusive states in LDS
 
     // ---------------- inter-chunk term, gate, store ----------------
-    if (active) {
+    if (MODE == 0 && active) {
       const float decay = fast_exp2(csf);
 #pragma unroll
       for (int pt = 0; pt < PT; ++pt) {
@@ -711,15 +759,111 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
     }
     cur = nxt;
   }
-  // rows past the last valid chunk (only when lengths < T)
-  constexpr int PD = 32 * PT;
-  for (int e = nvalid * kChunk * PD + threadIdx.x; e < T * PD; e += W * 64) {
-    const int tt = e / PD, p = e - tt * PD;
-    const int off = obase + tt * P.o_st + p;
-    if (P.out_f32)
-      static_cast<float*>(P.out)[off] = 0.f;
-    else
-      static_cast<uint16_t*>(P.out)[off] = 0;
+  if constexpr (MODE == 1) {
+    // the segment's contribution: state from zero and log2 decay
+#pragma unroll
+    for (int r = 0; r < SPT; ++r) {
+      const int f = threadIdx.x + r * W * 64;
+      if (f < kF4) P.seg_state[static_cast<size_t>(rec) * kF4 + f] = run[r];
+    }
+    if (threadIdx.x == 0) P.seg_decay[rec] = seg_log2;
+  } else {
+    // rows of this segment past the last valid chunk (only when lengths < T)
+    constexpr int PD = 32 * PT;
+    const int row_end = min(c_end * kChunk, T);
+    for (int e = max(c_begin, nvalid) * kChunk * PD + threadIdx.x; e < row_end * PD; e += W * 64) {
+      const int tt = e / PD, p = e - tt * PD;
+      const int off = obase + tt * P.o_st + p;
+      if (P.out_f32)
+        static_cast<float*>(P.out)[off] = 0.f;
+      else
+        static_cast<uint16_t*>(P.out)[off] = 0;
+    }
+  }
+}
+
+// Exclusive scan of the segment state records of each unit: record g's
+// contribution dS_g (state from zero, log2 decay T_g) is replaced by the state
+// entering segment g,
+//   S_0 = 0,  S_{g+1} = S_g 2^{T_g} + dS_g,
+// the composition the serial walk applies chunk by chunk. Workgroup
+// (unit, slice) takes 256 float4 of the unit's state, so the few units of a
+// long sequence still spread over many CUs.
+constexpr int kScanSlice = 256;
+
+__global__ __launch_bounds__(kScanSlice) void segment_scan_kernel(float4* state, const float* decay, int kf4, int G) {
+  constexpr int kBatch = 16;  // records loaded ahead of the serial chain
+  const int slices = kf4 / kScanSlice;
+  const int unit = blockIdx.x / slices;
+  const int f = (blockIdx.x - unit * slices) * kScanSlice + threadIdx.x;
+  float4* st = state + static_cast<size_t>(unit) * G * kf4;
+  const float* dec = decay + unit * G;
+  {
+    float4 run = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int g0 = 0; g0 < G; g0 += kBatch) {
+      float4 d[kBatch];
+      float m[kBatch];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        if (g0 + j < G) {
+          d[j] = st[static_cast<size_t>(g0 + j) * kf4 + f];
+          m[j] = fast_exp2(dec[g0 + j]);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        if (g0 + j < G) {
+          st[static_cast<size_t>(g0 + j) * kf4 + f] = run;
+          run = make_float4(run.x * m[j] + d[j].x, run.y * m[j] + d[j].y, run.z * m[j] + d[j].z,
+                            run.w * m[j] + d[j].w);
+        }
+      }
+    }
+  }
+}
+
+// Phase increments of each (unit, chunk): per rotary pair, the fp64 sum over
+// the chunk's valid rows of pi * tanh(theta) * dt, each increment formed in
+// fp32 exactly as the recurrence forms it (mamba_fused.py:102-109). Lanes of a
+// row group take consecutive pairs (one row's angles are contiguous), the
+// 256 / rpad row groups interleaved rows; LDS adds the group partials.
+__global__ __launch_bounds__(256) void chunk_phase_kernel(const MfmaParams P) {
+  __shared__ double part[256];
+  const int unit = blockIdx.x / P.NC;
+  const int chunk = blockIdx.x - unit * P.NC;
+  const int b = unit / P.H;
+  const int h = unit - b * P.H;
+  const int T = P.T;
+  int L = T;
+  if (P.lengths != nullptr) {
+    const int64_t l = P.lengths[b];
+    L = l < 0 ? 0 : (l > T ? T : static_cast<int>(l));
+  }
+  int rpad = 16;
+  while (rpad < P.R) rpad <<= 1;  // R <= 64
+  const int r = threadIdx.x & (rpad - 1);
+  const int grp = threadIdx.x / rpad;
+  const int ngrp = 256 / rpad;
+  const int t_begin = chunk * kChunk;
+  const int t_end = min(min(t_begin + kChunk, T), L);
+  const float* dtp = P.dt + b * P.d_sb + h * P.d_sh;
+  double acc = 0.0;
+  if (r < P.R) {
+    const int g0 = b * P.g_sb + h * P.g_sh + r * P.g_sr;
+#pragma unroll 4
+    for (int t = t_begin + grp; t < t_end; t += ngrp) {
+      const float th = P.angles_dtype == TF_FLOAT32 ? static_cast<const float*>(P.angles)[g0 + t * P.g_st]
+                                                    : to_f32(static_cast<const bf16_t*>(P.angles)[g0 + t * P.g_st]);
+      acc += static_cast<double>(tanh_fast(th) * kPi * dtp[t * P.d_st]);
+    }
+  }
+  part[threadIdx.x] = acc;
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    double sum = 0.0;
+    if (static_cast<int>(threadIdx.x) < P.R)
+      for (int g = 0; g < ngrp; ++g) sum += part[g * rpad + threadIdx.x];
+    P.chunk_phase[(static_cast<size_t>(unit) * P.NC + chunk) * 64 + threadIdx.x] = sum;
   }
 }
 
@@ -780,28 +924,106 @@ MfmaParams make_params(const tf_mamba_args& a) {
   P.H = static_cast<int>(a.heads);
   P.group = static_cast<int>(a.heads / a.qk_heads);
   P.R = static_cast<int>(a.rotary);
-  const int64_t units = a.batch * a.heads;
-  // Units sharing q/k rows (same batch) land on one XCD (workgroups are dealt
-  // to the 8 XCDs round-robin), so their L2 serves the shared rows.
-  P.xcd_per = (units % 8 == 0 && units >= 64) ? static_cast<int>(units / 8) : 0;
   P.out_f32 = a.out_dtype == TF_FLOAT32;
   P.trap_bf16 = a.trap_dtype == TF_BFLOAT16;
   P.angles_dtype = a.angles_dtype;
+  P.units = static_cast<int>(a.batch * a.heads);
+  P.G = 1;
+  P.SC = static_cast<int>((a.time + kChunk - 1) / kChunk);
+  P.NC = P.SC;
+  P.seg_state = nullptr;
+  P.chunk_phase = nullptr;
+  P.seg_decay = nullptr;
   return P;
+}
+
+// Chunk-parallel plan: with fewer (batch, head) units than half the CUs, each
+// unit's time axis is cut into G segments of SC chunks (whole super-chunks) so
+// about one workgroup per CU runs. The cost is a phase pre-pass over the
+// angles, a second, lighter pass over the inputs (the summary) and a tiny
+// scan; a unit walked serially by one workgroup would leave the other CUs idle.
+// Scratch layout: states [units][G][kf4] float4, chunk phase sums
+// [units][chunks][64] fp64, decays [units][G] fp32, each block 256-byte aligned.
+struct SegPlan {
+  int G = 1;
+  int SC = 0;
+  int64_t phase_off = 0, decay_off = 0, bytes = 0;
+};
+
+constexpr int64_t kTargetGroups = 256;  // one workgroup per CU (MI355X: 256 CUs)
+
+SegPlan plan_segments(const tf_mamba_args& a, int cw, int kf4) {
+  SegPlan p;
+  const int64_t units = a.batch * a.heads;
+  const int64_t chunks = (a.time + kChunk - 1) / kChunk;
+  p.SC = static_cast<int>(chunks);
+  if (units <= 0 || units > kTargetGroups / 2) return p;
+  int64_t g = kTargetGroups / units;
+  int64_t sc = (chunks + g - 1) / g;
+  sc = (sc + cw - 1) / cw * cw;
+  g = (chunks + sc - 1) / sc;
+  if (g < 2) return p;
+  p.G = static_cast<int>(g);
+  p.SC = static_cast<int>(sc);
+  const int64_t recs = units * g;
+  auto up = [](int64_t x) { return (x + 255) & ~int64_t(255); };
+  p.phase_off = up(recs * kf4 * 16);
+  p.decay_off = p.phase_off + up(units * chunks * 64 * 8);
+  p.bytes = p.decay_off + up(recs * 4);
+  return p;
+}
+
+int shape_cw(const tf_mamba_args& a) { return a.state == 128 ? 2 : 4; }
+
+template <int NT, int PT, int CW, bool WIDE>
+int launch_modes(MfmaParams P, hipStream_t stream) {
+  constexpr int kF4 = NT * PT * 256;
+  const int64_t items = static_cast<int64_t>(P.units) * P.G;
+  // Work items sharing q/k rows (same batch row and segment) are consecutive;
+  // dealing contiguous ranges to the 8 XCDs (workgroups go round-robin) keeps
+  // them on one L2.
+  P.xcd_per = (items % 8 == 0 && items >= 64) ? static_cast<int>(items / 8) : 0;
+  const dim3 grid(static_cast<uint32_t>(items)), block(CW * 128);
+  if (P.G > 1) {
+    // chunk phase sums -> segment state contributions (seeded with the phase
+    // carry) -> scan of the states -> outputs
+    hipLaunchKernelGGL(chunk_phase_kernel, dim3(static_cast<uint32_t>(P.units) * P.NC), dim3(256), 0, stream, P);
+    if (const int rc = launch_status()) return rc;
+    hipLaunchKernelGGL((mamba_mfma_kernel<NT, PT, CW, WIDE, 1>), grid, block, 0, stream, P);
+    if (const int rc = launch_status()) return rc;
+    static_assert(kF4 % kScanSlice == 0, "state slices");
+    hipLaunchKernelGGL(segment_scan_kernel, dim3(static_cast<uint32_t>(P.units) * (kF4 / kScanSlice)),
+                       dim3(kScanSlice), 0, stream,
+                       P.seg_state, P.seg_decay, kF4, P.G);
+    if (const int rc = launch_status()) return rc;
+  }
+  hipLaunchKernelGGL((mamba_mfma_kernel<NT, PT, CW, WIDE, 0>), grid, block, 0, stream, P);
+  return launch_status();
 }
 
 template <int NT, int PT, int CW>
 int launch_shape(const tf_mamba_args& a, hipStream_t stream) {
-  const int64_t units = a.batch * a.heads;
-  const dim3 grid(static_cast<uint32_t>(units)), block(CW * 128);
-  if (a.rotary > a.state / 4)
-    hipLaunchKernelGGL((mamba_mfma_kernel<NT, PT, CW, true>), grid, block, 0, stream, make_params(a));
-  else
-    hipLaunchKernelGGL((mamba_mfma_kernel<NT, PT, CW, false>), grid, block, 0, stream, make_params(a));
-  return launch_status();
+  MfmaParams P = make_params(a);
+  const SegPlan plan = plan_segments(a, CW, NT * PT * 256);
+  if (plan.G > 1 && a.workspace != nullptr && aligned(a.workspace, 256) && a.workspace_bytes >= plan.bytes) {
+    char* ws = static_cast<char*>(a.workspace);
+    P.G = plan.G;
+    P.SC = plan.SC;
+    P.seg_state = reinterpret_cast<float4*>(ws);
+    P.chunk_phase = reinterpret_cast<double*>(ws + plan.phase_off);
+    P.seg_decay = reinterpret_cast<float*>(ws + plan.decay_off);
+  }
+  if (a.rotary > a.state / 4) return launch_modes<NT, PT, CW, true>(P, stream);
+  return launch_modes<NT, PT, CW, false>(P, stream);
 }
 
 }  // namespace
+
+int64_t mfma_workspace_bytes(const tf_mamba_args& a) {
+  if (!mfma_supported(a)) return 0;
+  const SegPlan plan = plan_segments(a, shape_cw(a), static_cast<int>((a.state / 32) * (a.head_dim / 32) * 256));
+  return plan.G > 1 ? plan.bytes : 0;
+}
 
 bool mfma_supported(const tf_mamba_args& a) {
   if (a.q_dtype != TF_BFLOAT16 || a.k_dtype != TF_BFLOAT16 || a.v_dtype != TF_BFLOAT16 || a.z_dtype != TF_BFLOAT16)

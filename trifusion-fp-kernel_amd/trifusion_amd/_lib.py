@@ -63,6 +63,8 @@ class MambaArgs(ctypes.Structure):
             (name, c_i64)
             for name in ("batch", "time", "heads", "qk_heads", "state", "head_dim", "rotary")
         ],
+        ("workspace", c_ptr),
+        ("workspace_bytes", c_i64),
     ]
 
 
@@ -70,6 +72,7 @@ class MambaArgs(ctypes.Structure):
 _SIGNATURES = {
     "tf_fused_mamba": ([ctypes.POINTER(MambaArgs), c_ptr], c_i32),
     "tf_fused_mamba_variant": ([ctypes.POINTER(MambaArgs)], c_i32),
+    "tf_fused_mamba_workspace_size": ([ctypes.POINTER(MambaArgs)], c_i64),
     "tf_rmsnorm": ([c_ptr, c_i32, c_i64, c_ptr, c_ptr, c_i32, c_i64, c_i64, c_f32, c_ptr], c_i32),
     "tf_add_rmsnorm": (
         [c_ptr, c_i32, c_ptr, c_i32, c_ptr, c_ptr, c_ptr, c_i32, c_ptr, c_i32, c_i64, c_i64, c_f32, c_ptr],

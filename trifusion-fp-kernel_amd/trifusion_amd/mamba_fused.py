@@ -111,6 +111,17 @@ def launch(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths=None, vari
     kernel of the ``trifusion_amd::fused_mamba`` operator); returns ``out``."""
     lib = _lib.load()
     args = build_args(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths, variant)
+    # Long sequences over few (batch, head) units run chunk-parallel on scratch
+    # the library sizes; it comes from torch's caching allocator (the graph's
+    # private pool under capture), the C side never allocates.
+    need = lib.tf_fused_mamba_workspace_size(ctypes.byref(args))
+    if need < 0:
+        _lib.check(-need, "fused_mamba")
+    workspace = None
+    if need > 0:
+        workspace = torch.empty(need, dtype=torch.uint8, device=v.device)
+        args.workspace = workspace.data_ptr()
+        args.workspace_bytes = need
     _lib.check(lib.tf_fused_mamba(ctypes.byref(args), _lib.stream_of(v)), "fused_mamba")
     return out
 
