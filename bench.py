@@ -29,6 +29,14 @@ for _p in (ROOT, ROOT / "trifusion-fp-kernel_amd"):
 
 HBM_PEAK_GBS = 8000.0
 WORKLOAD = dict(batch=16, time=400, heads=16, head_dim=64, state=64, rotary=16, qk_heads=1)
+# other workloads are parity-test shapes; --workload times one of them instead
+WORKLOADS = {
+    "clip": ("fused_mamba clip B16 L400 H16 P64 N64 R16 Hq1", WORKLOAD, None),
+    "long": ("fused_mamba long clip B1 L7200 H16 P64 N64 R16 Hq1 (chunk-parallel)",
+             dict(WORKLOAD, batch=1, time=7200), None),
+    "varlen": ("fused_mamba varlen B32 L400 (lengths U{50..400}, seed 4) H16 P64 N64 R16 Hq1",
+               dict(WORKLOAD, batch=32), (50, 4)),
+}
 METRIC = "fused_mamba GB/s & %HBM peak; ms/forward 4s mono×16 encoder, 1 MI355X"
 TRAFFIC_FILE = ROOT / "profiles" / "fused_mamba_clip_b16_l400_pmc.txt"
 
@@ -43,6 +51,8 @@ def parse_args():
     p.add_argument("--no-encoder", action="store_true")
     p.add_argument("--encoder-only", action="store_true", help="only time the encoder forward (profiling aid)")
     p.add_argument("--variant", default="auto", choices=["auto", "mfma", "generic"])
+    p.add_argument("--workload", default="clip", choices=sorted(WORKLOADS),
+                   help="shape to time (clip: the headline B16 L400 workload)")
     p.add_argument("--eager", action="store_true", help="time Python-dispatched calls instead of graph replay")
     p.add_argument(
         "--calibrate-copy",
@@ -75,12 +85,12 @@ def traffic_bytes():
     return None
 
 
-def time_fused_mamba(args, torch, fused_mamba, dargs, steps, warmup, variant, eager):
+def time_fused_mamba(args, torch, fused_mamba, dargs, steps, warmup, variant, eager, lengths=None):
     stream = torch.cuda.current_stream()
     with torch.inference_mode():
         out = torch.empty_like(dargs[2])
         for _ in range(warmup):
-            fused_mamba(*dargs, out=out, variant=variant)
+            fused_mamba(*dargs, out=out, variant=variant, lengths=lengths)
         torch.cuda.synchronize()
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
@@ -88,7 +98,7 @@ def time_fused_mamba(args, torch, fused_mamba, dargs, steps, warmup, variant, ea
             torch.cuda.synchronize()
             start.record(stream)
             for _ in range(steps):
-                fused_mamba(*dargs, out=out, variant=variant)
+                fused_mamba(*dargs, out=out, variant=variant, lengths=lengths)
             end.record(stream)
             torch.cuda.synchronize()
             return start.elapsed_time(end) / steps
@@ -98,7 +108,7 @@ def time_fused_mamba(args, torch, fused_mamba, dargs, steps, warmup, variant, ea
         with torch.cuda.stream(side):
             with torch.cuda.graph(graph, stream=side):
                 for _ in range(steps):
-                    fused_mamba(*dargs, out=out, variant=variant)
+                    fused_mamba(*dargs, out=out, variant=variant, lengths=lengths)
         stream.wait_stream(side)
         graph.replay()  # warm replay
         torch.cuda.synchronize()
@@ -186,7 +196,7 @@ def main():
     import torch
 
     from trifusion_amd.mamba_fused import fused_mamba, selected_variant
-    from trifusion_amd.synthetic import algorithmic_bytes, clip_inputs
+    from trifusion_amd.synthetic import algorithmic_bytes, clip_inputs, clip_lengths
 
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
@@ -197,13 +207,17 @@ def main():
     if args.encoder_only:
         print(json.dumps({"encoder": encoder_ms(torch)}), flush=True)
         return
-    w = WORKLOAD
+    label, w, varlen = WORKLOADS[args.workload]
     host = clip_inputs(w["batch"], w["time"], heads=w["heads"], head_dim=w["head_dim"], state=w["state"],
                        rotary=w["rotary"], qk_heads=w["qk_heads"], seed=1)
     dargs = tuple(x.cuda() for x in host)
-    nbytes = algorithmic_bytes(host)
+    lengths = None
+    if varlen is not None:
+        lengths = clip_lengths(w["batch"], w["time"], varlen[0], seed=varlen[1]).cuda()
+    nbytes = algorithmic_bytes(host, lengths=None if lengths is None else lengths.cpu())
     kernel = selected_variant(*dargs, variant=args.variant)
-    ms = time_fused_mamba(args, torch, fused_mamba, dargs, args.steps, args.warmup, args.variant, args.eager)
+    ms = time_fused_mamba(args, torch, fused_mamba, dargs, args.steps, args.warmup, args.variant, args.eager,
+                          lengths)
     gbs = nbytes / (ms * 1e-3) / 1e9
     line = {
         "metric": METRIC,
@@ -219,7 +233,7 @@ def main():
         "dtype": "bf16",
         "data": "synthetic (seeded clip_inputs: x,B,C,z ~ N(0,1); dt = softplus(N(0,1)-2); A = -exp(U(0, ln16)))",
         "config": {
-            "workload": "fused_mamba clip B16 L400 H16 P64 N64 R16 Hq1",
+            "workload": label,
             "kernel": kernel,
             "timing": "eager calls" if args.eager else f"HIP graph of {args.steps} calls, HIP events on the launch stream",
             "algorithmic_bytes_per_call": nbytes,
@@ -231,7 +245,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gbs / HBM_PEAK_GBS, 4),
-            "traffic": traffic_bytes(),
+            "traffic": traffic_bytes() if args.workload == "clip" else None,
         },
     }
     if not args.no_encoder:
@@ -239,7 +253,7 @@ def main():
             line["encoder"] = encoder_ms(torch)
         except ImportError as err:  # encoder not built yet
             line["encoder"] = {"error": str(err)}
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and args.workload == "clip":  # the baseline times the clip workload
         line["cpu_baseline"] = cpu_baseline(torch, args.cpu_seconds)
     print(json.dumps(line), flush=True)
 
