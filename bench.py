@@ -49,6 +49,9 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline time budget")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-encoder", action="store_true")
+    p.add_argument("--no-kernels", action="store_true", help="skip the bandwidth-kernel lines")
+    p.add_argument("--kernels-only", action="store_true",
+                   help="only time the bandwidth kernels at the encoder shapes (profiling aid)")
     p.add_argument("--encoder-only", action="store_true", help="only time the encoder forward (profiling aid)")
     p.add_argument("--variant", default="auto", choices=["auto", "mfma", "generic"])
     p.add_argument("--workload", default="clip", choices=sorted(WORKLOADS),
@@ -155,6 +158,77 @@ def cpu_baseline(torch, budget_s):
     }
 
 
+def graph_us(torch, fn, steps=100):
+    """Average µs of ``fn()`` over a replayed graph of ``steps`` calls (HIP events)."""
+    stream = torch.cuda.current_stream()
+    with torch.inference_mode():
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        side = torch.cuda.Stream()
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            with torch.cuda.graph(graph, stream=side):
+                for _ in range(steps):
+                    fn()
+        stream.wait_stream(side)
+        graph.replay()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        graph.replay()
+        end.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) * 1e3 / steps
+
+
+def bandwidth_kernels(torch):
+    """Each single-pass kernel of the encoder at its 4 s mono x 16 shape (16 x 400
+    frames, dim 512, in-proj width 2240, FFN 2 x 1365): algorithmic bytes (each
+    input element read once, each output written once) / time vs 8 TB/s."""
+    from trifusion_amd.kernels import rms, swiglu
+    from trifusion_amd.kernels.buffers import mamba_controls, mask_buffer
+    from trifusion_amd.kernels.native import add, add_rms
+    from trifusion_amd.masking import masked_mean, time_mask
+
+    g = torch.Generator(device="cuda").manual_seed(5)
+    b, t, dim, proj, ffn, heads, n = 16, 400, 512, 2240, 1365, 16, 64
+    rows = b * t
+    x = torch.randn(b, t, dim, device="cuda", generator=g)
+    br = torch.randn(b, t, dim, device="cuda", generator=g).bfloat16()
+    w = torch.ones(dim, device="cuda")
+    p = torch.randn(b, t, proj, device="cuda", generator=g).bfloat16()
+    cview = p[..., 2 * 1024 + n: 2 * 1024 + 2 * n].reshape(b, t, 1, n)  # C columns of the in-proj output
+    a_cols = p[..., 2 * 1024 + 2 * n + heads: 2 * 1024 + 2 * n + 2 * heads]
+    d_cols = p[..., 2 * 1024 + 2 * n: 2 * 1024 + 2 * n + heads]
+    gu = torch.randn(b, t, 2 * ffn, device="cuda", generator=g).bfloat16()
+    lengths = torch.full((b,), t, dtype=torch.int64, device="cuda")
+    mask = time_mask(lengths, t)
+    bias = torch.zeros(heads, device="cuda")
+    wn = torch.ones(n, device="cuda")
+    cases = [
+        ("rms fp32->bf16 [6400,512]", lambda: rms(x, w, out_dtype=torch.bfloat16), rows * dim * (4 + 2)),
+        ("add_rms fp32+bf16 -> fp32,bf16 [6400,512]", lambda: add_rms(x, br, w, mask),
+         rows * dim * (4 + 2 + 4 + 2) + rows),
+        ("rms bf16 strided C/B columns [6400,64]", lambda: rms(cview, wn), rows * n * (2 + 2)),
+        ("swiglu bf16 [6400,2730] -> [6400,1365]", lambda: swiglu(gu), rows * 3 * ffn * 2),
+        ("mamba_controls bf16 [16,400,16] x2 -> fp32 [16,16,400] x2", lambda: mamba_controls(a_cols, d_cols, bias, 1e-4),
+         rows * heads * (2 + 2 + 4 + 4)),
+        ("masked_mean fp32 [16,400,512] -> [16,512]", lambda: masked_mean(x, lengths), rows * dim * 4 + b * dim * 4),
+        ("mask_rows fp32 [6400,512]", lambda: mask_buffer(x, mask), rows * dim * 8 + rows),
+        ("add fp32+bf16 -> fp32 [6400,512]", lambda: add(x, br, mask), rows * dim * (4 + 2 + 4) + rows),
+    ]
+    out = []
+    for name, fn, nbytes in cases:
+        us = graph_us(torch, fn)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out.append({"kernel": name, "us": round(us, 2), "bytes": nbytes, "GB/s": round(gbs, 1),
+                    "frac": round(gbs / HBM_PEAK_GBS, 4)})
+    return out
+
+
 def encoder_ms(torch):
     from trifusion_amd.runtime import InferenceEngine
     from trifusion_amd.model import Encoder, ModelConfig
@@ -207,6 +281,9 @@ def main():
     if args.encoder_only:
         print(json.dumps({"encoder": encoder_ms(torch)}), flush=True)
         return
+    if args.kernels_only:
+        print(json.dumps({"bandwidth_kernels": bandwidth_kernels(torch)}), flush=True)
+        return
     label, w, varlen = WORKLOADS[args.workload]
     host = clip_inputs(w["batch"], w["time"], heads=w["heads"], head_dim=w["head_dim"], state=w["state"],
                        rotary=w["rotary"], qk_heads=w["qk_heads"], seed=1)
@@ -248,6 +325,8 @@ def main():
             "traffic": traffic_bytes() if args.workload == "clip" else None,
         },
     }
+    if not args.no_kernels and args.workload == "clip":
+        line["bandwidth_kernels"] = bandwidth_kernels(torch)
     if not args.no_encoder:
         try:
             line["encoder"] = encoder_ms(torch)

@@ -10,6 +10,94 @@ namespace {
 
 constexpr int kRowsPerBlock = 4;  // one wave64 per row
 
+// Eight consecutive elements through 16-byte accesses (two for fp32): a wave
+// moves 1-2 KB per load instruction instead of 128-256 B, which is what keeps
+// enough bytes in flight to approach the HBM roofline.
+template <typename T>
+__device__ __forceinline__ void load8(const T* p, float (&v)[8]) {
+  if constexpr (sizeof(T) == 4) {
+    const float4 a = reinterpret_cast<const float4*>(p)[0];
+    const float4 b = reinterpret_cast<const float4*>(p)[1];
+    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w;
+    v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+  } else {
+    const uint4 u = *reinterpret_cast<const uint4*>(p);
+    const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[2 * e] = to_f32(__builtin_bit_cast(T, static_cast<uint16_t>(wd[e] & 0xffffu)));
+      v[2 * e + 1] = to_f32(__builtin_bit_cast(T, static_cast<uint16_t>(wd[e] >> 16)));
+    }
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void store8(T* p, const float (&v)[8]) {
+  if constexpr (sizeof(T) == 4) {
+    reinterpret_cast<float4*>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
+    reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
+  } else {
+    uint32_t wd[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t lo = __builtin_bit_cast(uint16_t, from_f32<T>(v[2 * e]));
+      const uint32_t hi = __builtin_bit_cast(uint16_t, from_f32<T>(v[2 * e + 1]));
+      wd[e] = lo | (hi << 16);
+    }
+    *reinterpret_cast<uint4*>(p) = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+  }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// RMSNorm rows through 8-element vectors: one wave per row, lane holds
+// elements 8*(lane + 64*j) .. +7, j < PER8 (512*PER8 >= d, d % 8 == 0).
+template <typename TX, typename TB, typename TS, typename TY, int PER8, bool ADD>
+__global__ __launch_bounds__(256) void row_norm_vec_kernel(const TX* __restrict__ x, int64_t x_stride,
+                                                           const TB* __restrict__ bsrc,
+                                                           const uint8_t* __restrict__ mask,
+                                                           const float* __restrict__ w, TS* __restrict__ s,
+                                                           TY* __restrict__ y, int64_t rows, int d, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const bool keep = !ADD || mask == nullptr || mask[row] != 0;
+  float v[PER8][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < PER8; ++j) {
+    const int i0 = 8 * (lane + 64 * j);
+    if (i0 < d) {
+      load8(x + row * x_stride + i0, v[j]);
+      if constexpr (ADD) {
+        float bv[8];
+        load8(bsrc + row * d + i0, bv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[j][e] = keep ? to_f32(from_f32<TS>(v[j][e] + bv[e])) : 0.f;
+        store8(s + row * d + i0, v[j]);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[j][e] = 0.f;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += v[j][e] * v[j][e];
+  }
+  ss = wave_sum(ss);
+  const float r = rsqrtf(ss / static_cast<float>(d) + eps);
+#pragma unroll
+  for (int j = 0; j < PER8; ++j) {
+    const int i0 = 8 * (lane + 64 * j);
+    if (i0 < d) {
+      float wv[8], o[8];
+      load8(w + i0, wv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = v[j][e] * r * wv[e];
+      store8(y + row * d + i0, o);
+    }
+  }
+}
+
 // One wave per row; lane holds elements lane + 64*j, j < PER (64*PER >= d).
 template <typename TX, typename TB, typename TS, typename TY, int PER, bool ADD>
 __global__ __launch_bounds__(256) void row_norm_kernel(const TX* __restrict__ x, int64_t x_stride,
@@ -52,6 +140,33 @@ template <typename TX, typename TB, typename TS, typename TY, bool ADD>
 int launch_row_norm(const void* x, int64_t x_stride, const void* bsrc, const uint8_t* mask,
                     const float* w, void* s, void* y, int64_t rows, int d, float eps,
                     hipStream_t stream) {
+  // 8-element vectors pay off once a row fills at least half a wave of them
+  const bool vec = d >= 256 && d % 8 == 0 && x_stride % 8 == 0 && aligned16(x) && aligned16(w) &&
+                   aligned16(y) && (!ADD || (aligned16(bsrc) && aligned16(s)));
+  if (vec) {
+    int per8 = 1;
+    while (per8 * 512 < d) per8 <<= 1;
+    const dim3 grid(static_cast<uint32_t>((rows + kRowsPerBlock - 1) / kRowsPerBlock));
+    const dim3 block(64 * kRowsPerBlock);
+    const TX* xp = static_cast<const TX*>(x);
+    const TB* bp = static_cast<const TB*>(bsrc);
+    TS* sp = static_cast<TS*>(s);
+    TY* yp = static_cast<TY*>(y);
+#define TF_NORM_VEC_CASE(P)                                                                       \
+  case P:                                                                                          \
+    hipLaunchKernelGGL((row_norm_vec_kernel<TX, TB, TS, TY, P, ADD>), grid, block, 0, stream, xp, \
+                       x_stride, bp, mask, w, sp, yp, rows, d, eps);                               \
+    return launch_status();
+    switch (per8) {
+      TF_NORM_VEC_CASE(1)
+      TF_NORM_VEC_CASE(2)
+      TF_NORM_VEC_CASE(4)
+      TF_NORM_VEC_CASE(8)
+      default:
+        break;
+    }
+#undef TF_NORM_VEC_CASE
+  }
   int per = 1;
   while (per * 64 < d) per <<= 1;
   const dim3 grid(static_cast<uint32_t>((rows + kRowsPerBlock - 1) / kRowsPerBlock));
@@ -80,7 +195,8 @@ int launch_row_norm(const void* x, int64_t x_stride, const void* bsrc, const uin
   return launch_status();
 }
 
-// SwiGLU over [rows, 2d] -> [rows, d]; one block per row.
+// SwiGLU over [rows, 2d] -> [rows, d]; one block per row (element loads: the
+// encoder's d = 1365 leaves rows at every 2-byte alignment).
 template <typename T>
 __global__ __launch_bounds__(256) void swiglu_kernel(const T* __restrict__ x, T* __restrict__ y,
                                                      int64_t d) {
@@ -94,6 +210,23 @@ __global__ __launch_bounds__(256) void swiglu_kernel(const T* __restrict__ x, T*
   }
 }
 
+// SwiGLU with d % 8 == 0 and aligned rows: 8 outputs per thread, grid-stride
+// (vector counts fit int32: the launcher checks).
+template <typename T>
+__global__ __launch_bounds__(256) void swiglu_vec_kernel(const T* __restrict__ x, T* __restrict__ y, int d8,
+                                                         int n8) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += gridDim.x * blockDim.x) {
+    const int row = i / d8, c = i - row * d8;
+    const int64_t g0 = (static_cast<int64_t>(row) * 2 * d8 + c) * 8;
+    float g[8], u[8], o[8];
+    load8(x + g0, g);
+    load8(x + g0 + static_cast<int64_t>(d8) * 8, u);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = g[e] * sigmoidf(g[e]) * u[e];
+    store8(y + static_cast<int64_t>(i) * 8, o);
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void mask_rows_kernel(const T* __restrict__ x, T* __restrict__ y,
                                                         const uint8_t* __restrict__ mask, int64_t d) {
@@ -101,6 +234,23 @@ __global__ __launch_bounds__(256) void mask_rows_kernel(const T* __restrict__ x,
   const bool keep = mask[row] != 0;
   for (int64_t j = threadIdx.x; j < d; j += blockDim.x)
     y[row * d + j] = keep ? x[row * d + j] : from_f32<T>(0.f);
+}
+
+// Row mask through 8-element vectors (d % 8 == 0, aligned): grid-stride over
+// vector indices that fit int32 (the launcher checks), 32-bit row division.
+template <typename T>
+__global__ __launch_bounds__(256) void mask_rows_vec_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                                            const uint8_t* __restrict__ mask, int d8, int n8) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += gridDim.x * blockDim.x) {
+    const int64_t e0 = static_cast<int64_t>(i) * 8;
+    float v[8];
+    load8(x + e0, v);
+    if (mask[i / d8] == 0) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = 0.f;
+    }
+    store8(y + e0, v);
+  }
 }
 
 template <typename TA, typename TB, typename TY>
@@ -113,6 +263,38 @@ __global__ __launch_bounds__(256) void add_kernel(const TA* __restrict__ a, cons
     const int64_t i = row * d + j;
     y[i] = from_f32<TY>(keep ? to_f32(a[i]) + to_f32(b[i]) : 0.f);
   }
+}
+
+template <typename TA, typename TB, typename TY>
+__global__ __launch_bounds__(256) void add_vec_kernel(const TA* __restrict__ a, const TB* __restrict__ b,
+                                                      const uint8_t* __restrict__ mask, TY* __restrict__ y,
+                                                      int d8, int n8) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n8; i += gridDim.x * blockDim.x) {
+    const int64_t e0 = static_cast<int64_t>(i) * 8;
+    float av[8], bv[8];
+    load8(a + e0, av);
+    load8(b + e0, bv);
+    const bool keep = mask == nullptr || mask[i / d8] != 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) av[e] = keep ? av[e] + bv[e] : 0.f;
+    store8(y + e0, av);
+  }
+}
+
+// Grid of a grid-stride vector kernel: enough 256-thread blocks to cover n8
+// vectors, capped so large tensors loop instead of launching millions of blocks.
+uint32_t vec_blocks(int64_t n8) {
+  const int64_t blocks = (n8 + 255) / 256;
+  return static_cast<uint32_t>(blocks < 16384 ? blocks : 16384);
+}
+
+// Vector path preconditions shared by the flat kernels: whole 8-element
+// vectors per row, 16-byte aligned pointers, vector indices within int32.
+bool flat_vec_ok(int64_t rows, int64_t d, std::initializer_list<const void*> ptrs) {
+  if (d % 8 != 0 || rows * (d / 8) > 0x7fffffff - 65536) return false;
+  for (const void* p : ptrs)
+    if (!aligned16(p)) return false;
+  return true;
 }
 
 // Output index i runs over [B, H, T] with t fastest (coalesced fp32 writes).
@@ -159,6 +341,53 @@ __global__ __launch_bounds__(256) void masked_mean_kernel(const T* __restrict__ 
   if (w == 0 && col < d)
     y[b * d + col] = (part[0][lane] + part[1][lane] + part[2][lane] + part[3][lane]) /
                      static_cast<float>(len);
+}
+
+// Masked mean with 4-column vectors (d % 4 == 0, aligned): block = 16 waves
+// over (batch b, 256 columns), wave w sums frames t = w (mod 16) with four
+// rows' loads in flight; LDS adds the 16 partials in wave order.
+template <typename T>
+__global__ __launch_bounds__(1024) void masked_mean_vec_kernel(const T* __restrict__ x,
+                                                               const int64_t* __restrict__ lengths,
+                                                               float* __restrict__ y, int64_t time, int64_t d) {
+  __shared__ float4 part[16][64];
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int64_t b = blockIdx.y;
+  const int64_t col = (static_cast<int64_t>(blockIdx.x) * 64 + lane) * 4;
+  const int64_t len = lengths[b];
+  const int64_t L = len < 0 ? 0 : (len > time ? time : len);
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (col < d) {
+    const T* base = x + b * time * d + col;
+#pragma unroll 4
+    for (int64_t t = w; t < L; t += 16) {
+      float v[4];
+      if constexpr (sizeof(T) == 4) {
+        const float4 f = *reinterpret_cast<const float4*>(base + t * d);
+        v[0] = f.x, v[1] = f.y, v[2] = f.z, v[3] = f.w;
+      } else {
+        const uint2 u = *reinterpret_cast<const uint2*>(base + t * d);
+        v[0] = to_f32(__builtin_bit_cast(T, static_cast<uint16_t>(u.x & 0xffffu)));
+        v[1] = to_f32(__builtin_bit_cast(T, static_cast<uint16_t>(u.x >> 16)));
+        v[2] = to_f32(__builtin_bit_cast(T, static_cast<uint16_t>(u.y & 0xffffu)));
+        v[3] = to_f32(__builtin_bit_cast(T, static_cast<uint16_t>(u.y >> 16)));
+      }
+      acc.x += v[0], acc.y += v[1], acc.z += v[2], acc.w += v[3];
+    }
+  }
+  part[w][lane] = acc;
+  __syncthreads();
+  if (w == 0 && col < d) {
+    float4 s = part[0][lane];
+#pragma unroll
+    for (int k = 1; k < 16; ++k) {
+      const float4 p = part[k][lane];
+      s.x += p.x, s.y += p.y, s.z += p.z, s.w += p.w;
+    }
+    const float n = static_cast<float>(len);
+    *reinterpret_cast<float4*>(y + b * d + col) = make_float4(s.x / n, s.y / n, s.z / n, s.w / n);
+  }
 }
 
 __global__ __launch_bounds__(256) void time_mask_kernel(const int64_t* __restrict__ lengths,
@@ -222,10 +451,17 @@ extern "C" int tf_swiglu(const void* x, void* y, int32_t dtype, int64_t rows, in
   if (rows < 0 || d < 1 || rows > 0x7fffffff) return TF_ERR_SHAPE;
   if (rows == 0) return TF_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool vec = tf::flat_vec_ok(rows, d, {x, y});  // whole output vectors; input rows follow
+  const int64_t n8 = rows * d / 8;
   TF_DISPATCH(dtype, T,
-              hipLaunchKernelGGL(tf::swiglu_kernel<T>, dim3(static_cast<uint32_t>(rows)), dim3(256), 0,
-                                 s, static_cast<const T*>(x), static_cast<T*>(y), d);
-              return tf::launch_status());
+              if (vec) {
+                hipLaunchKernelGGL(tf::swiglu_vec_kernel<T>, dim3(tf::vec_blocks(n8)), dim3(256), 0, s,
+                                   static_cast<const T*>(x), static_cast<T*>(y), static_cast<int>(d / 8),
+                                   static_cast<int>(n8));
+              } else {
+                hipLaunchKernelGGL(tf::swiglu_kernel<T>, dim3(static_cast<uint32_t>(rows)), dim3(256), 0, s,
+                                   static_cast<const T*>(x), static_cast<T*>(y), d);
+              } return tf::launch_status());
   return TF_ERR_DTYPE;
 }
 
@@ -235,10 +471,17 @@ extern "C" int tf_mask_rows(const void* x, void* y, int32_t dtype, const uint8_t
   if (rows < 0 || d < 1 || rows > 0x7fffffff) return TF_ERR_SHAPE;
   if (rows == 0) return TF_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool vec = tf::flat_vec_ok(rows, d, {x, y});
+  const int64_t n8 = rows * d / 8;
   TF_DISPATCH(dtype, T,
-              hipLaunchKernelGGL(tf::mask_rows_kernel<T>, dim3(static_cast<uint32_t>(rows)), dim3(256), 0,
-                                 s, static_cast<const T*>(x), static_cast<T*>(y), mask, d);
-              return tf::launch_status());
+              if (vec) {
+                hipLaunchKernelGGL(tf::mask_rows_vec_kernel<T>, dim3(tf::vec_blocks(n8)), dim3(256), 0, s,
+                                   static_cast<const T*>(x), static_cast<T*>(y), mask, static_cast<int>(d / 8),
+                                   static_cast<int>(n8));
+              } else {
+                hipLaunchKernelGGL(tf::mask_rows_kernel<T>, dim3(static_cast<uint32_t>(rows)), dim3(256), 0, s,
+                                   static_cast<const T*>(x), static_cast<T*>(y), mask, d);
+              } return tf::launch_status());
   return TF_ERR_DTYPE;
 }
 
@@ -249,15 +492,22 @@ extern "C" int tf_add(const void* a, int32_t a_dtype, const void* b, int32_t b_d
   if (rows < 0 || d < 1 || rows > 0x7fffffff) return TF_ERR_SHAPE;
   if (rows == 0) return TF_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool vec = tf::flat_vec_ok(rows, d, {a, b, y});
+  const int64_t n8 = rows * d / 8;
   TF_DISPATCH(
       a_dtype, TA,
       TF_DISPATCH(b_dtype, TB,
                   TF_DISPATCH(y_dtype, TY,
-                              hipLaunchKernelGGL((tf::add_kernel<TA, TB, TY>),
-                                                 dim3(static_cast<uint32_t>(rows)), dim3(256), 0, s,
-                                                 static_cast<const TA*>(a), static_cast<const TB*>(b),
-                                                 mask, static_cast<TY*>(y), d);
-                              return tf::launch_status())));
+                              if (vec) {
+                                hipLaunchKernelGGL((tf::add_vec_kernel<TA, TB, TY>), dim3(tf::vec_blocks(n8)),
+                                                   dim3(256), 0, s, static_cast<const TA*>(a),
+                                                   static_cast<const TB*>(b), mask, static_cast<TY*>(y),
+                                                   static_cast<int>(d / 8), static_cast<int>(n8));
+                              } else {
+                                hipLaunchKernelGGL((tf::add_kernel<TA, TB, TY>), dim3(static_cast<uint32_t>(rows)),
+                                                   dim3(256), 0, s, static_cast<const TA*>(a),
+                                                   static_cast<const TB*>(b), mask, static_cast<TY*>(y), d);
+                              } return tf::launch_status())));
   return TF_ERR_DTYPE;
 }
 
@@ -283,11 +533,17 @@ extern "C" int tf_masked_mean(const void* x, int32_t dtype, const int64_t* lengt
   if (batch < 0 || time < 0 || d < 1 || batch > 65535) return TF_ERR_SHAPE;
   if (batch == 0) return TF_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid(tf::blocks_for(d, 64), static_cast<uint32_t>(batch));
+  const bool vec = d % 4 == 0 && tf::aligned16(x) && tf::aligned16(y);
   TF_DISPATCH(dtype, T,
-              hipLaunchKernelGGL(tf::masked_mean_kernel<T>, grid, dim3(256), 0, s, static_cast<const T*>(x),
-                                 lengths, y, time, d);
-              return tf::launch_status());
+              if (vec) {
+                const dim3 grid(tf::blocks_for(d, 256), static_cast<uint32_t>(batch));
+                hipLaunchKernelGGL(tf::masked_mean_vec_kernel<T>, grid, dim3(1024), 0, s,
+                                   static_cast<const T*>(x), lengths, y, time, d);
+              } else {
+                const dim3 grid(tf::blocks_for(d, 64), static_cast<uint32_t>(batch));
+                hipLaunchKernelGGL(tf::masked_mean_kernel<T>, grid, dim3(256), 0, s, static_cast<const T*>(x),
+                                   lengths, y, time, d);
+              } return tf::launch_status());
   return TF_ERR_DTYPE;
 }
 
