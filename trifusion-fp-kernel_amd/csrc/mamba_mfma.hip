@@ -245,25 +245,31 @@ __device__ __forceinline__ void score_tile(const f32x16& acc, float cst, const f
   }
 }
 
-// Global inputs of one wave's 32 rows: row t of the lane in MFMA row form
-// (q, k, v and the controls), and for the phase lane rows first .. first+RPL-1
-// of its rotary pair (column offset gcol). Rows past L read a valid row; their
-// dt is 0, so they reach neither the outputs nor the state.
-template <int KS, int PS, int RPL>
-struct HalfIn {
+// Global inputs of one wave's 32 rows, in two parts loaded at different
+// times. Rows past L read a valid row; their dt is 0, so they reach neither the
+// outputs nor the state.
+//   HalfRows: row t of the lane in MFMA row form (q for the output pass, k, v),
+//     loaded at the start of the super-chunk that uses them (first needed after
+//     the controls and phase pass 1, which cover their latency);
+//   HalfCtl: the controls of row t and, for the phase lane, the raw angles of
+//     rows first .. first+RPL-1 of its rotary pair (column offset gcol),
+//     prefetched one super-chunk ahead (needed first thing).
+template <int KS, int PS>
+struct HalfRows {
   u32x4 q[KS], k[KS], v[PS];
+};
+
+template <int RPL>
+struct HalfCtl {
   float th[RPL];
   float dt, dn, adt, tr, tn;
 };
 
-template <bool WITH_Q, int KS, int PS, int RPL>
-__device__ __forceinline__ void load_half(const MfmaParams& P, HalfIn<KS, PS, RPL>& in, const uint16_t* qbase,
-                                          const uint16_t* kbase, const uint16_t* vbase, const float* dtb,
-                                          const float* adtb, int trb, int gcol, int t0, int t, int first, int L,
+template <bool WITH_Q, int KS, int PS>
+__device__ __forceinline__ void load_rows(const MfmaParams& P, HalfRows<KS, PS>& in, const uint16_t* qbase,
+                                          const uint16_t* kbase, const uint16_t* vbase, int t0, int t, int L,
                                           int hh) {
-  const bool valid = t < L;
-  const bool next = t + 1 < P.T;
-  const int tl = valid ? t : t0;
+  const int tl = t < L ? t : t0;
   const uint16_t* q_row = qbase + tl * P.q_st;
   const uint16_t* k_row = kbase + tl * P.k_st;
   const uint16_t* v_row = vbase + tl * P.v_st;
@@ -274,6 +280,13 @@ __device__ __forceinline__ void load_half(const MfmaParams& P, HalfIn<KS, PS, RP
   }
 #pragma unroll
   for (int s = 0; s < PS; ++s) in.v[s] = load_row8(v_row, kidx(s, hh, 0));
+}
+
+template <int RPL>
+__device__ __forceinline__ void load_ctl(const MfmaParams& P, HalfCtl<RPL>& in, const float* dtb, const float* adtb,
+                                         int trb, int gcol, int t, int first, int L) {
+  const bool valid = t < L;
+  const bool next = t + 1 < P.T;
   in.dt = valid ? dtb[t * P.d_st] : 0.f;
   in.dn = next ? dtb[(t + 1) * P.d_st] : 0.f;
   in.adt = valid ? adtb[t * P.a_st] : 0.f;
@@ -387,16 +400,15 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
   const u32x4 ident0 = identity_rows(0, (threadIdx.x >> 5) & 1, threadIdx.x & 31);
   const u32x4 ident1 = identity_rows(1, (threadIdx.x >> 5) & 1, threadIdx.x & 31);
 
-  // inputs of the first super-chunk; later ones are prefetched one super-chunk
-  // ahead, while the state scan and the output phase run
-  using In = HalfIn<KS, PS, RPL>;
-  In cur = {};
+  // controls and angles of the first super-chunk; later ones are prefetched one
+  // super-chunk ahead, while the state scan and the output phase run
+  using Ctl = HalfCtl<RPL>;
+  Ctl cur = {};
   if (c_begin + cw < c_stop) {
     const int ln = threadIdx.x & 63;
     const int p0 = ln & (RP - 1);
     const int r0 = (c_begin + cw) * kChunk + 32 * hf;
-    load_half<MODE == 0>(P, cur, qbase, kbase, vbase, dtb, adtb, trb, gbase + (p0 < R ? p0 : 0) * P.g_sr,
-                         (c_begin + cw) * kChunk, r0 + (ln & 31), r0 + (ln / RP) * RPL, L, ln >> 5);
+    load_ctl(P, cur, dtb, adtb, trb, gbase + (p0 < R ? p0 : 0) * P.g_sr, r0 + (ln & 31), r0 + (ln / RP) * RPL, L);
   }
 
   lds_barrier();
@@ -422,9 +434,14 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
     // Values carried from one "if (active)" region to a later one are given a
     // definition on the idle path too: left undefined there, the compiler
     // carries them around the loop and holds their registers through every phase.
-    u32x4 (&q)[KS] = cur.q;
-    u32x4 (&k)[KS] = cur.k;
-    u32x4 (&v)[PS] = cur.v;
+    // Row loads are issued at two points: half 0 here, half 1 after its phase
+    // pass 1. Load issue stalls while the chip-wide burst drains; staggered, one
+    // wave of each SIMD computes while the other waits.
+    HalfRows<KS, PS> rows = {};
+    if (active && hf == 0) load_rows<MODE == 0>(P, rows, qbase, kbase, vbase, t0, t, L, hh);
+    u32x4 (&q)[KS] = rows.q;
+    u32x4 (&k)[KS] = rows.k;
+    u32x4 (&v)[PS] = rows.v;
     float (&th)[RPL] = cur.th;
     const float dtv = cur.dt;
     float csr = 0.f, gam = 0.f, scl = 0.f;
@@ -455,6 +472,7 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
       double sum = seg_part;
       for (int off = RP; off < 64; off <<= 1) sum += __shfl_xor(sum, off);
       if (seg == 0 && pair_on) sh.wsum[sub][pp] = sum;
+      if (hf == 1) load_rows<MODE == 0>(P, rows, qbase, kbase, vbase, t0, t, L, hh);
     }
     lds_barrier();  // barrier 1: half sums of decay and phase visible
 
@@ -673,12 +691,12 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
         for (int s = 0; s < PS; ++s) zrow[s] = u32x4{0u, 0u, 0u, 0u};
       }
     }
-    // inputs of the same half of the next super-chunk
-    In nxt = {};
+    // controls and angles of the same half of the next super-chunk
+    Ctl nxt = {};
     if (g0 + CW + cw < c_stop) {
       const int tn = (g0 + CW + cw) * kChunk;
-      load_half<MODE == 0>(P, nxt, qbase, kbase, vbase, dtb, adtb, trb, gbase + (pair_on ? pp : 0) * P.g_sr, tn,
-                           tn + 32 * hf + c32, tn + 32 * hf + seg * RPL, L, hh);
+      load_ctl(P, nxt, dtb, adtb, trb, gbase + (pair_on ? pp : 0) * P.g_sr, tn + 32 * hf + c32,
+               tn + 32 * hf + seg * RPL, L);
     }
 
     // ---------------- state scan over the CW chunks ----------------
