@@ -44,6 +44,9 @@ class ModelConfig:
     init_std: float = 0.02
 
 
+FFN_ALIGN = 32  # FFN width the GEMMs and SwiGLU run at (each half zero-padded up to it)
+
+
 class EncoderBlock(nn.Module):
     def __init__(self, c):
         super().__init__()
@@ -52,9 +55,35 @@ class EncoderBlock(nn.Module):
         self.ff_norm = RMSNorm(c.dim, c.norm_eps)
         self.gate_up = nn.Linear(c.dim, 2 * c.ffn_dim, bias=False)
         self.down = nn.Linear(c.ffn_dim, c.dim, bias=False)
+        self._padded = None
+        self._padded_key = None
+
+    def _padded_ffn(self):
+        """gate_up and down with each FFN half zero-padded to a multiple of
+        FFN_ALIGN. An odd width (1365) leaves every GEMM output row and every
+        down-projection input row misaligned, which the library GEMMs and the
+        SwiGLU kernel run at a fraction of their rate; the padded rows give
+        silu(0) * 0 = 0 and meet zero columns of down, so the result is the same
+        up to the GEMMs' summation order. Rebuilt when either weight changes."""
+        w1, w2 = self.gate_up.weight, self.down.weight
+        key = (w1.data_ptr(), w1._version, w2.data_ptr(), w2._version, w1.dtype, w1.device)
+        if self._padded_key != key:
+            f, d = self.down.in_features, self.down.out_features
+            fp = -(-f // FFN_ALIGN) * FFN_ALIGN
+            with torch.no_grad():
+                g1 = w1.new_zeros(2 * fp, d)
+                g1[:f] = w1[:f]
+                g1[fp : fp + f] = w1[f:]
+                g2 = w2.new_zeros(d, fp)
+                g2[:, :f] = w2
+            self._padded, self._padded_key = (g1, g2), key
+        return self._padded
 
     def ffn(self, h):
-        return self.down(swiglu(self.gate_up(h)))
+        if self.down.in_features % FFN_ALIGN == 0:
+            return self.down(swiglu(self.gate_up(h)))
+        g1, g2 = self._padded_ffn()
+        return F.linear(swiglu(F.linear(h, g1)), g2)
 
 
 class Encoder(nn.Module):
