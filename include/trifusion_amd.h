@@ -63,6 +63,23 @@ typedef enum tf_mamba_variant {
  *                 chunk-parallel: the time axis is cut into segments that run
  *                 on separate workgroups, joined by a scan of their states.
  *                 Otherwise each unit is walked by one workgroup.
+ *   dt_bias       [H] fp32 or NULL (extension). Non-NULL selects raw controls:
+ *                 adt and dt then point at the raw `a` and `ddt` columns of
+ *                 the in-projection (fp32 or bf16, both of one dtype, any
+ *                 [B, H, T] strides), and each step's controls are computed in
+ *                 the recurrence as mamba_controls computes them
+ *                 (src/trifusion_l4/kernels/primitives.py:190-216):
+ *                   dt  = softplus(ddt + dt_bias[h])   (linear above 20)
+ *                   adt = min(-(relu(a) + 1/(1 - min(a, 0))), -a_floor) * dt
+ *                 so no [B, H, T] control tensors are written or read.
+ *   a_floor       decay floor of the raw controls (the reference uses 1e-4).
+ *   reverse       1 (extension): each batch row runs over its valid prefix
+ *                 (L = lengths[b], or T) in reverse. Step t < L reads row
+ *                 L-1-t of every time-indexed operand and writes row L-1-t of
+ *                 out; rows t >= L are written as 0. The result equals the
+ *                 reference's reverse_valid(fused_mamba(reverse_valid(...)))
+ *                 of the backward direction (src/trifusion_l4/model.py:174-179,
+ *                 kernels/__init__.py:44-55) with no reversed copies.
  * Stride arrays follow the dimension order above.
  */
 typedef struct tf_mamba_args {
@@ -79,6 +96,9 @@ typedef struct tf_mamba_args {
   int64_t batch, time, heads, qk_heads, state, head_dim, rotary;
   void *workspace;
   int64_t workspace_bytes;
+  const float *dt_bias;
+  float a_floor;
+  int32_t reverse;
 } tf_mamba_args;
 
 /*
@@ -175,6 +195,25 @@ int tf_masked_mean(const void *x, int32_t dtype, const int64_t *lengths, float *
  * time_mask (src/trifusion_l4/masking.py:6-7) on the device. */
 int tf_time_mask(const int64_t *lengths, uint8_t *mask, int64_t batch, int64_t time,
                  void *stream);
+
+/*
+ * Valid-prefix reversal: for x, y contiguous [B, T, D],
+ *   y[b, t, :] = x[b, L-1-t, :] for t < L = clamp(lengths[b], 0, T), else 0.
+ * Replaces reverse_valid/_reverse (src/trifusion_l4/kernels/__init__.py:44-55,
+ * kernels/primitives.py:40-47). x and y must not overlap.
+ */
+int tf_reverse_valid(const void *x, void *y, int32_t dtype, const int64_t *lengths,
+                     int64_t batch, int64_t time, int64_t d, void *stream);
+
+/*
+ * Mean of the two directions fused with RMSNorm:
+ *   s = (a + b) * 0.5 (fp32),  y = s * rsqrt(mean(s^2) + eps) * w  (fp32 out)
+ * over contiguous [rows, d], d <= 4096. Replaces mean_norm (`_norm` MODE 2,
+ * src/trifusion_l4/kernels/native.py:8-39,77-78).
+ */
+int tf_mean_rmsnorm(const void *a, int32_t a_dtype, const void *b, int32_t b_dtype,
+                    const float *w, float *y, int64_t rows, int64_t d, float eps,
+                    void *stream);
 
 /* Library version string (static storage). */
 const char *tf_version(void);

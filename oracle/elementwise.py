@@ -8,7 +8,9 @@ Pinning (tests/test_oracle_elementwise.py): ``rms_norm`` against
 independently split tensor; ``mamba_controls`` against ``F.softplus`` (same
 threshold 20) and hand-evaluated special cases of the decay control;
 ``masked_mean`` against a Python loop over valid frames; ``mask_rows`` and
-``add`` against explicit ``torch.where`` forms.
+``add`` against explicit ``torch.where`` forms; ``reverse_valid`` against a
+Python loop, ``torch.flip`` at full length and its own square (the masked
+identity); ``mean_norm`` against ``F.rms_norm`` of the mean and the a == b case.
 """
 
 import torch
@@ -74,3 +76,30 @@ def masked_mean(x, lengths):
     """Masked mean over time, ``sum_t x*mask / length`` in fp32 (``decoder.py:60-62``)."""
     mask = time_mask(lengths, x.shape[1])
     return (x.float() * mask[..., None]).sum(1) / lengths[:, None]
+
+
+def reverse_valid(x, lengths):
+    """Reverse the valid prefix of each row of ``x`` ``[B, T, D]``:
+    ``y[b, t] = x[b, L_b - 1 - t]`` for ``t < L_b``, else 0, with ``L_b`` the
+    length clamped to ``[0, T]``.
+
+    Reference: ``src/trifusion_l4/kernels/__init__.py:44-55`` (its gather form)
+    and the ``_reverse`` kernel ``src/trifusion_l4/kernels/primitives.py:40-47``.
+    """
+    b, t, d = x.shape
+    n = lengths.clamp(0, t)
+    pos = torch.arange(t, device=x.device)[None, :]
+    src = (n[:, None] - 1 - pos).clamp_min(0)
+    y = torch.gather(x, 1, src[..., None].expand(b, t, d))
+    return y.masked_fill((pos >= n[:, None])[..., None], 0)
+
+
+def mean_norm(a, b, weight, eps=1e-5):
+    """RMSNorm of the mean of two directions, fp32 math and output:
+    ``s = (a + b) / 2``, ``y = s * rsqrt(mean(s^2) + eps) * w``.
+
+    Reference: ``_norm`` MODE 2 ``src/trifusion_l4/kernels/native.py:8-39``
+    (``x = (x + a) * 0.5``, fp32 output ``:46``) through ``mean_norm`` ``:77-78``.
+    """
+    s = (a.float() + b.float()) * 0.5
+    return s * torch.rsqrt(s.square().mean(-1, keepdim=True) + eps) * weight.float()

@@ -7,7 +7,10 @@ inputs and outputs under autocast (the reference runs its forward under
 ``torch.autocast("cuda", bfloat16)``, ``src/trifusion_l4/runtime.py:79-82``), the
 B/C norms (output dtype = input dtype, ``src/trifusion_l4/kernels/native.py:46``),
 SwiGLU and the recurrence output. The residual stream, norms' statistics and the
-pooled embedding stay fp32. Parity target: sigmoid probabilities within 1e-2.
+pooled embedding stay fp32. With ``cfg.bidirectional`` each block also runs the
+backward direction the reference's way, on explicitly reversed valid prefixes
+(``src/trifusion_l4/model.py:174-184``). Parity target: sigmoid probabilities
+within 1e-2.
 """
 
 import torch
@@ -76,6 +79,12 @@ def encoder_forward(sd, cfg, audio, lengths, channels):
         pre = f"blocks.{i}."
         h = _bf(E.rms_norm(x, sd[pre + "pre.weight"], cfg.norm_eps))
         m = mamba_block(sd, pre + "mamba.", cfg, h, frames)
+        if getattr(cfg, "bidirectional", False):
+            # the reference's backward direction on the reversed valid prefix
+            # and the RMSNorm of the two directions' mean (model.py:174-184)
+            hb = E.reverse_valid(h, frames)
+            mb = E.reverse_valid(mamba_block(sd, pre + "mamba_bwd.", cfg, hb, frames), frames)
+            m = E.mean_norm(m, mb, sd[pre + "mn.weight"], cfg.norm_eps)
         x = E.add(x, m, mask)
         h = _bf(E.rms_norm(x, sd[pre + "ff_norm.weight"], cfg.norm_eps))
         g = _linear(h, sd[pre + "gate_up.weight"])

@@ -18,12 +18,17 @@ Three independent formulations of the same recurrence:
 ``fused_mamba_f64``
     Unchunked FP64 step loop, generalising the reference's independent check
     ``tests/test_recurrence.py:50-86`` to any B, T, H, Hq, N, P and R.
+``fused_mamba_reversed``
+    The backward direction of the reference's bidirectional block: the
+    chunked form over explicitly reversed valid prefixes
+    (``src/trifusion_l4/model.py:174-179``).
 ``fused_mamba_attention_f64``
     Quadratic closed form ``y = silu(z) * ((L o (qr kr^T)) v + (D + delta) v)``
     with ``L[t,u] = exp(sum_{m=u+1..t} adt_m)`` for ``u < t``: no recurrence at
     all, so it pins the loop (and through it the chunked form).
 
-Pinning (tests/test_oracle_recurrence.py): chunked(fp32) == f64 loop to 1e-5,
+Pinning (tests/test_oracle_recurrence.py): reversed == per-row truncate, flip,
+chunked, flip back (exact), chunked(fp32) == f64 loop to 1e-5,
 f64 loop == attention form to 1e-10, T=1 closed form, causal linear attention
 special case, chunk-size independence, causality, phase against an FP64
 cumulative sum, and planted mistakes that each check must catch.
@@ -167,6 +172,34 @@ def fused_mamba_chunked(
     if lengths is not None:
         valid = torch.arange(t)[None, :] < lengths.cpu()[:, None]
         out = out * valid[:, :, None, None]
+    return out if out_dtype is None else out.to(out_dtype)
+
+
+def fused_mamba_reversed(q, k, v, adt, dt, trap, qb, kb, angles, d, z, lengths=None, out_dtype=None):
+    """Backward direction of the reference's bidirectional block
+    (``src/trifusion_l4/model.py:174-179``): every time-indexed operand has its
+    valid prefix reversed (``reverse_valid``, ``kernels/__init__.py:44-55``), the
+    recurrence runs, and its output is reversed back, so row ``t < L`` holds the
+    output of step ``L-1-t`` and rows past ``L`` are 0. ``lengths`` ``None``
+    reverses the whole sequence.
+    """
+    from .elementwise import reverse_valid
+
+    bsz, t = v.shape[:2]
+    n = torch.full((bsz,), t, dtype=torch.int64) if lengths is None else lengths.cpu().clamp(0, t)
+
+    def rev_t(x):  # [B, T, ...]
+        shape = x.shape
+        return reverse_valid(x.reshape(shape[0], shape[1], -1), n).reshape(shape)
+
+    def rev_ht(x):  # [B, H, T]
+        return reverse_valid(x.transpose(1, 2), n).transpose(1, 2)
+
+    y = fused_mamba_chunked(
+        rev_t(q), rev_t(k), rev_t(v), rev_ht(adt), rev_ht(dt), rev_ht(trap), qb, kb, rev_t(angles), d, rev_t(z),
+        lengths=n,
+    )
+    out = rev_t(y)
     return out if out_dtype is None else out.to(out_dtype)
 
 

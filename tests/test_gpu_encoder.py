@@ -96,3 +96,40 @@ def test_load_student_round_trip(tmp_path):
     portable = runtime.load_student(path, optimized=False)
     c = runtime.InferenceEngine(portable).eager(audio, lengths, channels)
     assert (c.sigmoid() - a.sigmoid()).abs().max().item() <= PROB_TOL
+
+
+def make_bidirectional(depth=2, seed=5):
+    torch.manual_seed(seed)
+    model = Encoder(ModelConfig(depth=depth, bidirectional=True)).eval().requires_grad_(False)
+    runtime.prepare_static_weights(model)
+    return model.to(DEV)
+
+
+def test_bidirectional_encoder_matches_oracle():
+    """Backward direction via the recurrence's reverse flag vs the oracle's
+    explicitly reversed valid prefixes (reference model.py:174-184)."""
+    model = make_bidirectional()
+    audio = clip_audio(4, 48000, seed=7, channels=2)
+    lengths = torch.tensor([48000, 20000, 7000, 31999])
+    channels = torch.tensor([2, 1, 2, 1])
+    eng = runtime.InferenceEngine(model)
+    logits = eng.eager(audio.to(DEV), lengths.to(DEV), channels.to(DEV)).cpu()
+    ref = encoder_forward(model.state_dict(), model.config, audio, lengths, channels)
+    diff = (logits.sigmoid() - ref.sigmoid()).abs().max().item()
+    print(f"bidirectional prob max diff {diff:.2e}", flush=True)
+    assert torch.isfinite(logits).all() and diff <= PROB_TOL
+
+
+def test_bidirectional_graph_replay_equals_eager():
+    model = make_bidirectional(seed=6)
+    audio = clip_audio(3, 32000, seed=8).to(DEV)
+    lengths = torch.tensor([32000, 15000, 800], device=DEV)
+    channels = torch.ones(3, dtype=torch.int64, device=DEV)
+    eng = runtime.InferenceEngine(model, graphs=True)
+    eager = eng.eager(audio, lengths, channels).clone()
+    for _ in range(3):
+        graph = eng(audio, lengths, channels)
+        torch.cuda.synchronize()
+        assert torch.equal(graph, eager)
+        eng.eager(audio, lengths, channels)
+    assert eng.graph_hits >= 2

@@ -59,6 +59,7 @@ def test_reference_shapes(variant, batch, time, heads):
     ref = fused_mamba_chunked(*args)
     y = run(args, variant)
     assert torch.isfinite(y).all()
+    print(f"  max_rel={max_rel(y, ref):.3e}", flush=True)
     assert max_rel(y, ref) <= MAX_REL
     yb = run(args, variant, out_dtype=torch.bfloat16)
     refb = ref.to(torch.bfloat16)

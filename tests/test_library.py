@@ -37,8 +37,9 @@ def test_library_exports_every_declared_symbol():
 def test_struct_layout_matches_header():
     from trifusion_amd._lib import MambaArgs
 
-    # 13 pointers, 10 int32, 33 int64 strides, 7 int64 dims, workspace pointer + bytes
-    assert ctypes.sizeof(MambaArgs) == 13 * 8 + 10 * 4 + 33 * 8 + 7 * 8 + 8 + 8
+    # 13 pointers, 10 int32, 33 int64 strides, 7 int64 dims, workspace pointer + bytes,
+    # dt_bias pointer, a_floor float, reverse int32
+    assert ctypes.sizeof(MambaArgs) == 13 * 8 + 10 * 4 + 33 * 8 + 7 * 8 + 8 + 8 + 8 + 4 + 4
     text = HEADER.read_text()
     body = text[text.index("typedef struct tf_mamba_args") : text.index("} tf_mamba_args;")]
     names_in_header = re.findall(r"\*?(\w+)(?:\[\d\])?[,;]", body)

@@ -67,3 +67,39 @@ def test_masked_mean_matches_loop():
         n = int(lengths[b])
         expect = sum(x[b, t].float() for t in range(n)) / n
         assert torch.allclose(y[b], expect, atol=1e-6)
+
+
+def _reverse_loop(x, lengths):
+    b, t, _ = x.shape
+    y = torch.zeros_like(x)
+    for i in range(b):
+        n = max(0, min(int(lengths[i]), t))
+        for s in range(n):
+            y[i, s] = x[i, n - 1 - s]
+    return y
+
+
+def test_reverse_valid_matches_loop_flip_and_squares_to_mask():
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(5, 9, 3, generator=g)
+    lengths = torch.tensor([9, 4, 0, 1, 12])  # full, ragged, empty, single, past T
+    y = E.reverse_valid(x, lengths)
+    assert torch.equal(y, _reverse_loop(x, lengths))
+    assert torch.equal(y[0], torch.flip(x[0], (0,)))
+    assert torch.equal(y[4], torch.flip(x[4], (0,)))
+    assert not y[2].any() and torch.equal(y[3, 0], x[3, 0]) and not y[3, 1:].any()
+    mask = E.time_mask(lengths.clamp(0, 9), 9)
+    assert torch.equal(E.reverse_valid(y, lengths), E.mask_rows(x, mask))
+
+
+def test_mean_norm_matches_rms_norm_of_the_mean():
+    g = torch.Generator().manual_seed(8)
+    a = torch.randn(11, 512, generator=g)
+    b = torch.randn(11, 512, generator=g)
+    w = torch.rand(512, generator=g) + 0.5
+    expect = F.rms_norm((a + b) / 2, (512,), w, eps=1e-5)
+    assert torch.allclose(E.mean_norm(a, b, w), expect, rtol=1e-5, atol=1e-6)
+    assert torch.allclose(E.mean_norm(a, a, w), F.rms_norm(a, (512,), w, eps=1e-5), rtol=1e-5, atol=1e-6)
+    ab = a.to(torch.bfloat16)
+    assert E.mean_norm(ab, ab, w).dtype == torch.float32
+    assert not E.mean_norm(torch.zeros(2, 512), torch.zeros(2, 512), w).any()

@@ -163,6 +163,55 @@ def test_lengths_mask_rows_only():
         assert torch.all(masked[b, n:] == 0)
 
 
+def _flip_t(args):
+    q, k, v, adt, dt, trap, qb, kb, angles, d, z = args
+
+    def f(x):
+        return torch.flip(x, (1,))
+
+    def g(x):
+        return torch.flip(x, (2,))
+
+    return (f(q), f(k), f(v), g(adt), g(dt), g(trap), qb, kb, f(angles), d, f(z))
+
+
+def _truncate(args, b, n):
+    q, k, v, adt, dt, trap, qb, kb, angles, d, z = args
+
+    def s(x):
+        return x[b : b + 1, :n]
+
+    def u(x):
+        return x[b : b + 1, :, :n]
+
+    return (s(q), s(k), s(v), u(adt), u(dt), u(trap), qb, kb, s(angles), d, s(z))
+
+
+def test_reversed_is_per_row_flip_of_the_valid_prefix():
+    """The gather-based reversed oracle against its definition taken another way:
+    each row cut to its length, flipped with torch.flip, run, flipped back."""
+    args = clip_inputs(3, 150, heads=2, head_dim=32, state=16, dtype=torch.float32, seed=13)
+    lengths = torch.tensor([150, 77, 1])
+    out = R.fused_mamba_reversed(*args, lengths=lengths)
+    for b, n in enumerate(lengths.tolist()):
+        ref = torch.flip(R.fused_mamba_chunked(*_flip_t(_truncate(args, b, n))), (1,))
+        assert R.max_rel(out[b : b + 1, :n], ref) <= 1e-5
+        assert not out[b, n:].any()
+    full = R.fused_mamba_reversed(*args)
+    assert R.max_rel(full, torch.flip(R.fused_mamba_chunked(*_flip_t(args)), (1,))) <= 1e-5
+
+
+def test_planted_off_by_one_reversal_is_caught():
+    """A reversal that starts one row early (x[L - t] instead of x[L-1-t])
+    fails the per-row flip check."""
+    args = clip_inputs(2, 90, heads=2, head_dim=32, state=16, dtype=torch.float32, seed=14)
+    lengths = torch.tensor([90, 41])
+    out = R.fused_mamba_reversed(*args, lengths=lengths - 1)  # planted: one row short
+    b, n = 1, 41
+    ref = torch.flip(R.fused_mamba_chunked(*_flip_t(_truncate(args, b, n))), (1,))
+    assert R.max_rel(out[b : b + 1, :n], ref) > 1e-3
+
+
 # --- planted mistakes: each variant must be caught by the checks above -------
 
 

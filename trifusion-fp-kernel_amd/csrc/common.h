@@ -57,6 +57,21 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 
 __device__ __forceinline__ float sigmoidf(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
+// Mamba-3 discretisation controls of one step from the raw in-projection
+// columns (src/trifusion_l4/kernels/primitives.py:209-214): the step
+// dt = softplus(ddt + bias), linear above 20, and the signed decay
+// adt = min(-(relu(a) + 1/(1 - min(a, 0))), -floor) * dt. Shared by the
+// controls kernel and the recurrence's raw-controls prologue, so both give
+// the same bits.
+__device__ __forceinline__ float control_step(float ddt, float bias) {
+  const float v = ddt + bias;
+  return v > 20.f ? v : log1pf(expf(v));
+}
+
+__device__ __forceinline__ float control_decay(float a, float step, float floor_) {
+  return fminf(-(fmaxf(a, 0.f) + 1.f / (1.f - fminf(a, 0.f))), -floor_) * step;
+}
+
 // x - 2pi*floor(x/2pi), the reduction the reference applies to phases.
 __device__ __forceinline__ float mod_two_pi(float x) {
   return x - kTwoPi * floorf(x / kTwoPi);

@@ -1,6 +1,7 @@
 // Single-pass bandwidth kernels around the recurrence: RMSNorm (optionally
-// fused with the residual add that precedes it), SwiGLU, row masking, masked
-// add, the Mamba-3 controls and masked mean-pooling. Reductions are wave64
+// fused with the residual add that precedes it, or with the mean of the two
+// directions of a bidirectional block), SwiGLU, row masking, masked add, the
+// Mamba-3 controls, masked mean-pooling and valid-prefix reversal. Reductions are wave64
 // shuffles; every kernel reads each input element once and writes each output
 // element once.
 #include "common.h"
@@ -9,6 +10,10 @@ namespace tf {
 namespace {
 
 constexpr int kRowsPerBlock = 4;  // one wave64 per row
+
+// What the row norms normalise: x itself; the masked sum s = (x + b) * mask,
+// stored as it is normalised; or the mean of two directions (x + b) / 2.
+enum NormOp { kNormPlain = 0, kNormAdd = 1, kNormMean = 2 };
 
 // Eight consecutive elements through 16-byte accesses (two for fp32): a wave
 // moves 1-2 KB per load instruction instead of 128-256 B, which is what keeps
@@ -52,7 +57,7 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 
 // RMSNorm rows through 8-element vectors: one wave per row, lane holds
 // elements 8*(lane + 64*j) .. +7, j < PER8 (512*PER8 >= d, d % 8 == 0).
-template <typename TX, typename TB, typename TS, typename TY, int PER8, bool ADD>
+template <typename TX, typename TB, typename TS, typename TY, int PER8, int OP>
 __global__ __launch_bounds__(256) void row_norm_vec_kernel(const TX* __restrict__ x, int64_t x_stride,
                                                            const TB* __restrict__ bsrc,
                                                            const uint8_t* __restrict__ mask,
@@ -61,7 +66,7 @@ __global__ __launch_bounds__(256) void row_norm_vec_kernel(const TX* __restrict_
   const int lane = threadIdx.x & 63;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const bool keep = !ADD || mask == nullptr || mask[row] != 0;
+  const bool keep = OP != kNormAdd || mask == nullptr || mask[row] != 0;
   float v[PER8][8];
   float ss = 0.f;
 #pragma unroll
@@ -69,12 +74,17 @@ __global__ __launch_bounds__(256) void row_norm_vec_kernel(const TX* __restrict_
     const int i0 = 8 * (lane + 64 * j);
     if (i0 < d) {
       load8(x + row * x_stride + i0, v[j]);
-      if constexpr (ADD) {
+      if constexpr (OP != kNormPlain) {
         float bv[8];
         load8(bsrc + row * d + i0, bv);
+        if constexpr (OP == kNormAdd) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[j][e] = keep ? to_f32(from_f32<TS>(v[j][e] + bv[e])) : 0.f;
-        store8(s + row * d + i0, v[j]);
+          for (int e = 0; e < 8; ++e) v[j][e] = keep ? to_f32(from_f32<TS>(v[j][e] + bv[e])) : 0.f;
+          store8(s + row * d + i0, v[j]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[j][e] = (v[j][e] + bv[e]) * 0.5f;
+        }
       }
     } else {
 #pragma unroll
@@ -99,7 +109,7 @@ __global__ __launch_bounds__(256) void row_norm_vec_kernel(const TX* __restrict_
 }
 
 // One wave per row; lane holds elements lane + 64*j, j < PER (64*PER >= d).
-template <typename TX, typename TB, typename TS, typename TY, int PER, bool ADD>
+template <typename TX, typename TB, typename TS, typename TY, int PER, int OP>
 __global__ __launch_bounds__(256) void row_norm_kernel(const TX* __restrict__ x, int64_t x_stride,
                                                        const TB* __restrict__ bsrc,
                                                        const uint8_t* __restrict__ mask,
@@ -108,7 +118,7 @@ __global__ __launch_bounds__(256) void row_norm_kernel(const TX* __restrict__ x,
   const int lane = threadIdx.x & 63;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const bool keep = !ADD || mask == nullptr || mask[row] != 0;
+  const bool keep = OP != kNormAdd || mask == nullptr || mask[row] != 0;
   float v[PER];
   float ss = 0.f;
 #pragma unroll
@@ -117,11 +127,13 @@ __global__ __launch_bounds__(256) void row_norm_kernel(const TX* __restrict__ x,
     float val = 0.f;
     if (i < d) {
       val = to_f32(x[row * x_stride + i]);
-      if constexpr (ADD) {
+      if constexpr (OP == kNormAdd) {
         val = keep ? val + to_f32(bsrc[row * d + i]) : 0.f;
         const TS stored = from_f32<TS>(val);
         s[row * d + i] = stored;
         val = to_f32(stored);
+      } else if constexpr (OP == kNormMean) {
+        val = (val + to_f32(bsrc[row * d + i])) * 0.5f;
       }
     }
     v[j] = val;
@@ -136,13 +148,13 @@ __global__ __launch_bounds__(256) void row_norm_kernel(const TX* __restrict__ x,
   }
 }
 
-template <typename TX, typename TB, typename TS, typename TY, bool ADD>
+template <typename TX, typename TB, typename TS, typename TY, int OP>
 int launch_row_norm(const void* x, int64_t x_stride, const void* bsrc, const uint8_t* mask,
                     const float* w, void* s, void* y, int64_t rows, int d, float eps,
                     hipStream_t stream) {
   // 8-element vectors pay off once a row fills at least half a wave of them
   const bool vec = d >= 256 && d % 8 == 0 && x_stride % 8 == 0 && aligned16(x) && aligned16(w) &&
-                   aligned16(y) && (!ADD || (aligned16(bsrc) && aligned16(s)));
+                   aligned16(y) && (OP == kNormPlain || aligned16(bsrc)) && (OP != kNormAdd || aligned16(s));
   if (vec) {
     int per8 = 1;
     while (per8 * 512 < d) per8 <<= 1;
@@ -154,7 +166,7 @@ int launch_row_norm(const void* x, int64_t x_stride, const void* bsrc, const uin
     TY* yp = static_cast<TY*>(y);
 #define TF_NORM_VEC_CASE(P)                                                                       \
   case P:                                                                                          \
-    hipLaunchKernelGGL((row_norm_vec_kernel<TX, TB, TS, TY, P, ADD>), grid, block, 0, stream, xp, \
+    hipLaunchKernelGGL((row_norm_vec_kernel<TX, TB, TS, TY, P, OP>), grid, block, 0, stream, xp,  \
                        x_stride, bp, mask, w, sp, yp, rows, d, eps);                               \
     return launch_status();
     switch (per8) {
@@ -177,7 +189,7 @@ int launch_row_norm(const void* x, int64_t x_stride, const void* bsrc, const uin
   TY* yp = static_cast<TY*>(y);
 #define TF_NORM_CASE(P)                                                                          \
   case P:                                                                                         \
-    hipLaunchKernelGGL((row_norm_kernel<TX, TB, TS, TY, P, ADD>), grid, block, 0, stream, xp,    \
+    hipLaunchKernelGGL((row_norm_kernel<TX, TB, TS, TY, P, OP>), grid, block, 0, stream, xp,     \
                        x_stride, bp, mask, w, sp, yp, rows, d, eps);                              \
     break;
   switch (per) {
@@ -312,12 +324,9 @@ __global__ __launch_bounds__(256) void controls_kernel(const T* __restrict__ a, 
   const int64_t h = bh % heads;
   const int64_t b = bh / heads;
   const int64_t src = b * sb + t * st + h;
-  const float av = to_f32(a[src]);
-  const float v = to_f32(ddt[src]) + bias[h];
-  const float control = fminf(-(fmaxf(av, 0.f) + 1.f / (1.f - fminf(av, 0.f))), -floor_);
-  const float step = v > 20.f ? v : log1pf(expf(v));
+  const float step = control_step(to_f32(ddt[src]), bias[h]);
   dt[i] = step;
-  adt[i] = control * step;
+  adt[i] = control_decay(to_f32(a[src]), step, floor_);
 }
 
 // Block = 4 waves over (batch b, 64 columns); wave w sums frames t = w (mod 4).
@@ -398,6 +407,28 @@ __global__ __launch_bounds__(256) void time_mask_kernel(const int64_t* __restric
   mask[i] = (i % time) < lengths[i / time] ? 1 : 0;
 }
 
+// Valid-prefix reversal, one wave per (b, t) row moving U-sized units:
+// y[b, t] = x[b, L-1-t] for t < L, else 0 (primitives.py:40-47).
+template <typename U>
+__global__ __launch_bounds__(256) void reverse_valid_kernel(const U* __restrict__ x, U* __restrict__ y,
+                                                            const int64_t* __restrict__ lengths, int time,
+                                                            int units, int rows) {
+  const int lane = threadIdx.x & 63;
+  const int row = static_cast<int>(blockIdx.x) * kRowsPerBlock + static_cast<int>(threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int b = row / time;
+  const int t = row - b * time;
+  const int64_t l = lengths[b];
+  const int L = l < 0 ? 0 : (l > time ? time : static_cast<int>(l));
+  U* dst = y + static_cast<int64_t>(row) * units;
+  if (t < L) {
+    const U* src = x + (static_cast<int64_t>(b) * time + (L - 1 - t)) * units;
+    for (int c = lane; c < units; c += 64) dst[c] = src[c];
+  } else {
+    for (int c = lane; c < units; c += 64) dst[c] = U{};
+  }
+}
+
 uint32_t blocks_for(int64_t n, int per_block) {
   return static_cast<uint32_t>((n + per_block - 1) / per_block);
 }
@@ -418,7 +449,7 @@ extern "C" int tf_rmsnorm(const void* x, int32_t x_dtype, int64_t x_row_stride, 
   hipStream_t s = static_cast<hipStream_t>(stream);
   TF_DISPATCH(x_dtype, TX,
               TF_DISPATCH(y_dtype, TY,
-                          return (tf::launch_row_norm<TX, float, float, TY, false>(
+                          return (tf::launch_row_norm<TX, float, float, TY, tf::kNormPlain>(
                               x, x_row_stride, nullptr, nullptr, w, nullptr, y, rows,
                               static_cast<int>(d), eps, s))));
   return TF_ERR_DTYPE;
@@ -435,13 +466,13 @@ extern "C" int tf_add_rmsnorm(const void* a, int32_t a_dtype, const void* b, int
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int di = static_cast<int>(d);
   if (b_dtype == TF_FLOAT32 && y_dtype == TF_FLOAT32)
-    return tf::launch_row_norm<float, float, float, float, true>(a, d, b, mask, w, s, y, rows, di, eps, st);
+    return tf::launch_row_norm<float, float, float, float, tf::kNormAdd>(a, d, b, mask, w, s, y, rows, di, eps, st);
   if (b_dtype == TF_FLOAT32 && y_dtype == TF_BFLOAT16)
-    return tf::launch_row_norm<float, float, float, bf16_t, true>(a, d, b, mask, w, s, y, rows, di, eps, st);
+    return tf::launch_row_norm<float, float, float, bf16_t, tf::kNormAdd>(a, d, b, mask, w, s, y, rows, di, eps, st);
   if (b_dtype == TF_BFLOAT16 && y_dtype == TF_FLOAT32)
-    return tf::launch_row_norm<float, bf16_t, float, float, true>(a, d, b, mask, w, s, y, rows, di, eps, st);
+    return tf::launch_row_norm<float, bf16_t, float, float, tf::kNormAdd>(a, d, b, mask, w, s, y, rows, di, eps, st);
   if (b_dtype == TF_BFLOAT16 && y_dtype == TF_BFLOAT16)
-    return tf::launch_row_norm<float, bf16_t, float, bf16_t, true>(a, d, b, mask, w, s, y, rows, di, eps, st);
+    return tf::launch_row_norm<float, bf16_t, float, bf16_t, tf::kNormAdd>(a, d, b, mask, w, s, y, rows, di, eps, st);
   return TF_ERR_DTYPE;
 }
 
@@ -556,4 +587,41 @@ extern "C" int tf_time_mask(const int64_t* lengths, uint8_t* mask, int64_t batch
   hipLaunchKernelGGL(tf::time_mask_kernel, dim3(tf::blocks_for(total, 256)), dim3(256), 0,
                      static_cast<hipStream_t>(stream), lengths, mask, time, total);
   return tf::launch_status();
+}
+
+extern "C" int tf_reverse_valid(const void* x, void* y, int32_t dtype, const int64_t* lengths, int64_t batch,
+                                int64_t time, int64_t d, void* stream) {
+  if (!x || !y || !lengths) return TF_ERR_NULL;
+  if (!tf::dtype_ok(dtype)) return TF_ERR_DTYPE;
+  if (batch < 0 || time < 0 || d < 1 || batch * time > 0x7fffffff - 64) return TF_ERR_SHAPE;
+  const int rows = static_cast<int>(batch * time);
+  if (rows == 0) return TF_OK;
+  const int64_t bytes = d * tf::dtype_size(dtype);  // bytes per row
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(tf::blocks_for(rows, tf::kRowsPerBlock)), block(64 * tf::kRowsPerBlock);
+  const int t = static_cast<int>(time);
+  if (bytes % 16 == 0 && tf::aligned16(x) && tf::aligned16(y)) {
+    hipLaunchKernelGGL(tf::reverse_valid_kernel<uint4>, grid, block, 0, s, static_cast<const uint4*>(x),
+                       static_cast<uint4*>(y), lengths, t, static_cast<int>(bytes / 16), rows);
+  } else if (bytes % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 4 == 0 && reinterpret_cast<uintptr_t>(y) % 4 == 0) {
+    hipLaunchKernelGGL(tf::reverse_valid_kernel<uint32_t>, grid, block, 0, s, static_cast<const uint32_t*>(x),
+                       static_cast<uint32_t*>(y), lengths, t, static_cast<int>(bytes / 4), rows);
+  } else {
+    hipLaunchKernelGGL(tf::reverse_valid_kernel<uint16_t>, grid, block, 0, s, static_cast<const uint16_t*>(x),
+                       static_cast<uint16_t*>(y), lengths, t, static_cast<int>(bytes / 2), rows);
+  }
+  return tf::launch_status();
+}
+
+extern "C" int tf_mean_rmsnorm(const void* a, int32_t a_dtype, const void* b, int32_t b_dtype, const float* w,
+                               float* y, int64_t rows, int64_t d, float eps, void* stream) {
+  if (!a || !b || !w || !y) return TF_ERR_NULL;
+  if (rows < 0 || d < 1 || d > 4096) return TF_ERR_SHAPE;
+  if (rows == 0) return TF_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  TF_DISPATCH(a_dtype, TA,
+              TF_DISPATCH(b_dtype, TB,
+                          return (tf::launch_row_norm<TA, TB, float, float, tf::kNormMean>(
+                              a, d, b, nullptr, w, nullptr, y, rows, static_cast<int>(d), eps, s))));
+  return TF_ERR_DTYPE;
 }

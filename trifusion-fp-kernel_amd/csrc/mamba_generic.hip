@@ -8,13 +8,24 @@
 // dtype (:143), the decayed score -> v dtype (:146) and the decay-scaled v ->
 // k dtype (:151-152). It is the kernel for shapes and dtypes the MFMA path does
 // not take (fp32 operands, odd sizes) and an independent second implementation
-// the MFMA kernel is tested against.
+// the MFMA kernel is tested against. Raw controls and the reversed walk follow
+// the MFMA kernel's definitions (computed per step; row L-1-t for step t).
 #include "mamba_internal.h"
+
+// Every product and sum is rounded on its own, as the elementwise reference
+// formulation rounds it: a multiply-add fused here or not, depending on how
+// the compiler happens to schedule the surrounding code, moves the inputs of
+// the bf16 rounding points by an ulp and flips rounded q/k elements.
+#pragma clang fp contract(off)
 
 namespace tf {
 namespace {
 
 constexpr int kThreads = 256;
+
+// sigmoid with the correctly rounded-to-1-ulp expf rather than the fast
+// hardware exp: the trapezoid weights feed the bf16 rounding of kr.
+__device__ __forceinline__ float sigmoid_exact(float x) { return 1.0f / (1.0f + expf(-x)); }
 constexpr int kNMax = 128;
 constexpr int kPMax = 64;
 constexpr int kStatePerThread = kNMax * kPMax / kThreads;
@@ -43,6 +54,12 @@ __global__ __launch_bounds__(kThreads) void mamba_generic_kernel(const tf_mamba_
   const int T = static_cast<int>(a.time);
   const int qh = h / static_cast<int>(a.heads / a.qk_heads);
   const int L = valid_length(a, b);
+  // reverse: step t < L reads and writes row L-1-t; steps >= L have no row
+  const bool rev = a.reverse != 0;
+  const int tlim = rev ? L : T;
+  auto row = [&](int t) -> int64_t { return rev ? L - 1 - t : t; };
+  const bool raw = a.dt_bias != nullptr;
+  const float step_bias = raw ? a.dt_bias[h] : 0.f;
 
   const int64_t qo = b * a.q_stride[0] + qh * a.q_stride[2];
   const int64_t ko = b * a.k_stride[0] + qh * a.k_stride[2];
@@ -67,15 +84,21 @@ __global__ __launch_bounds__(kThreads) void mamba_generic_kernel(const tf_mamba_
     if (tid < kChunk) {
       const int t = t0 + tid;
       const bool valid = t < L;
-      const bool next = t + 1 < T;
-      const float dt = valid ? load_f32(a.dt, a.dt_dtype, dto + t * a.dt_stride[2]) : 0.f;
-      const float dn = next ? load_f32(a.dt, a.dt_dtype, dto + (t + 1) * a.dt_stride[2]) : 0.f;
+      const bool next = t + 1 < tlim;
+      float dt = valid ? load_f32(a.dt, a.dt_dtype, dto + row(t) * a.dt_stride[2]) : 0.f;
+      float dn = next ? load_f32(a.dt, a.dt_dtype, dto + row(t + 1) * a.dt_stride[2]) : 0.f;
+      float ad = valid ? load_f32(a.adt, a.adt_dtype, ao + row(t) * a.adt_stride[2]) : 0.f;
+      if (raw) {  // controls from the raw a/ddt columns (primitives.py:209-214)
+        dt = valid ? control_step(dt, step_bias) : 0.f;
+        dn = next ? control_step(dn, step_bias) : 0.f;
+        ad = valid ? control_decay(ad, dt, a.a_floor) : 0.f;
+      }
       const float tr =
-          sigmoidf(valid ? load_f32(a.trap, a.trap_dtype, tro + t * a.trap_stride[2]) : 0.f);
+          sigmoid_exact(valid ? load_f32(a.trap, a.trap_dtype, tro + row(t) * a.trap_stride[2]) : 0.f);
       const float tn =
-          sigmoidf(next ? load_f32(a.trap, a.trap_dtype, tro + (t + 1) * a.trap_stride[2]) : 0.f);
+          sigmoid_exact(next ? load_f32(a.trap, a.trap_dtype, tro + row(t + 1) * a.trap_stride[2]) : 0.f);
       const float gamma = dt * tr;
-      const float da = valid ? load_f32(a.adt, a.adt_dtype, ao + t * a.adt_stride[2]) * kLog2e : 0.f;
+      const float da = ad * kLog2e;
       sh.cs[tid] = wave_inclusive_scan(da);
       sh.gamma[tid] = gamma;
       sh.scale[tid] = dn * (1.f - tn) + gamma;
@@ -85,15 +108,15 @@ __global__ __launch_bounds__(kThreads) void mamba_generic_kernel(const tf_mamba_
       const int r = e / n_state, n = e - r * n_state;
       const int t = t0 + r;
       const bool valid = t < L;
-      const float qv = valid ? load_f32(a.q, a.q_dtype, qo + t * a.q_stride[1] + n * a.q_stride[3]) : 0.f;
-      const float kv = valid ? load_f32(a.k, a.k_dtype, ko + t * a.k_stride[1] + n * a.k_stride[3]) : 0.f;
+      const float qv = valid ? load_f32(a.q, a.q_dtype, qo + row(t) * a.q_stride[1] + n * a.q_stride[3]) : 0.f;
+      const float kv = valid ? load_f32(a.k, a.k_dtype, ko + row(t) * a.k_stride[1] + n * a.k_stride[3]) : 0.f;
       sh.qr[r][n] = qv + a.qb[h * n_state + n];
       sh.kr[r][n] = kv + a.kb[h * n_state + n];
     }
     for (int e = tid; e < kChunk * p_dim; e += kThreads) {
       const int r = e / p_dim, p = e - r * p_dim;
       const int t = t0 + r;
-      sh.v[r][p] = t < L ? load_f32(a.v, a.v_dtype, vo + t * a.v_stride[1] + p * a.v_stride[3]) : 0.f;
+      sh.v[r][p] = t < L ? load_f32(a.v, a.v_dtype, vo + row(t) * a.v_stride[1] + p * a.v_stride[3]) : 0.f;
     }
     __syncthreads();
     // skip term from the unrotated biased vectors (mamba_fused.py:124)
@@ -115,7 +138,7 @@ __global__ __launch_bounds__(kThreads) void mamba_generic_kernel(const tf_mamba_
         float co = 1.f, si = 0.f;
         if (i < rot) {
           const float th =
-              valid ? load_f32(a.angles, a.angles_dtype, go + t * a.angles_stride[1] + i * a.angles_stride[3])
+              valid ? load_f32(a.angles, a.angles_dtype, go + row(t) * a.angles_stride[1] + i * a.angles_stride[3])
                     : 0.f;
           cum += tanh(static_cast<double>(th)) * kPiD * static_cast<double>(sh.dt[r]);
           const float ph = static_cast<float>(mod_two_pi_d(cum + carry));
@@ -157,10 +180,11 @@ __global__ __launch_bounds__(kThreads) void mamba_generic_kernel(const tf_mamba_
         float intra = 0.f;
         for (int u = 0; u < r; ++u) intra += sh.sc[r][u] * sh.v[u][p];
         y = inter * exp2f(sh.cs[r]) + intra + (skip + sh.qk[r]) * sh.v[r][p];
-        const float zz = load_f32(a.z, a.z_dtype, zo + t * a.z_stride[1] + p * a.z_stride[3]);
+        const float zz = load_f32(a.z, a.z_dtype, zo + row(t) * a.z_stride[1] + p * a.z_stride[3]);
         y *= zz * sigmoidf(zz);
       }
-      store_f32(a.out, a.out_dtype, oo + t * a.out_stride[1] + p * a.out_stride[3], y);
+      // rows in [L, T) are the same rows in either direction
+      store_f32(a.out, a.out_dtype, oo + (t < L ? row(t) : t) * a.out_stride[1] + p * a.out_stride[3], y);
     }
     // state update S <- S*2^tot + round_k(v*2^(tot-cs))^T kr (mamba_fused.py:150-152)
     const float tot = sh.cs[kChunk - 1];

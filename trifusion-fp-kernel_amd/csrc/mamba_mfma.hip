@@ -172,8 +172,8 @@ struct MfmaParams {
   const uint16_t* k;
   const uint16_t* v;
   const uint16_t* z;
-  const float* adt;
-  const float* dt;
+  const void* adt;  // adt and dt, or the raw a and ddt columns (ctl_raw)
+  const void* dt;
   const void* trap;
   const void* angles;
   const float* qb;
@@ -192,6 +192,14 @@ struct MfmaParams {
   int r_sb, r_sh, r_st;
   int T, H, group, R, xcd_per;
   int out_f32, trap_bf16, angles_dtype;
+  // Raw controls: adt/dt hold the in-projection's a/ddt columns (bf16 when
+  // ctl_bf16), turned into the step and decay in the prologue.
+  int ctl_raw, ctl_bf16;
+  float a_floor;
+  const float* dt_bias;
+  // Reverse: step t < L of a unit reads and writes row L-1-t. The host negates
+  // every time stride; the kernel moves each unit's bases to row L-1.
+  int rev;
   // Chunk-parallel form: the time axis of each of the `units` (batch, head)
   // units is cut into G segments of SC chunks, one workgroup per (segment,
   // unit). Scratch: per (unit, chunk) the phase sum per pair ([NC][64] fp64,
@@ -282,14 +290,22 @@ __device__ __forceinline__ void load_rows(const MfmaParams& P, HalfRows<KS, PS>&
   for (int s = 0; s < PS; ++s) in.v[s] = load_row8(v_row, kidx(s, hh, 0));
 }
 
+// Element i of a control tensor (fp32, or bf16 for raw controls).
+__device__ __forceinline__ float ctl_value(const void* base, int bf16, int i) {
+  return bf16 ? to_f32(static_cast<const bf16_t*>(base)[i]) : static_cast<const float*>(base)[i];
+}
+
+// Loads row t's controls (raw values when P.ctl_raw; converted where used, so
+// the loads stay in flight) and the halo step t + 1 when t + 1 < tlim: T, or
+// the valid length of a reversed unit, whose step L has no row.
 template <int RPL>
-__device__ __forceinline__ void load_ctl(const MfmaParams& P, HalfCtl<RPL>& in, const float* dtb, const float* adtb,
-                                         int trb, int gcol, int t, int first, int L) {
+__device__ __forceinline__ void load_ctl(const MfmaParams& P, HalfCtl<RPL>& in, int dto, int ado, int trb,
+                                         int gcol, int t, int first, int L, int tlim) {
   const bool valid = t < L;
-  const bool next = t + 1 < P.T;
-  in.dt = valid ? dtb[t * P.d_st] : 0.f;
-  in.dn = next ? dtb[(t + 1) * P.d_st] : 0.f;
-  in.adt = valid ? adtb[t * P.a_st] : 0.f;
+  const bool next = t + 1 < tlim;
+  in.dt = valid ? ctl_value(P.dt, P.ctl_bf16, dto + t * P.d_st) : 0.f;
+  in.dn = next ? ctl_value(P.dt, P.ctl_bf16, dto + (t + 1) * P.d_st) : 0.f;
+  in.adt = valid ? ctl_value(P.adt, P.ctl_bf16, ado + t * P.a_st) : 0.f;
   if (P.trap_bf16) {
     const bf16_t* tp = static_cast<const bf16_t*>(P.trap) + trb;
     in.tr = valid ? to_f32(tp[t * P.r_st]) : 0.f;
@@ -359,17 +375,21 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
   const int c_stop = min(c_end, nvalid);
   const int rs = (R + 1) & ~1;  // row stride of the staged phases (even: 8-byte pair reads)
   const float skip = P.d[h];
+  const int tlim = P.rev ? L : T;  // steps that have a row (halo bound)
 
-  // per-unit bases
-  const uint16_t* qbase = P.q + b * P.q_sb + qh * P.q_sh;
-  const uint16_t* kbase = P.k + b * P.k_sb + qh * P.k_sh;
-  const uint16_t* vbase = P.v + b * P.v_sb + h * P.v_sh;
-  const uint16_t* zbase = P.z + b * P.z_sb + h * P.z_sh;
-  const float* dtb = P.dt + b * P.d_sb + h * P.d_sh;
-  const float* adtb = P.adt + b * P.a_sb + h * P.a_sh;
-  const int trb = b * P.r_sb + h * P.r_sh;
-  const int gbase = b * P.g_sb + h * P.g_sh;
-  const int obase = b * P.o_sb + h * P.o_sh;
+  // per-unit bases, at row L-1 for a reversed unit (the time strides are
+  // negated, so step t lands on row L-1-t)
+  const int roff = P.rev ? max(L - 1, 0) : 0;
+  const uint16_t* qbase = P.q + b * P.q_sb + qh * P.q_sh - roff * P.q_st;
+  const uint16_t* kbase = P.k + b * P.k_sb + qh * P.k_sh - roff * P.k_st;
+  const uint16_t* vbase = P.v + b * P.v_sb + h * P.v_sh - roff * P.v_st;
+  const uint16_t* zbase = P.z + b * P.z_sb + h * P.z_sh - roff * P.z_st;
+  const int dto = b * P.d_sb + h * P.d_sh - roff * P.d_st;
+  const int ado = b * P.a_sb + h * P.a_sh - roff * P.a_st;
+  const int trb = b * P.r_sb + h * P.r_sh - roff * P.r_st;
+  const int gbase = b * P.g_sb + h * P.g_sh - roff * P.g_st;
+  const int obase = b * P.o_sb + h * P.o_sh - roff * P.o_st;
+  const float step_bias = P.ctl_raw ? P.dt_bias[h] : 0.f;
 
   // Phase carry entering the segment (both passes): the fp64 sum of the
   // preceding chunks' phase sums, reduced mod 2pi. kr depends on the absolute
@@ -408,7 +428,8 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
     const int ln = threadIdx.x & 63;
     const int p0 = ln & (RP - 1);
     const int r0 = (c_begin + cw) * kChunk + 32 * hf;
-    load_ctl(P, cur, dtb, adtb, trb, gbase + (p0 < R ? p0 : 0) * P.g_sr, r0 + (ln & 31), r0 + (ln / RP) * RPL, L);
+    load_ctl(P, cur, dto, ado, trb, gbase + (p0 < R ? p0 : 0) * P.g_sr, r0 + (ln & 31), r0 + (ln / RP) * RPL, L,
+             tlim);
   }
 
   lds_barrier();
@@ -443,15 +464,23 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
     u32x4 (&k)[KS] = rows.k;
     u32x4 (&v)[PS] = rows.v;
     float (&th)[RPL] = cur.th;
-    const float dtv = cur.dt;
+    float dtv = cur.dt;
     float csr = 0.f, gam = 0.f, scl = 0.f;
     double seg_part = 0.0;
     // ---------------- controls, phase pass 1 ----------------
     if (active) {
+      float dnv = cur.dn, adv = cur.adt;
+      if (P.ctl_raw) {
+        // step and decay from the raw columns (primitives.py:209-214); rows
+        // without a step keep dt = adt = 0
+        dtv = t < L ? control_step(dtv, step_bias) : 0.f;
+        dnv = t + 1 < tlim ? control_step(dnv, step_bias) : 0.f;
+        adv = t < L ? control_decay(adv, dtv, P.a_floor) : 0.f;
+      }
       // controls (mamba_fused.py:98-110) and the half's cumulative log2 decay
       gam = dtv * sigmoid_fast(cur.tr);
-      scl = cur.dn * (1.f - sigmoid_fast(cur.tn)) + gam;
-      csr = half_scan(cur.adt * kLog2e, c32);
+      scl = dnv * (1.f - sigmoid_fast(cur.tn)) + gam;
+      csr = half_scan(adv * kLog2e, c32);
       const float ltot = half_last(csr);
       if (hh == 0) {
         sh.dt[cw][32 * hf + c32] = dtv;
@@ -685,18 +714,13 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
       const uint16_t* z_row = zbase + (t < L ? t : t0) * P.z_st;
 #pragma unroll
       for (int s = 0; s < PS; ++s) zrow[s] = load_row8(z_row, kidx(s, hh, 0));
-      // rows in [L, T) get z = 0, whose gate silu(0) = 0 writes them as zeros
-      if (t >= L) {
-#pragma unroll
-        for (int s = 0; s < PS; ++s) zrow[s] = u32x4{0u, 0u, 0u, 0u};
-      }
     }
     // controls and angles of the same half of the next super-chunk
     Ctl nxt = {};
     if (g0 + CW + cw < c_stop) {
       const int tn = (g0 + CW + cw) * kChunk;
-      load_ctl(P, nxt, dtb, adtb, trb, gbase + (pair_on ? pp : 0) * P.g_sr, tn + 32 * hf + c32,
-               tn + 32 * hf + seg * RPL, L);
+      load_ctl(P, nxt, dto, ado, trb, gbase + (pair_on ? pp : 0) * P.g_sr, tn + 32 * hf + c32,
+               tn + 32 * hf + seg * RPL, L, tlim);
     }
 
     // ---------------- state scan over the CW chunks ----------------
@@ -758,7 +782,7 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
           const float zz = slot_f(zrow[2 * pt + (e >> 3)], e & 7);
           yv[e] = (yacc[pt][e] + yi[e] * decay) * (zz * sigmoid_fast(zz));
         }
-        if (t < T) {
+        if (t < L) {  // rows in [L, T) are zero-filled after the loop
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
             const float y[4] = {yv[4 * g], yv[4 * g + 1], yv[4 * g + 2], yv[4 * g + 3]};
@@ -786,12 +810,15 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
     }
     if (threadIdx.x == 0) P.seg_decay[rec] = seg_log2;
   } else {
-    // rows of this segment past the last valid chunk (only when lengths < T)
+    // rows of this segment in [L, T) (only when lengths < T); they are the same
+    // rows in either direction, addressed with the unreversed base and stride
     constexpr int PD = 32 * PT;
     const int row_end = min(c_end * kChunk, T);
-    for (int e = max(c_begin, nvalid) * kChunk * PD + threadIdx.x; e < row_end * PD; e += W * 64) {
+    const int o_st = P.rev ? -P.o_st : P.o_st;
+    const int obase_fwd = b * P.o_sb + h * P.o_sh;
+    for (int e = max(c_begin * kChunk, L) * PD + threadIdx.x; e < row_end * PD; e += W * 64) {
       const int tt = e / PD, p = e - tt * PD;
-      const int off = obase + tt * P.o_st + p;
+      const int off = obase_fwd + tt * o_st + p;
       if (P.out_f32)
         static_cast<float*>(P.out)[off] = 0.f;
       else
@@ -864,15 +891,18 @@ __global__ __launch_bounds__(256) void chunk_phase_kernel(const MfmaParams P) {
   const int ngrp = 256 / rpad;
   const int t_begin = chunk * kChunk;
   const int t_end = min(min(t_begin + kChunk, T), L);
-  const float* dtp = P.dt + b * P.d_sb + h * P.d_sh;
+  const int roff = P.rev ? max(L - 1, 0) : 0;  // reversed unit: step t reads row L-1-t
+  const int dto = b * P.d_sb + h * P.d_sh - roff * P.d_st;
+  const float step_bias = P.ctl_raw ? P.dt_bias[h] : 0.f;
   double acc = 0.0;
   if (r < P.R) {
-    const int g0 = b * P.g_sb + h * P.g_sh + r * P.g_sr;
-#pragma unroll 4
+    const int g0 = b * P.g_sb + h * P.g_sh + r * P.g_sr - roff * P.g_st;
     for (int t = t_begin + grp; t < t_end; t += ngrp) {
       const float th = P.angles_dtype == TF_FLOAT32 ? static_cast<const float*>(P.angles)[g0 + t * P.g_st]
                                                     : to_f32(static_cast<const bf16_t*>(P.angles)[g0 + t * P.g_st]);
-      acc += static_cast<double>(tanh_fast(th) * kPi * dtp[t * P.d_st]);
+      float dt = ctl_value(P.dt, P.ctl_bf16, dto + t * P.d_st);
+      if (P.ctl_raw) dt = control_step(dt, step_bias);
+      acc += static_cast<double>(tanh_fast(th) * kPi * dt);
     }
   }
   part[threadIdx.x] = acc;
@@ -919,8 +949,8 @@ MfmaParams make_params(const tf_mamba_args& a) {
   P.k = static_cast<const uint16_t*>(a.k);
   P.v = static_cast<const uint16_t*>(a.v);
   P.z = static_cast<const uint16_t*>(a.z);
-  P.adt = static_cast<const float*>(a.adt);
-  P.dt = static_cast<const float*>(a.dt);
+  P.adt = a.adt;
+  P.dt = a.dt;
   P.trap = a.trap;
   P.angles = a.angles;
   P.qb = a.qb;
@@ -952,6 +982,15 @@ MfmaParams make_params(const tf_mamba_args& a) {
   P.seg_state = nullptr;
   P.chunk_phase = nullptr;
   P.seg_decay = nullptr;
+  P.ctl_raw = a.dt_bias != nullptr;
+  P.ctl_bf16 = a.dt_dtype == TF_BFLOAT16;
+  P.a_floor = a.a_floor;
+  P.dt_bias = a.dt_bias;
+  P.rev = a.reverse != 0;
+  if (P.rev) {
+    P.q_st = -P.q_st, P.k_st = -P.k_st, P.v_st = -P.v_st, P.z_st = -P.z_st, P.o_st = -P.o_st;
+    P.g_st = -P.g_st, P.a_st = -P.a_st, P.d_st = -P.d_st, P.r_st = -P.r_st;
+  }
   return P;
 }
 
@@ -1046,7 +1085,11 @@ int64_t mfma_workspace_bytes(const tf_mamba_args& a) {
 bool mfma_supported(const tf_mamba_args& a) {
   if (a.q_dtype != TF_BFLOAT16 || a.k_dtype != TF_BFLOAT16 || a.v_dtype != TF_BFLOAT16 || a.z_dtype != TF_BFLOAT16)
     return false;
-  if (a.adt_dtype != TF_FLOAT32 || a.dt_dtype != TF_FLOAT32) return false;
+  if (a.dt_bias == nullptr) {
+    if (a.adt_dtype != TF_FLOAT32 || a.dt_dtype != TF_FLOAT32) return false;
+  } else if (a.adt_dtype != a.dt_dtype || (a.dt_dtype != TF_FLOAT32 && a.dt_dtype != TF_BFLOAT16)) {
+    return false;
+  }
   if (a.trap_dtype != TF_FLOAT32 && a.trap_dtype != TF_BFLOAT16) return false;
   if (a.angles_dtype != TF_FLOAT32 && a.angles_dtype != TF_BFLOAT16) return false;
   if (a.out_dtype != TF_BFLOAT16 && a.out_dtype != TF_FLOAT32) return false;

@@ -65,6 +65,9 @@ class MambaArgs(ctypes.Structure):
         ],
         ("workspace", c_ptr),
         ("workspace_bytes", c_i64),
+        ("dt_bias", c_ptr),
+        ("a_floor", c_f32),
+        ("reverse", c_i32),
     ]
 
 
@@ -87,6 +90,8 @@ _SIGNATURES = {
     ),
     "tf_masked_mean": ([c_ptr, c_i32, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_ptr], c_i32),
     "tf_time_mask": ([c_ptr, c_ptr, c_i64, c_i64, c_ptr], c_i32),
+    "tf_reverse_valid": ([c_ptr, c_ptr, c_i32, c_ptr, c_i64, c_i64, c_i64, c_ptr], c_i32),
+    "tf_mean_rmsnorm": ([c_ptr, c_i32, c_ptr, c_i32, c_ptr, c_ptr, c_i64, c_i64, c_f32, c_ptr], c_i32),
     "tf_version": ([], ctypes.c_char_p),
 }
 

@@ -1,7 +1,8 @@
 """Inference kernels around the recurrence (reference ``src/trifusion_l4/kernels/__init__.py``).
 
-``RMSNorm`` mirrors ``kernels/__init__.py:15-28`` and ``swiglu`` mirrors
-``:31-41``; both launch gfx950 HIP kernels through the C ABI.
+``RMSNorm`` mirrors ``kernels/__init__.py:15-28``, ``swiglu`` mirrors
+``:31-41`` and ``reverse_valid`` mirrors ``:44-55``; all launch gfx950 HIP
+kernels through the C ABI.
 """
 
 import torch
@@ -42,4 +43,32 @@ def launch_swiglu(x):
     return y
 
 
-__all__ = ["RMSNorm", "swiglu", "rms"]
+def reverse_valid(x, lengths):
+    """Reverse the valid prefix of each row of ``x`` ``[B, T, D]``:
+    ``y[b, t] = x[b, lengths[b] - 1 - t]`` for ``t < lengths[b]``, else 0
+    (``trifusion_amd::reverse_valid``)."""
+    return ops.reverse_valid(x, lengths)
+
+
+def launch_reverse_valid(x, lengths):
+    lib = _lib.load()
+    _lib.require_cuda(x, lengths, what="reverse_valid")
+    if x.dim() != 3:
+        raise ValueError(f"reverse_valid: x must be [B, T, D], got {tuple(x.shape)}")
+    b, t, d = x.shape
+    if tuple(lengths.shape) != (b,) or lengths.dtype != torch.int64:
+        raise ValueError("reverse_valid: lengths must be an int64 tensor of shape [B]")
+    x = x.contiguous()
+    lengths = lengths.contiguous()
+    y = torch.empty_like(x)
+    if x.numel() == 0:
+        return y
+    status = lib.tf_reverse_valid(
+        x.data_ptr(), y.data_ptr(), _lib.dtype_code(x, "reverse_valid"), lengths.data_ptr(), b, t, d,
+        _lib.stream_of(x),
+    )
+    _lib.check(status, "reverse_valid")
+    return y
+
+
+__all__ = ["RMSNorm", "swiglu", "rms", "reverse_valid"]

@@ -3,7 +3,9 @@
 ``rms`` replaces the MODE-0 ``_norm`` launch (``native.py:8-39,42-70``), ``add``
 replaces ``_add`` (``:81-100``) and ``add_rms`` fuses an ``add`` with the
 RMSNorm that follows it in the next block, writing both the residual sum and
-its normalised copy in one pass.
+its normalised copy in one pass. ``mean_norm`` replaces the MODE-2 ``_norm``
+launch (``:77-78``): the RMSNorm of the mean of a bidirectional block's two
+directions.
 """
 
 import torch
@@ -134,6 +136,43 @@ def launch_add_rms(a, b, weight, mask=None, eps=1e-5, out_dtype=torch.bfloat16):
     )
     _lib.check(status, "add_rms")
     return s, y
+
+
+def mean_norm(a, b, weight, eps=1e-5):
+    """``rms((a + b) / 2, weight)`` with fp32 math and an fp32 output
+    (reference ``native.mean_norm``, ``src/trifusion_l4/kernels/native.py:77-78``;
+    ``trifusion_amd::mean_rms_norm``)."""
+    return ops.mean_rms_norm(a, b, weight, eps)
+
+
+def launch_mean_rms(a, b, weight, eps=1e-5):
+    lib = _lib.load()
+    _lib.require_cuda(a, b, weight, what="mean_norm")
+    if a.shape != b.shape:
+        raise ValueError("mean_norm: shapes differ")
+    if weight.dtype != torch.float32 or not weight.is_contiguous():
+        weight = weight.float().contiguous()
+    d = a.shape[-1]
+    if weight.shape != (d,):
+        raise ValueError(f"mean_norm: weight must be [{d}]")
+    a = a.contiguous()
+    b = b.contiguous()
+    rows = a.numel() // d if d else 0
+    y = torch.empty(a.shape, device=a.device, dtype=torch.float32)
+    status = lib.tf_mean_rmsnorm(
+        a.data_ptr(),
+        _lib.dtype_code(a, "mean_norm"),
+        b.data_ptr(),
+        _lib.dtype_code(b, "mean_norm"),
+        weight.data_ptr(),
+        y.data_ptr(),
+        rows,
+        d,
+        float(eps),
+        _lib.stream_of(a),
+    )
+    _lib.check(status, "mean_norm")
+    return y
 
 
 def _mask_ptr(mask, rows):

@@ -5,9 +5,18 @@ the same parameter names and in-projection layout ``z, x, B, C, dt, a, trap,
 angles`` (``:26-30,43-55``), B/C RMSNorm over the state dim with one B/C head
 (``:21,56-57``), the discretisation controls (``:58-65``), rotary angles shared by
 all heads as a stride-0 view (``:66``) and the fused recurrence called on
-strided column slices of the projection, no copies (``:70-82``). The controls,
-norms and recurrence are gfx950 HIP kernels; the two projections are torch
-GEMMs (hipBLASLt).
+strided column slices of the projection, no copies (``:70-82``). The norms and
+recurrence are gfx950 HIP kernels; the two projections are torch GEMMs
+(hipBLASLt).
+
+By default the controls (``:58-65``) are computed inside the recurrence from
+the raw ``a``/``ddt`` columns (``fuse_controls``; the same per-step formula as
+the separate ``mamba_controls`` kernel, which ``fuse_controls = False``
+restores). ``forward(u, lengths, reverse=True)`` is the backward direction of
+the reference's bidirectional block, ``reverse_valid(backward_mamba(
+reverse_valid(u)))`` (``src/trifusion_l4/model.py:174-179``): every step of the
+block is per-row except the recurrence, which walks each valid prefix in
+reverse, so no reversed copies are made.
 """
 
 import torch
@@ -43,6 +52,7 @@ class Mamba3Inference(nn.Module):
         self.C_norm = RMSNorm(self.d_state)
         # "mfma" (chunked MFMA scan), "generic" (fp32-FMA kernel) or "auto"
         self.variant = "auto"
+        self.fuse_controls = True
 
     def split(self, p):
         return p.split(
@@ -59,13 +69,18 @@ class Mamba3Inference(nn.Module):
             -1,
         )
 
-    def forward(self, u, lengths=None):
+    def forward(self, u, lengths=None, reverse=False):
         b, t, _ = u.shape
         p = self.in_proj(u)
         z, v, k, q, ddt, a, trap, angles = self.split(p)
         q = self.C_norm(q.reshape(b, t, 1, self.d_state))
         k = self.B_norm(k.reshape(b, t, 1, self.d_state))
-        adt, dt = mamba_controls(a, ddt, self.dt_bias, self.A_floor)
+        if self.fuse_controls and self.dt_bias.dtype == torch.float32:
+            adt, dt = a.transpose(1, 2), ddt.transpose(1, 2)
+            raw = {"dt_bias": self.dt_bias, "a_floor": self.A_floor}
+        else:
+            adt, dt = mamba_controls(a, ddt, self.dt_bias, self.A_floor)
+            raw = {}
         angles = angles.unsqueeze(2).expand(b, t, self.nheads, self.num_rope_angles)
         y = fused_mamba(
             q,
@@ -81,5 +96,7 @@ class Mamba3Inference(nn.Module):
             z.reshape(b, t, self.nheads, self.headdim),
             lengths=lengths,
             variant=self.variant,
+            reverse=reverse,
+            **raw,
         )
         return self.out_proj(y.reshape(b, t, self.d_inner))

@@ -6,9 +6,20 @@ same name, positional order and ``warps`` keyword, output allocated like
 on the current stream, forward only. Shapes are generalised from the
 reference's fixed N=128, P=64, R=32 (``:159-160``) to N in {16, 32, 64, 128},
 P in {32, 64} and any R <= N/2; other dims raise ``ValueError`` as the reference
-does. Two keyword-only extensions: ``out=`` (write into a caller tensor, e.g. an
-fp32 one) and ``lengths=`` (per-row valid lengths: rows past the length are 0
-and fully padded chunks are skipped).
+does. Keyword-only extensions:
+
+* ``out=``: write into a caller tensor (e.g. an fp32 one);
+* ``lengths=``: per-row valid lengths; rows past the length are 0 and fully
+  padded chunks are skipped;
+* ``reverse=True``: run each row over its valid prefix in reverse and write the
+  outputs back in place, the backward direction of the reference's
+  bidirectional block (``reverse_valid(fused_mamba(reverse_valid(x)))``,
+  ``src/trifusion_l4/model.py:174-179``) without the two reversed copies;
+* ``dt_bias=`` (with ``a_floor=``): raw controls. ``adt`` and ``dt`` are then
+  the raw ``a`` and ``ddt`` in-projection columns viewed as ``[B, H, T]``, and
+  the recurrence computes ``mamba_controls`` (``src/trifusion_l4/kernels/
+  buffers.py:82-101``) per step itself, so the ``[B, H, T]`` control tensors
+  and their launch disappear.
 """
 
 import ctypes
@@ -26,7 +37,8 @@ def _shape_error(message):
     return ValueError(f"fused_mamba: {message}")
 
 
-def build_args(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths=None, variant="auto"):
+def build_args(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths=None, variant="auto", reverse=False,
+               dt_bias=None, a_floor=1e-4):
     """Validate the operands and pack them into a ``tf_mamba_args`` struct."""
     what = "fused_mamba"
     for name, t in (("q", q), ("k", k), ("v", v), ("z", z), ("angles", angles)):
@@ -62,7 +74,12 @@ def build_args(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths=None, 
     if lengths is not None:
         if tuple(lengths.shape) != (b,) or lengths.dtype != torch.int64 or not lengths.is_contiguous():
             raise _shape_error("lengths must be a contiguous int64 tensor of shape [B]")
-    _lib.require_cuda(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths, what=what)
+    if dt_bias is not None:
+        if tuple(dt_bias.shape) != (h,) or dt_bias.dtype != torch.float32 or not dt_bias.is_contiguous():
+            raise _shape_error(f"dt_bias must be a contiguous float32 tensor of shape {(h,)}")
+        if adt.dtype != dt.dtype:
+            raise TypeError("fused_mamba: raw controls a and ddt must share one dtype")
+    _lib.require_cuda(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths, dt_bias, what=what)
 
     a = _lib.MambaArgs()
     for name, ten in (
@@ -81,6 +98,9 @@ def build_args(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths=None, 
     ):
         setattr(a, name, ten.data_ptr())
     a.lengths = lengths.data_ptr() if lengths is not None else None
+    a.dt_bias = dt_bias.data_ptr() if dt_bias is not None else None
+    a.a_floor = float(a_floor)
+    a.reverse = 1 if reverse else 0
     for name, ten in (
         ("q", q),
         ("k", k),
@@ -106,11 +126,12 @@ def build_args(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths=None, 
     return a
 
 
-def launch(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths=None, variant="auto"):
+def launch(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths=None, variant="auto", reverse=False,
+           dt_bias=None, a_floor=1e-4):
     """Validate, then enqueue ``tf_fused_mamba`` on the current stream (the CUDA
     kernel of the ``trifusion_amd::fused_mamba`` operator); returns ``out``."""
     lib = _lib.load()
-    args = build_args(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths, variant)
+    args = build_args(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths, variant, reverse, dt_bias, a_floor)
     # Long sequences over few (batch, head) units run chunk-parallel on scratch
     # the library sizes; it comes from torch's caching allocator (the graph's
     # private pool under capture), the C side never allocates.
@@ -126,26 +147,51 @@ def launch(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths=None, vari
     return out
 
 
-def fused_mamba(q, k, v, adt, dt, trap, qb, kb, angles, d, z, warps=8, *, out=None, lengths=None, variant="auto"):
+def fused_mamba(
+    q,
+    k,
+    v,
+    adt,
+    dt,
+    trap,
+    qb,
+    kb,
+    angles,
+    d,
+    z,
+    warps=8,
+    *,
+    out=None,
+    lengths=None,
+    variant="auto",
+    reverse=False,
+    dt_bias=None,
+    a_floor=1e-4,
+):
     """Fused Mamba-3 recurrence forward; returns ``out`` ``[B, T, H, P]``.
 
     ``warps`` is accepted for signature compatibility; gfx950 launch shapes are
     chosen by the library. ``variant`` selects ``"auto"`` (MFMA chunked scan
-    where supported), ``"mfma"`` or ``"generic"``. Dispatches through the
-    ``trifusion_amd::fused_mamba`` operator (``fused_mamba.out`` with ``out=``).
+    where supported), ``"mfma"`` or ``"generic"``. ``reverse``, ``dt_bias`` and
+    ``a_floor`` are the extensions described in the module docstring.
+    Dispatches through the ``trifusion_amd::fused_mamba`` operator
+    (``fused_mamba.out`` with ``out=``).
     """
     del warps
+    ext = (lengths, variant, bool(reverse), dt_bias, float(a_floor))
     if out is None:
-        return ops.fused_mamba(q, k, v, adt, dt, trap, qb, kb, angles, d, z, lengths, variant)
-    return ops.fused_mamba.out(q, k, v, adt, dt, trap, qb, kb, angles, d, z, lengths, variant, out=out)
+        return ops.fused_mamba(q, k, v, adt, dt, trap, qb, kb, angles, d, z, *ext)
+    return ops.fused_mamba.out(q, k, v, adt, dt, trap, qb, kb, angles, d, z, *ext, out=out)
 
 
-def selected_variant(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out=None, lengths=None, variant="auto"):
+def selected_variant(
+    q, k, v, adt, dt, trap, qb, kb, angles, d, z, out=None, lengths=None, variant="auto", reverse=False, dt_bias=None
+):
     """Name of the kernel ``fused_mamba`` would launch for these operands."""
     lib = _lib.load()
     if out is None:
         out = torch.empty_like(v, memory_format=torch.contiguous_format)
-    args = build_args(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths, variant)
+    args = build_args(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths, variant, reverse, dt_bias)
     code = lib.tf_fused_mamba_variant(ctypes.byref(args))
     if code < 0:
         _lib.check(-code, "fused_mamba")

@@ -9,6 +9,11 @@ hop), ``depth`` blocks of
     512 -> masked residual
 
 and a masked mean-pool over valid frames followed by a 512 -> 5 linear head.
+With ``bidirectional=True`` each block also runs a backward Mamba-3 over each
+clip's reversed valid prefix and feeds the RMSNorm of the two directions' mean
+to the residual, the bidirectional mixing of the reference's TriFusion block
+(``src/trifusion_l4/model.py:174-184``); the backward direction reverses
+inside the recurrence (``reverse=True``) instead of through reversed copies.
 ``forward(audio, lengths, channels)`` returns ``{"logits": [B, 5]}``, the contract
 ``InferenceEngine`` relies on (reference ``src/trifusion_l4/runtime.py:82``,
 ``src/trifusion_l4/model.py:259-260``). The residual stream is fp32; each residual
@@ -24,7 +29,7 @@ import torch.nn.functional as F
 from torch import nn
 
 from .kernels import RMSNorm, swiglu
-from .kernels.native import add, add_rms, rms
+from .kernels.native import add, add_rms, mean_norm, rms
 from .mamba import Mamba3Inference
 from .masking import masked, masked_mean, time_mask
 
@@ -42,6 +47,7 @@ class ModelConfig:
     stem_padding: int = 120
     norm_eps: float = 1e-5
     init_std: float = 0.02
+    bidirectional: bool = False
 
 
 FFN_ALIGN = 32  # FFN width the GEMMs and SwiGLU run at (each half zero-padded up to it)
@@ -52,6 +58,11 @@ class EncoderBlock(nn.Module):
         super().__init__()
         self.pre = RMSNorm(c.dim, c.norm_eps)
         self.mamba = Mamba3Inference(c)
+        if c.bidirectional:
+            self.mamba_bwd = Mamba3Inference(c)
+            self.mn = RMSNorm(c.dim, c.norm_eps)
+        else:
+            self.mamba_bwd = None
         self.ff_norm = RMSNorm(c.dim, c.norm_eps)
         self.gate_up = nn.Linear(c.dim, 2 * c.ffn_dim, bias=False)
         self.down = nn.Linear(c.ffn_dim, c.dim, bias=False)
@@ -104,8 +115,9 @@ class Encoder(nn.Module):
 
     def set_variant(self, variant):
         """Select the recurrence kernel ("auto", "mfma" or "generic") of every block."""
-        for blk in self.blocks:
-            blk.mamba.variant = variant
+        for m in self.modules():
+            if isinstance(m, Mamba3Inference):
+                m.variant = variant
 
     def frames(self, lengths, time):
         """Valid frames per clip: floor(len / stride) for the padded stem, in [1, time]."""
@@ -132,6 +144,10 @@ class Encoder(nn.Module):
         h = rms(x, blocks[0].pre.weight, blocks[0].pre.eps, out_dtype=torch.bfloat16)
         for i, blk in enumerate(blocks):
             m = blk.mamba(h, frames)
+            if blk.mamba_bwd is not None:
+                # rows past each clip's length are 0 in both directions
+                mb = blk.mamba_bwd(h, frames, reverse=True)
+                m = mean_norm(m, mb, blk.mn.weight, blk.mn.eps)
             x, h = add_rms(x, m, blk.ff_norm.weight, mask, blk.ff_norm.eps)
             d = blk.ffn(h)
             if i + 1 < len(blocks):

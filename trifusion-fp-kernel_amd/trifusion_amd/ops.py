@@ -20,12 +20,15 @@ import torch
 
 NAMESPACE = "trifusion_amd"
 
+# keyword extensions of fused_mamba: valid lengths, kernel choice, reversed
+# walk of the valid prefix, raw controls (dt_bias) and their decay floor
+_EXT = "Tensor? lengths=None, str variant='auto', bool reverse=False, Tensor? dt_bias=None, float a_floor=0.0001"
+
 _SCHEMAS = {
     "fused_mamba": "fused_mamba(Tensor q, Tensor k, Tensor v, Tensor adt, Tensor dt, Tensor trap, Tensor qb, "
-    "Tensor kb, Tensor angles, Tensor d, Tensor z, Tensor? lengths=None, str variant='auto') -> Tensor",
+    f"Tensor kb, Tensor angles, Tensor d, Tensor z, {_EXT}) -> Tensor",
     "fused_mamba.out": "fused_mamba.out(Tensor q, Tensor k, Tensor v, Tensor adt, Tensor dt, Tensor trap, "
-    "Tensor qb, Tensor kb, Tensor angles, Tensor d, Tensor z, Tensor? lengths=None, str variant='auto', *, "
-    "Tensor(a!) out) -> Tensor(a!)",
+    f"Tensor qb, Tensor kb, Tensor angles, Tensor d, Tensor z, {_EXT}, *, Tensor(a!) out) -> Tensor(a!)",
     "rms_norm": "rms_norm(Tensor x, Tensor weight, float eps=1e-05, ScalarType? out_dtype=None) -> Tensor",
     "add_rms_norm": "add_rms_norm(Tensor a, Tensor b, Tensor weight, Tensor? mask=None, float eps=1e-05, "
     "ScalarType? out_dtype=None) -> (Tensor, Tensor)",
@@ -35,6 +38,8 @@ _SCHEMAS = {
     "mamba_controls": "mamba_controls(Tensor a, Tensor dt, Tensor bias, float floor) -> (Tensor, Tensor)",
     "masked_mean": "masked_mean(Tensor x, Tensor lengths) -> Tensor",
     "time_mask": "time_mask(Tensor lengths, int time) -> Tensor",
+    "reverse_valid": "reverse_valid(Tensor x, Tensor lengths) -> Tensor",
+    "mean_rms_norm": "mean_rms_norm(Tensor a, Tensor b, Tensor weight, float eps=1e-05) -> Tensor",
 }
 
 OPERATORS = tuple(_SCHEMAS)
@@ -43,17 +48,19 @@ OPERATORS = tuple(_SCHEMAS)
 # ---- CUDA kernels: the ctypes launches (imported lazily: those modules call these operators) ----
 
 
-def _cuda_fused_mamba(q, k, v, adt, dt, trap, qb, kb, angles, d, z, lengths=None, variant="auto"):
+def _cuda_fused_mamba(q, k, v, adt, dt, trap, qb, kb, angles, d, z, lengths=None, variant="auto", reverse=False,
+                      dt_bias=None, a_floor=1e-4):
     from .mamba_fused import launch
 
     out = torch.empty_like(v, memory_format=torch.contiguous_format)
-    return launch(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths, variant)
+    return launch(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths, variant, reverse, dt_bias, a_floor)
 
 
-def _cuda_fused_mamba_out(q, k, v, adt, dt, trap, qb, kb, angles, d, z, lengths=None, variant="auto", *, out):
+def _cuda_fused_mamba_out(q, k, v, adt, dt, trap, qb, kb, angles, d, z, lengths=None, variant="auto", reverse=False,
+                          dt_bias=None, a_floor=1e-4, *, out):
     from .mamba_fused import launch
 
-    return launch(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths, variant)
+    return launch(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths, variant, reverse, dt_bias, a_floor)
 
 
 def _cuda_rms_norm(x, weight, eps=1e-5, out_dtype=None):
@@ -104,14 +111,28 @@ def _cuda_time_mask(lengths, time):
     return launch_time_mask(lengths, time)
 
 
+def _cuda_reverse_valid(x, lengths):
+    from .kernels import launch_reverse_valid
+
+    return launch_reverse_valid(x, lengths)
+
+
+def _cuda_mean_rms_norm(a, b, weight, eps=1e-5):
+    from .kernels.native import launch_mean_rms
+
+    return launch_mean_rms(a, b, weight, eps)
+
+
 # ---- Meta kernels: output shapes and dtypes only ----
 
 
-def _meta_fused_mamba(q, k, v, adt, dt, trap, qb, kb, angles, d, z, lengths=None, variant="auto"):
+def _meta_fused_mamba(q, k, v, adt, dt, trap, qb, kb, angles, d, z, lengths=None, variant="auto", reverse=False,
+                      dt_bias=None, a_floor=1e-4):
     return torch.empty_like(v, memory_format=torch.contiguous_format)
 
 
-def _meta_fused_mamba_out(q, k, v, adt, dt, trap, qb, kb, angles, d, z, lengths=None, variant="auto", *, out):
+def _meta_fused_mamba_out(q, k, v, adt, dt, trap, qb, kb, angles, d, z, lengths=None, variant="auto", reverse=False,
+                          dt_bias=None, a_floor=1e-4, *, out):
     return out
 
 
@@ -148,6 +169,14 @@ def _meta_time_mask(lengths, time):
     return lengths.new_empty((lengths.shape[0], time), dtype=torch.bool)
 
 
+def _meta_reverse_valid(x, lengths):
+    return torch.empty_like(x, memory_format=torch.contiguous_format)
+
+
+def _meta_mean_rms_norm(a, b, weight, eps=1e-5):
+    return a.new_empty(a.shape, dtype=torch.float32)
+
+
 # ---- CPU kernels: loud failure, no fallback ----
 
 
@@ -172,6 +201,8 @@ _KERNELS = {
     "mamba_controls": (_cuda_mamba_controls, _meta_mamba_controls),
     "masked_mean": (_cuda_masked_mean, _meta_masked_mean),
     "time_mask": (_cuda_time_mask, _meta_time_mask),
+    "reverse_valid": (_cuda_reverse_valid, _meta_reverse_valid),
+    "mean_rms_norm": (_cuda_mean_rms_norm, _meta_mean_rms_norm),
 }
 
 _LIBRARY = torch.library.Library(NAMESPACE, "DEF")
