@@ -186,15 +186,16 @@ def graph_us(torch, fn, steps=100):
 
 def bandwidth_kernels(torch):
     """Each single-pass kernel of the encoder at its 4 s mono x 16 shape (16 x 400
-    frames, dim 512, in-proj width 2240, FFN 2 x 1365): algorithmic bytes (each
-    input element read once, each output written once) / time vs 8 TB/s."""
+    frames, dim 512, in-proj width 2240 in rows of 2304, FFN 2 x 1365 run at
+    2 x 1408): algorithmic bytes (each input element read once, each output
+    written once) / time vs 8 TB/s."""
     from trifusion_amd.kernels import rms, swiglu
     from trifusion_amd.kernels.buffers import mamba_controls, mask_buffer
     from trifusion_amd.kernels.native import add, add_rms
     from trifusion_amd.masking import masked_mean, time_mask
 
     g = torch.Generator(device="cuda").manual_seed(5)
-    b, t, dim, proj, ffn, heads, n = 16, 400, 512, 2240, 1365, 16, 64
+    b, t, dim, proj, ffn, heads, n = 16, 400, 512, 2304, 1408, 16, 64
     rows = b * t
     x = torch.randn(b, t, dim, device="cuda", generator=g)
     br = torch.randn(b, t, dim, device="cuda", generator=g).bfloat16()
@@ -213,7 +214,7 @@ def bandwidth_kernels(torch):
         ("add_rms fp32+bf16 -> fp32,bf16 [6400,512]", lambda: add_rms(x, br, w, mask),
          rows * dim * (4 + 2 + 4 + 2) + rows),
         ("rms bf16 strided C/B columns [6400,64]", lambda: rms(cview, wn), rows * n * (2 + 2)),
-        ("swiglu bf16 [6400,2730] -> [6400,1365]", lambda: swiglu(gu), rows * 3 * ffn * 2),
+        ("swiglu bf16 [6400,2816] -> [6400,1408]", lambda: swiglu(gu), rows * 3 * ffn * 2),
         ("mamba_controls bf16 [16,400,16] x2 -> fp32 [16,16,400] x2", lambda: mamba_controls(a_cols, d_cols, bias, 1e-4),
          rows * heads * (2 + 2 + 4 + 4)),
         ("masked_mean fp32 [16,400,512] -> [16,512]", lambda: masked_mean(x, lengths), rows * dim * 4 + b * dim * 4),

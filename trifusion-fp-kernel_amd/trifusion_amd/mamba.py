@@ -20,11 +20,17 @@ reverse, so no reversed copies are made.
 """
 
 import torch
+import torch.nn.functional as F
 from torch import nn
 
 from .kernels import RMSNorm
 from .kernels.buffers import mamba_controls
 from .mamba_fused import fused_mamba
+
+# Output width the in-projection GEMM runs at: rows of zeros pad the weight to
+# a multiple of this (2240 -> 2304 at dim 512); the extra columns of the
+# projection are never read, the splits are views of its first 2240 columns.
+PROJ_ALIGN = 128
 
 
 class Mamba3Inference(nn.Module):
@@ -53,6 +59,25 @@ class Mamba3Inference(nn.Module):
         # "mfma" (chunked MFMA scan), "generic" (fp32-FMA kernel) or "auto"
         self.variant = "auto"
         self.fuse_controls = True
+        self._padded = None
+        self._padded_key = None
+
+    def _padded_in_proj(self):
+        """in_proj.weight with zero output rows up to a multiple of PROJ_ALIGN,
+        rebuilt when the weight changes. The library GEMM runs an odd tile count
+        (2240 = 17.5 x 128) markedly slower than the padded 2304."""
+        w = self.in_proj.weight
+        rows = w.shape[0]
+        padded = -(-rows // PROJ_ALIGN) * PROJ_ALIGN
+        if padded == rows:
+            return w
+        key = (w.data_ptr(), w._version, w.dtype, w.device)
+        if self._padded_key != key:
+            with torch.no_grad():
+                wp = w.new_zeros(padded, w.shape[1])
+                wp[:rows] = w
+            self._padded, self._padded_key = wp, key
+        return self._padded
 
     def split(self, p):
         return p.split(
@@ -71,7 +96,8 @@ class Mamba3Inference(nn.Module):
 
     def forward(self, u, lengths=None, reverse=False):
         b, t, _ = u.shape
-        p = self.in_proj(u)
+        width = self.in_proj.out_features
+        p = F.linear(u, self._padded_in_proj())[..., :width]
         z, v, k, q, ddt, a, trap, angles = self.split(p)
         q = self.C_norm(q.reshape(b, t, 1, self.d_state))
         k = self.B_norm(k.reshape(b, t, 1, self.d_state))

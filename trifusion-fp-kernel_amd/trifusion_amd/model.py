@@ -50,7 +50,7 @@ class ModelConfig:
     bidirectional: bool = False
 
 
-FFN_ALIGN = 32  # FFN width the GEMMs and SwiGLU run at (each half zero-padded up to it)
+FFN_ALIGN = 64  # FFN width the GEMMs and SwiGLU run at (each half zero-padded up to it)
 
 
 class EncoderBlock(nn.Module):
@@ -70,12 +70,13 @@ class EncoderBlock(nn.Module):
         self._padded_key = None
 
     def _padded_ffn(self):
-        """gate_up and down with each FFN half zero-padded to a multiple of
-        FFN_ALIGN. An odd width (1365) leaves every GEMM output row and every
-        down-projection input row misaligned, which the library GEMMs and the
-        SwiGLU kernel run at a fraction of their rate; the padded rows give
-        silu(0) * 0 = 0 and meet zero columns of down, so the result is the same
-        up to the GEMMs' summation order. Rebuilt when either weight changes."""
+        """The FFN weights at a width the library GEMMs run well: each half of
+        gate_up zero-padded to a multiple of FFN_ALIGN rows and stored K-major
+        ([dim, 2 * width], used as ``h @ w``), and down with matching zero
+        columns. An odd width (1365) leaves every GEMM tile and SwiGLU row
+        misaligned; the padded rows give silu(0) * 0 = 0 and meet zero columns
+        of down, so the result is the same up to the GEMMs' summation order.
+        Rebuilt when either weight changes."""
         w1, w2 = self.gate_up.weight, self.down.weight
         key = (w1.data_ptr(), w1._version, w2.data_ptr(), w2._version, w1.dtype, w1.device)
         if self._padded_key != key:
@@ -87,14 +88,12 @@ class EncoderBlock(nn.Module):
                 g1[fp : fp + f] = w1[f:]
                 g2 = w2.new_zeros(d, fp)
                 g2[:, :f] = w2
-            self._padded, self._padded_key = (g1, g2), key
+            self._padded, self._padded_key = (g1.t().contiguous(), g2), key
         return self._padded
 
     def ffn(self, h):
-        if self.down.in_features % FFN_ALIGN == 0:
-            return self.down(swiglu(self.gate_up(h)))
-        g1, g2 = self._padded_ffn()
-        return F.linear(swiglu(F.linear(h, g1)), g2)
+        g1t, g2 = self._padded_ffn()
+        return F.linear(swiglu(h @ g1t), g2)
 
 
 class Encoder(nn.Module):
