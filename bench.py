@@ -191,7 +191,8 @@ def bandwidth_kernels(torch):
     written once) / time vs 8 TB/s."""
     from trifusion_amd.kernels import rms, swiglu
     from trifusion_amd.kernels.buffers import mamba_controls, mask_buffer
-    from trifusion_amd.kernels.native import add, add_rms
+    from trifusion_amd.kernels.native import add, add_rms, mask_rms, rms_pair
+    from trifusion_amd.stem import frame_audio
     from trifusion_amd.masking import masked_mean, time_mask
 
     g = torch.Generator(device="cuda").manual_seed(5)
@@ -201,25 +202,30 @@ def bandwidth_kernels(torch):
     br = torch.randn(b, t, dim, device="cuda", generator=g).bfloat16()
     w = torch.ones(dim, device="cuda")
     p = torch.randn(b, t, proj, device="cuda", generator=g).bfloat16()
-    cview = p[..., 2 * 1024 + n: 2 * 1024 + 2 * n].reshape(b, t, 1, n)  # C columns of the in-proj output
+    bcview = p[..., 2 * 1024: 2 * 1024 + 2 * n]  # B and C columns of the in-proj output
     a_cols = p[..., 2 * 1024 + 2 * n + heads: 2 * 1024 + 2 * n + 2 * heads]
     d_cols = p[..., 2 * 1024 + 2 * n: 2 * 1024 + 2 * n + heads]
     gu = torch.randn(b, t, 2 * ffn, device="cuda", generator=g).bfloat16()
     lengths = torch.full((b,), t, dtype=torch.int64, device="cuda")
     mask = time_mask(lengths, t)
     bias = torch.zeros(heads, device="cuda")
+    audio = torch.rand(b, 1, 64000, device="cuda", generator=g) * 2 - 1
+    chans = torch.ones(b, dtype=torch.int64, device="cuda")
     wn = torch.ones(n, device="cuda")
     cases = [
         ("rms fp32->bf16 [6400,512]", lambda: rms(x, w, out_dtype=torch.bfloat16), rows * dim * (4 + 2)),
         ("add_rms fp32+bf16 -> fp32,bf16 [6400,512]", lambda: add_rms(x, br, w, mask),
          rows * dim * (4 + 2 + 4 + 2) + rows),
-        ("rms bf16 strided C/B columns [6400,64]", lambda: rms(cview, wn), rows * n * (2 + 2)),
+        ("rms pair bf16 strided B|C columns [6400,2x64]", lambda: rms_pair(bcview, wn, wn), rows * 2 * n * (2 + 2)),
         ("swiglu bf16 [6400,2816] -> [6400,1408]", lambda: swiglu(gu), rows * 3 * ffn * 2),
         ("mamba_controls bf16 [16,400,16] x2 -> fp32 [16,16,400] x2", lambda: mamba_controls(a_cols, d_cols, bias, 1e-4),
          rows * heads * (2 + 2 + 4 + 4)),
         ("masked_mean fp32 [16,400,512] -> [16,512]", lambda: masked_mean(x, lengths), rows * dim * 4 + b * dim * 4),
         ("mask_rows fp32 [6400,512]", lambda: mask_buffer(x, mask), rows * dim * 8 + rows),
         ("add fp32+bf16 -> fp32 [6400,512]", lambda: add(x, br, mask), rows * dim * (4 + 2 + 4) + rows),
+        ("mask_rms bf16 -> fp32,bf16 [6400,512]", lambda: mask_rms(br, mask, w), rows * dim * (2 + 4 + 2) + rows),
+        ("frame_audio fp32 [16,1,64000] -> bf16 [16,400,448]", lambda: frame_audio(audio, chans, 400, 160, 120, 448),
+         b * 64000 * 4 + rows * 448 * 2),
     ]
     out = []
     for name, fn, nbytes in cases:

@@ -215,6 +215,64 @@ int tf_mean_rmsnorm(const void *a, int32_t a_dtype, const void *b, int32_t b_dty
                     const float *w, float *y, int64_t rows, int64_t d, float eps,
                     void *stream);
 
+/*
+ * RMSNorm of a masked row, writing the masked row too:
+ *   s = mask[row] ? x : 0   (stored fp32),   y = rmsnorm(s) * w   (y_dtype)
+ * over contiguous [rows, d], d <= 4096; mask uint8 [rows] or NULL. The first
+ * residual of the encoder: the masked stem output (masking.py:10-11) and the
+ * first block's `_norm` MODE 0 (src/trifusion_l4/kernels/native.py:8-39) in one
+ * pass.
+ */
+int tf_mask_rmsnorm(const void *x, int32_t x_dtype, const uint8_t *mask, const float *w, float *s,
+                    void *y, int32_t y_dtype, int64_t rows, int64_t d, float eps, void *stream);
+
+/*
+ * Two RMSNorms per row: row r holds two groups of d elements at
+ * x + r * x_row_stride (0 = 2d); group g is normalised with w_g into the
+ * contiguous y[r, g, :]. The B and C norms of the Mamba-3 block
+ * (src/trifusion_l4/mamba.py:56-57: B_norm and C_norm over adjacent columns of
+ * the in-projection) in one launch instead of two.
+ */
+int tf_rmsnorm_pair(const void *x, int32_t x_dtype, int64_t x_row_stride, const float *w0,
+                    const float *w1, void *y, int32_t y_dtype, int64_t rows, int64_t d, float eps,
+                    void *stream);
+
+/*
+ * Channel mix and framing of the encoder's strided Conv1d stem: for audio fp32
+ * contiguous [B, C, N] and channels int64 [B],
+ *   mono[b, n] = sum_{c < min(channels[b], C)} audio[b, c, n] / channels[b],
+ *   framed[b, t, k] = bf16(mono[b, t*stride + k - pad]) for k < kernel (0 outside
+ *   [0, N)), and 0 for kernel <= k < width,
+ * into contiguous bf16 [B, frames, width] (width % 8 == 0, 16-byte aligned),
+ * frames = (N + 2 pad - kernel) / stride + 1. The stem is then one GEMM.
+ * No counterpart in the reference, whose front end is an STFT
+ * (src/trifusion_l4/front.py); this is the front of the benchmark encoder.
+ */
+int tf_frame_audio(const float *audio, const int64_t *channels, void *framed, int64_t batch,
+                   int64_t chans, int64_t samples, int64_t frames, int64_t kernel, int64_t width,
+                   int64_t stride, int64_t pad, void *stream);
+
+/*
+ * Valid frames and row mask from sample lengths:
+ *   frames[b] = clamp(floor(lengths[b] / stride), 1, T),  mask[b, t] = t < frames[b]
+ * (int64 [B] and uint8 [B, T]). The hop-count frame lengths the reference front
+ * end derives from sample lengths (src/trifusion_l4/front.py:62-67,90:
+ * floor division by the 160-sample hop) fused with time_mask
+ * (src/trifusion_l4/masking.py:6-7).
+ */
+int tf_frames_mask(const int64_t *lengths, int64_t stride, int64_t *frames, uint8_t *mask,
+                   int64_t batch, int64_t time, void *stream);
+
+/*
+ * Small bf16 linear layer on an fp32 input, as an autocast forward computes it:
+ *   y[b, o] = bf16(sum_k bf16(x[b, k]) * bf16(w[o, k]) + bf16(bias[o]))  (fp32 out)
+ * x fp32 [B, D], w [O, D] and bias [O] (or NULL) of w_dtype. One launch for the
+ * encoder head's cast, GEMM and cast; the reference's classifier heads are torch
+ * Linear layers under autocast (src/trifusion_l4/decoder.py).
+ */
+int tf_small_linear(const float *x, const void *w, const void *bias, int32_t w_dtype, float *y,
+                    int64_t batch, int64_t out_features, int64_t in_features, void *stream);
+
 /* Library version string (static storage). */
 const char *tf_version(void);
 

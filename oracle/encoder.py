@@ -34,6 +34,34 @@ def _linear(x, w, b=None):
     return _bf(y)
 
 
+def channel_mean(audio, channels):
+    """Mean over each clip's first ``channels[b]`` channels, fp32 ``[B, N]``."""
+    c = audio.shape[1]
+    chan = torch.arange(c)[None, :] < channels[:, None]
+    return (audio * chan[..., None]).sum(1) / channels[:, None].to(audio.dtype)
+
+
+def frame_audio(audio, channels, kernel, stride, pad, width=None):
+    """bf16 frames ``[B, T, width]`` of the zero-padded channel mean: frame t
+    holds samples ``t*stride - pad .. + kernel - 1``; columns past ``kernel``
+    are 0. The stem Conv1d is ``frame_audio(...) @ w.T``."""
+    mono = channel_mean(audio, channels)
+    framed = F.pad(mono, (pad, pad)).unfold(1, kernel, stride)
+    width = width or kernel
+    return F.pad(framed, (0, width - kernel)).to(BF16)
+
+
+def valid_frames(lengths, stride, time):
+    """``clamp(floor(lengths / stride), 1, time)``: frames of a clip at the
+    stem hop."""
+    return torch.div(lengths, stride, rounding_mode="floor").clamp(1, time)
+
+
+def small_linear(x, w, b=None):
+    """The autocast bf16 linear layer on an fp32 input, fp32 result."""
+    return _linear(x, w, None if b is None else b.to(BF16)).float()
+
+
 def mamba_block(sd, prefix, cfg, h, frames):
     d_inner = 2 * cfg.dim
     heads = d_inner // cfg.head_dim
@@ -66,13 +94,10 @@ def encoder_forward(sd, cfg, audio, lengths, channels):
     """Logits [B, num_outputs] (fp32) of the encoder with state dict ``sd``."""
     sd = {k: v.detach().cpu() for k, v in sd.items()}
     audio, lengths, channels = audio.cpu(), lengths.cpu(), channels.cpu()
-    b, c, _ = audio.shape
-    chan = torch.arange(c)[None, :] < channels[:, None]
-    mono = (audio * chan[..., None]).sum(1) / channels[:, None].to(audio.dtype)
-    framed = F.pad(mono, (cfg.stem_padding, cfg.stem_padding)).unfold(1, cfg.stem_kernel, cfg.stem_stride)
-    x = _linear(framed, sd["stem.weight"].reshape(cfg.dim, cfg.stem_kernel))
+    framed = frame_audio(audio, channels, cfg.stem_kernel, cfg.stem_stride, cfg.stem_padding)
+    x = _linear(framed.float(), sd["stem.weight"].reshape(cfg.dim, cfg.stem_kernel))
     t = x.shape[1]
-    frames = (lengths // cfg.stem_stride).clamp(1, t)
+    frames = valid_frames(lengths, cfg.stem_stride, t)
     mask = E.time_mask(frames, t)
     x = E.mask_rows(x.float(), mask)
     for i in range(cfg.depth):
@@ -91,4 +116,4 @@ def encoder_forward(sd, cfg, audio, lengths, channels):
         f = E.swiglu(g.to(BF16)).float()
         x = E.add(x, _linear(f, sd[pre + "down.weight"]), mask)
     pooled = E.masked_mean(x, frames)
-    return _linear(pooled, sd["head.weight"], sd["head.bias"].to(BF16)).float()
+    return small_linear(pooled, sd["head.weight"], sd["head.bias"])

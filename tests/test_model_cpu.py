@@ -60,3 +60,15 @@ def test_padded_in_projection_keeps_the_split():
     with torch.no_grad():
         m.in_proj.weight.add_(1)
     assert m._padded_in_proj() is not wp
+
+
+def test_padded_stem_weight():
+    from trifusion_amd.model import STEM_ALIGN
+
+    torch.manual_seed(3)
+    enc = Encoder(ModelConfig(depth=1)).eval()
+    c = enc.config
+    w = enc._stem_weight()
+    assert w.shape[1] % STEM_ALIGN == 0 and w.shape[1] >= c.stem_kernel
+    assert torch.equal(w[:, : c.stem_kernel], enc.stem.weight.reshape(c.dim, c.stem_kernel))
+    assert not w[:, c.stem_kernel :].any() and enc._stem_weight() is w

@@ -12,8 +12,9 @@ namespace {
 constexpr int kRowsPerBlock = 4;  // one wave64 per row
 
 // What the row norms normalise: x itself; the masked sum s = (x + b) * mask,
-// stored as it is normalised; or the mean of two directions (x + b) / 2.
-enum NormOp { kNormPlain = 0, kNormAdd = 1, kNormMean = 2 };
+// stored as it is normalised; the mean of two directions (x + b) / 2; or the
+// masked row s = x * mask, stored as it is normalised.
+enum NormOp { kNormPlain = 0, kNormAdd = 1, kNormMean = 2, kNormMask = 3 };
 
 // Eight consecutive elements through 16-byte accesses (two for fp32): a wave
 // moves 1-2 KB per load instruction instead of 128-256 B, which is what keeps
@@ -66,7 +67,7 @@ __global__ __launch_bounds__(256) void row_norm_vec_kernel(const TX* __restrict_
   const int lane = threadIdx.x & 63;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const bool keep = OP != kNormAdd || mask == nullptr || mask[row] != 0;
+  const bool keep = (OP != kNormAdd && OP != kNormMask) || mask == nullptr || mask[row] != 0;
   float v[PER8][8];
   float ss = 0.f;
 #pragma unroll
@@ -74,7 +75,7 @@ __global__ __launch_bounds__(256) void row_norm_vec_kernel(const TX* __restrict_
     const int i0 = 8 * (lane + 64 * j);
     if (i0 < d) {
       load8(x + row * x_stride + i0, v[j]);
-      if constexpr (OP != kNormPlain) {
+      if constexpr (OP == kNormAdd || OP == kNormMean) {
         float bv[8];
         load8(bsrc + row * d + i0, bv);
         if constexpr (OP == kNormAdd) {
@@ -85,6 +86,11 @@ __global__ __launch_bounds__(256) void row_norm_vec_kernel(const TX* __restrict_
 #pragma unroll
           for (int e = 0; e < 8; ++e) v[j][e] = (v[j][e] + bv[e]) * 0.5f;
         }
+      }
+      if constexpr (OP == kNormMask) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[j][e] = keep ? to_f32(from_f32<TS>(v[j][e])) : 0.f;
+        store8(s + row * d + i0, v[j]);
       }
     } else {
 #pragma unroll
@@ -118,7 +124,7 @@ __global__ __launch_bounds__(256) void row_norm_kernel(const TX* __restrict__ x,
   const int lane = threadIdx.x & 63;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
   if (row >= rows) return;
-  const bool keep = OP != kNormAdd || mask == nullptr || mask[row] != 0;
+  const bool keep = (OP != kNormAdd && OP != kNormMask) || mask == nullptr || mask[row] != 0;
   float v[PER];
   float ss = 0.f;
 #pragma unroll
@@ -134,6 +140,10 @@ __global__ __launch_bounds__(256) void row_norm_kernel(const TX* __restrict__ x,
         val = to_f32(stored);
       } else if constexpr (OP == kNormMean) {
         val = (val + to_f32(bsrc[row * d + i])) * 0.5f;
+      } else if constexpr (OP == kNormMask) {
+        const TS stored = from_f32<TS>(keep ? val : 0.f);
+        s[row * d + i] = stored;
+        val = to_f32(stored);
       }
     }
     v[j] = val;
@@ -154,7 +164,8 @@ int launch_row_norm(const void* x, int64_t x_stride, const void* bsrc, const uin
                     hipStream_t stream) {
   // 8-element vectors pay off once a row fills at least half a wave of them
   const bool vec = d >= 256 && d % 8 == 0 && x_stride % 8 == 0 && aligned16(x) && aligned16(w) &&
-                   aligned16(y) && (OP == kNormPlain || aligned16(bsrc)) && (OP != kNormAdd || aligned16(s));
+                   aligned16(y) && (OP == kNormPlain || OP == kNormMask || aligned16(bsrc)) &&
+                   ((OP != kNormAdd && OP != kNormMask) || aligned16(s));
   if (vec) {
     int per8 = 1;
     while (per8 * 512 < d) per8 <<= 1;
@@ -407,6 +418,62 @@ __global__ __launch_bounds__(256) void time_mask_kernel(const int64_t* __restric
   mask[i] = (i % time) < lengths[i / time] ? 1 : 0;
 }
 
+// Two RMSNorms per row, one wave per (row, group): group g of row r is the d
+// elements at x + r * x_stride + g * d, normalised with weight w_g into
+// y[(2 r + g) * d ...]. The B and C projections of the Mamba-3 block sit side
+// by side in the in-projection output, so both norms take one launch.
+template <typename TX, typename TY>
+__global__ __launch_bounds__(256) void pair_norm_kernel(const TX* __restrict__ x, int64_t x_stride,
+                                                        const float* __restrict__ w0, const float* __restrict__ w1,
+                                                        TY* __restrict__ y, int64_t rows, int d, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t vrow = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
+  if (vrow >= 2 * rows) return;
+  const int64_t row = vrow >> 1;
+  const int g = static_cast<int>(vrow & 1);
+  const TX* src = x + row * x_stride + g * d;
+  const float* w = g ? w1 : w0;
+  float ss = 0.f;
+  for (int i = lane; i < d; i += 64) {
+    const float v = to_f32(src[i]);
+    ss += v * v;
+  }
+  ss = wave_sum(ss);
+  const float r = rsqrtf(ss / static_cast<float>(d) + eps);
+  for (int i = lane; i < d; i += 64) y[vrow * d + i] = from_f32<TY>(to_f32(src[i]) * r * w[i]);
+}
+
+// The same through 8-element vectors for power-of-two d in [8, 256]: lane l of
+// a wave takes elements 8*(l % (2d/8)) .. +7 of row 256/d * wave + l / (2d/8),
+// so a wave moves 256/d whole rows (both groups) per 16-byte access instead of
+// one group per 2-byte access; the d/8 lanes of a group reduce by xor shuffles.
+template <typename TX, typename TY>
+__global__ __launch_bounds__(256) void pair_norm_vec_kernel(const TX* __restrict__ x, int64_t x_stride,
+                                                            const float* __restrict__ w0,
+                                                            const float* __restrict__ w1, TY* __restrict__ y,
+                                                            int64_t rows, int d, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int per_row = d / 4;  // lanes per row: 2d / 8
+  const int64_t row = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * (64 / per_row) + lane / per_row;
+  const int c = 8 * (lane % per_row);  // column within [group 0 | group 1]
+  const int g = c >= d;
+  float v[8];
+  float ss = 0.f;
+  if (row < rows) {
+    load8(x + row * x_stride + c, v);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += v[e] * v[e];
+  }
+  for (int off = 1; off < d / 8; off <<= 1) ss += __shfl_xor(ss, off);
+  if (row >= rows) return;
+  const float r = rsqrtf(ss / static_cast<float>(d) + eps);
+  float wv[8], o[8];
+  load8((g ? w1 : w0) + (c - g * d), wv);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = v[e] * r * wv[e];
+  store8(y + row * 2 * d + c, o);
+}
+
 // Valid-prefix reversal, one wave per (b, t) row moving U-sized units:
 // y[b, t] = x[b, L-1-t] for t < L, else 0 (primitives.py:40-47).
 template <typename U>
@@ -623,5 +690,50 @@ extern "C" int tf_mean_rmsnorm(const void* a, int32_t a_dtype, const void* b, in
               TF_DISPATCH(b_dtype, TB,
                           return (tf::launch_row_norm<TA, TB, float, float, tf::kNormMean>(
                               a, d, b, nullptr, w, nullptr, y, rows, static_cast<int>(d), eps, s))));
+  return TF_ERR_DTYPE;
+}
+
+extern "C" int tf_mask_rmsnorm(const void* x, int32_t x_dtype, const uint8_t* mask, const float* w, float* s,
+                               void* y, int32_t y_dtype, int64_t rows, int64_t d, float eps, void* stream) {
+  if (!x || !w || !s || !y) return TF_ERR_NULL;
+  if (rows < 0 || d < 1 || d > 4096) return TF_ERR_SHAPE;
+  if (rows == 0) return TF_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  TF_DISPATCH(x_dtype, TX,
+              TF_DISPATCH(y_dtype, TY,
+                          return (tf::launch_row_norm<TX, float, float, TY, tf::kNormMask>(
+                              x, d, nullptr, mask, w, s, y, rows, static_cast<int>(d), eps, st))));
+  return TF_ERR_DTYPE;
+}
+
+extern "C" int tf_rmsnorm_pair(const void* x, int32_t x_dtype, int64_t x_row_stride, const float* w0,
+                               const float* w1, void* y, int32_t y_dtype, int64_t rows, int64_t d, float eps,
+                               void* stream) {
+  if (!x || !w0 || !w1 || !y) return TF_ERR_NULL;
+  if (rows < 0 || d < 1 || d > 4096) return TF_ERR_SHAPE;
+  if (x_row_stride == 0) x_row_stride = 2 * d;
+  if (x_row_stride < 2 * d) return TF_ERR_STRIDE;
+  if (rows == 0) return TF_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool pow2 = d >= 8 && d <= 256 && (d & (d - 1)) == 0;
+  if (pow2 && x_row_stride % 8 == 0 && tf::aligned16(x) && tf::aligned16(y) && tf::aligned16(w0) &&
+      tf::aligned16(w1)) {
+    const int64_t rows_per_block = 4 * (256 / d);
+    const dim3 vgrid(tf::blocks_for(rows, static_cast<int>(rows_per_block))), vblock(256);
+    TF_DISPATCH(x_dtype, TX,
+                TF_DISPATCH(y_dtype, TY,
+                            hipLaunchKernelGGL((tf::pair_norm_vec_kernel<TX, TY>), vgrid, vblock, 0, st,
+                                               static_cast<const TX*>(x), x_row_stride, w0, w1,
+                                               static_cast<TY*>(y), rows, static_cast<int>(d), eps);
+                            return tf::launch_status()));
+    return TF_ERR_DTYPE;
+  }
+  const dim3 grid(tf::blocks_for(2 * rows, tf::kRowsPerBlock)), block(64 * tf::kRowsPerBlock);
+  TF_DISPATCH(x_dtype, TX,
+              TF_DISPATCH(y_dtype, TY,
+                          hipLaunchKernelGGL((tf::pair_norm_kernel<TX, TY>), grid, block, 0, st,
+                                             static_cast<const TX*>(x), x_row_stride, w0, w1,
+                                             static_cast<TY*>(y), rows, static_cast<int>(d), eps);
+                          return tf::launch_status()));
   return TF_ERR_DTYPE;
 }

@@ -92,6 +92,11 @@ _SIGNATURES = {
     "tf_time_mask": ([c_ptr, c_ptr, c_i64, c_i64, c_ptr], c_i32),
     "tf_reverse_valid": ([c_ptr, c_ptr, c_i32, c_ptr, c_i64, c_i64, c_i64, c_ptr], c_i32),
     "tf_mean_rmsnorm": ([c_ptr, c_i32, c_ptr, c_i32, c_ptr, c_ptr, c_i64, c_i64, c_f32, c_ptr], c_i32),
+    "tf_mask_rmsnorm": ([c_ptr, c_i32, c_ptr, c_ptr, c_ptr, c_ptr, c_i32, c_i64, c_i64, c_f32, c_ptr], c_i32),
+    "tf_rmsnorm_pair": ([c_ptr, c_i32, c_i64, c_ptr, c_ptr, c_ptr, c_i32, c_i64, c_i64, c_f32, c_ptr], c_i32),
+    "tf_frame_audio": ([c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_ptr], c_i32),
+    "tf_frames_mask": ([c_ptr, c_i64, c_ptr, c_ptr, c_i64, c_i64, c_ptr], c_i32),
+    "tf_small_linear": ([c_ptr, c_ptr, c_ptr, c_i32, c_ptr, c_i64, c_i64, c_i64, c_ptr], c_i32),
     "tf_version": ([], ctypes.c_char_p),
 }
 

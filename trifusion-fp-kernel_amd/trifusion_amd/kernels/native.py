@@ -175,6 +175,58 @@ def launch_mean_rms(a, b, weight, eps=1e-5):
     return y
 
 
+def mask_rms(x, mask, weight, eps=1e-5, out_dtype=torch.bfloat16):
+    """``s = x`` with rows whose mask is false set to 0 (fp32) and ``y = rms(s,
+    weight)`` (``out_dtype``) in one pass (``trifusion_amd::mask_rms_norm``)."""
+    return ops.mask_rms_norm(x, mask, weight, eps, out_dtype)
+
+
+def launch_mask_rms(x, mask, weight, eps=1e-5, out_dtype=torch.bfloat16):
+    lib = _lib.load()
+    _lib.require_cuda(x, mask, weight, what="mask_rms")
+    x = x.contiguous()
+    d = x.shape[-1]
+    if weight.shape != (d,) or weight.dtype != torch.float32:
+        raise ValueError(f"mask_rms: weight must be float32 [{d}]")
+    rows = x.numel() // d if d else 0
+    s = torch.empty(x.shape, device=x.device, dtype=torch.float32)
+    y = torch.empty(x.shape, device=x.device, dtype=out_dtype or torch.bfloat16)
+    status = lib.tf_mask_rmsnorm(
+        x.data_ptr(), _lib.dtype_code(x, "mask_rms"), _mask_ptr(mask, rows), weight.contiguous().data_ptr(),
+        s.data_ptr(), y.data_ptr(), _lib.dtype_code(y, "mask_rms"), rows, d, float(eps), _lib.stream_of(x),
+    )
+    _lib.check(status, "mask_rms")
+    return s, y
+
+
+def rms_pair(x, w0, w1, eps=1e-5):
+    """Two RMSNorms per row of ``x`` ``[..., 2d]``: the first ``d`` columns with
+    ``w0``, the last ``d`` with ``w1``; returns contiguous ``[..., 2, d]`` in x's
+    dtype (``trifusion_amd::rms_norm_pair``). Rows may sit at any stride."""
+    return ops.rms_norm_pair(x, w0, w1, eps)
+
+
+def launch_rms_pair(x, w0, w1, eps=1e-5):
+    lib = _lib.load()
+    _lib.require_cuda(x, w0, w1, what="rms_pair")
+    two_d = x.shape[-1]
+    if two_d % 2:
+        raise ValueError("rms_pair: last dim must be even")
+    d = two_d // 2
+    for w in (w0, w1):
+        if w.shape != (d,) or w.dtype != torch.float32 or not w.is_contiguous():
+            raise ValueError(f"rms_pair: weights must be contiguous float32 [{d}]")
+    xv, row_stride = _row_view(x)
+    rows = x.numel() // two_d if two_d else 0
+    y = torch.empty((*x.shape[:-1], 2, d), device=x.device, dtype=x.dtype)
+    status = lib.tf_rmsnorm_pair(
+        xv.data_ptr(), _lib.dtype_code(xv, "rms_pair"), row_stride, w0.data_ptr(), w1.data_ptr(), y.data_ptr(),
+        _lib.dtype_code(y, "rms_pair"), rows, d, float(eps), _lib.stream_of(x),
+    )
+    _lib.check(status, "rms_pair")
+    return y
+
+
 def _mask_ptr(mask, rows):
     if mask is None:
         return None

@@ -24,6 +24,7 @@ import torch.nn.functional as F
 from torch import nn
 
 from .kernels import RMSNorm
+from .kernels.native import rms_pair
 from .kernels.buffers import mamba_controls
 from .mamba_fused import fused_mamba
 
@@ -99,8 +100,15 @@ class Mamba3Inference(nn.Module):
         width = self.in_proj.out_features
         p = F.linear(u, self._padded_in_proj())[..., :width]
         z, v, k, q, ddt, a, trap, angles = self.split(p)
-        q = self.C_norm(q.reshape(b, t, 1, self.d_state))
-        k = self.B_norm(k.reshape(b, t, 1, self.d_state))
+        if self.B_norm.eps == self.C_norm.eps:
+            # B and C sit side by side in the projection: both norms, one launch
+            n = self.d_state
+            kq = p[..., 2 * self.d_inner : 2 * self.d_inner + 2 * n]
+            y = rms_pair(kq, self.B_norm.weight, self.C_norm.weight, self.B_norm.eps)
+            k, q = y[:, :, 0:1], y[:, :, 1:2]
+        else:
+            q = self.C_norm(q.reshape(b, t, 1, self.d_state))
+            k = self.B_norm(k.reshape(b, t, 1, self.d_state))
         if self.fuse_controls and self.dt_bias.dtype == torch.float32:
             adt, dt = a.transpose(1, 2), ddt.transpose(1, 2)
             raw = {"dt_bias": self.dt_bias, "a_floor": self.A_floor}

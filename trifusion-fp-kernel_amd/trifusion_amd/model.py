@@ -29,9 +29,10 @@ import torch.nn.functional as F
 from torch import nn
 
 from .kernels import RMSNorm, swiglu
-from .kernels.native import add, add_rms, mean_norm, rms
+from .kernels.native import add, add_rms, mask_rms, mean_norm
 from .mamba import Mamba3Inference
-from .masking import masked, masked_mean, time_mask
+from .masking import masked_mean
+from .stem import frame_audio, frames_mask, small_linear
 
 
 @dataclass
@@ -51,6 +52,7 @@ class ModelConfig:
 
 
 FFN_ALIGN = 64  # FFN width the GEMMs and SwiGLU run at (each half zero-padded up to it)
+STEM_ALIGN = 64  # stem GEMM depth: the frame width, zero columns past the kernel
 
 
 class EncoderBlock(nn.Module):
@@ -103,6 +105,8 @@ class Encoder(nn.Module):
         self.stem = nn.Conv1d(1, c.dim, c.stem_kernel, stride=c.stem_stride, padding=c.stem_padding, bias=False)
         self.blocks = nn.ModuleList([EncoderBlock(c) for _ in range(c.depth)])
         self.head = nn.Linear(c.dim, c.num_outputs)
+        self._stem_w = None
+        self._stem_key = None
         self.reset_parameters()
 
     def reset_parameters(self):
@@ -122,25 +126,38 @@ class Encoder(nn.Module):
         """Valid frames per clip: floor(len / stride) for the padded stem, in [1, time]."""
         return (lengths // self.config.stem_stride).clamp(1, time)
 
-    def stem_forward(self, audio, channels):
-        """Channel mix then the strided Conv1d stem as one GEMM over framed audio."""
-        b, c, n = audio.shape
-        chan = torch.arange(c, device=audio.device)[None, :] < channels[:, None]
-        mono = (audio * chan[..., None]).sum(1) / channels[:, None].to(audio.dtype)
+    def _stem_weight(self):
+        """The stem kernel as a [dim, width] GEMM weight, zero columns from
+        stem_kernel up to a multiple of STEM_ALIGN (400 -> 448: the library GEMM
+        runs K = 448 faster than K = 400); rebuilt when the weight changes."""
         cfg = self.config
-        pad = F.pad(mono, (cfg.stem_padding, cfg.stem_padding))
-        framed = pad.unfold(1, cfg.stem_kernel, cfg.stem_stride)  # [B, T, K] view
-        w = self.stem.weight.reshape(cfg.dim, cfg.stem_kernel)
+        w = self.stem.weight
+        key = (w.data_ptr(), w._version, w.dtype, w.device)
+        if self._stem_key != key:
+            width = -(-cfg.stem_kernel // STEM_ALIGN) * STEM_ALIGN
+            with torch.no_grad():
+                wp = w.new_zeros(cfg.dim, width)
+                wp[:, : cfg.stem_kernel] = w.reshape(cfg.dim, cfg.stem_kernel)
+            self._stem_w, self._stem_key = wp, key
+        return self._stem_w
+
+    def stem_forward(self, audio, channels):
+        """Channel mix and framing in one kernel (bf16 frames of the zero-padded
+        channel mean, zero columns up to the padded weight's width), then the
+        strided Conv1d stem as one GEMM."""
+        cfg = self.config
+        w = self._stem_weight()
+        framed = frame_audio(audio.float(), channels.to(torch.int64), cfg.stem_kernel, cfg.stem_stride,
+                             cfg.stem_padding, w.shape[1])
         return F.linear(framed.to(w.dtype), w)  # [B, T, dim]
 
     def encode(self, audio, lengths, channels):
         x = self.stem_forward(audio, channels)
         b, t, _ = x.shape
-        frames = self.frames(lengths, t)
-        mask = time_mask(frames, t)
-        x = masked(x.float().contiguous(), mask)
+        frames, mask = frames_mask(lengths, self.config.stem_stride, t)
         blocks = self.blocks
-        h = rms(x, blocks[0].pre.weight, blocks[0].pre.eps, out_dtype=torch.bfloat16)
+        # masked fp32 residual and the first block's normalised input, one pass
+        x, h = mask_rms(x, mask, blocks[0].pre.weight, blocks[0].pre.eps)
         for i, blk in enumerate(blocks):
             m = blk.mamba(h, frames)
             if blk.mamba_bwd is not None:
@@ -159,5 +176,8 @@ class Encoder(nn.Module):
     def forward(self, audio, lengths, channels):
         x, frames = self.encode(audio, lengths, channels)
         pooled = masked_mean(x, frames)
-        logits = self.head(pooled.to(self.head.weight.dtype)).float()
+        if self.head.weight.dtype == torch.bfloat16:
+            logits = small_linear(pooled, self.head.weight, self.head.bias)
+        else:
+            logits = self.head(pooled.to(self.head.weight.dtype)).float()
         return {"logits": logits, "embedding": pooled}

@@ -40,6 +40,12 @@ _SCHEMAS = {
     "time_mask": "time_mask(Tensor lengths, int time) -> Tensor",
     "reverse_valid": "reverse_valid(Tensor x, Tensor lengths) -> Tensor",
     "mean_rms_norm": "mean_rms_norm(Tensor a, Tensor b, Tensor weight, float eps=1e-05) -> Tensor",
+    "mask_rms_norm": "mask_rms_norm(Tensor x, Tensor mask, Tensor weight, float eps=1e-05, "
+    "ScalarType? out_dtype=None) -> (Tensor, Tensor)",
+    "rms_norm_pair": "rms_norm_pair(Tensor x, Tensor w0, Tensor w1, float eps=1e-05) -> Tensor",
+    "frame_audio": "frame_audio(Tensor audio, Tensor channels, int kernel, int stride, int pad, int width) -> Tensor",
+    "frames_mask": "frames_mask(Tensor lengths, int stride, int time) -> (Tensor, Tensor)",
+    "small_linear": "small_linear(Tensor x, Tensor weight, Tensor? bias=None) -> Tensor",
 }
 
 OPERATORS = tuple(_SCHEMAS)
@@ -123,6 +129,36 @@ def _cuda_mean_rms_norm(a, b, weight, eps=1e-5):
     return launch_mean_rms(a, b, weight, eps)
 
 
+def _cuda_mask_rms_norm(x, mask, weight, eps=1e-5, out_dtype=None):
+    from .kernels.native import launch_mask_rms
+
+    return launch_mask_rms(x, mask, weight, eps, out_dtype or torch.bfloat16)
+
+
+def _cuda_rms_norm_pair(x, w0, w1, eps=1e-5):
+    from .kernels.native import launch_rms_pair
+
+    return launch_rms_pair(x, w0, w1, eps)
+
+
+def _cuda_frame_audio(audio, channels, kernel, stride, pad, width):
+    from .stem import launch_frame_audio
+
+    return launch_frame_audio(audio, channels, kernel, stride, pad, width)
+
+
+def _cuda_frames_mask(lengths, stride, time):
+    from .stem import launch_frames_mask
+
+    return launch_frames_mask(lengths, stride, time)
+
+
+def _cuda_small_linear(x, weight, bias=None):
+    from .stem import launch_small_linear
+
+    return launch_small_linear(x, weight, bias)
+
+
 # ---- Meta kernels: output shapes and dtypes only ----
 
 
@@ -177,6 +213,28 @@ def _meta_mean_rms_norm(a, b, weight, eps=1e-5):
     return a.new_empty(a.shape, dtype=torch.float32)
 
 
+def _meta_mask_rms_norm(x, mask, weight, eps=1e-5, out_dtype=None):
+    return x.new_empty(x.shape, dtype=torch.float32), x.new_empty(x.shape, dtype=out_dtype or torch.bfloat16)
+
+
+def _meta_rms_norm_pair(x, w0, w1, eps=1e-5):
+    return x.new_empty((*x.shape[:-1], 2, x.shape[-1] // 2))
+
+
+def _meta_frame_audio(audio, channels, kernel, stride, pad, width):
+    b, _, n = audio.shape
+    return audio.new_empty((b, (n + 2 * pad - kernel) // stride + 1, width), dtype=torch.bfloat16)
+
+
+def _meta_frames_mask(lengths, stride, time):
+    b = lengths.shape[0]
+    return lengths.new_empty((b,), dtype=torch.int64), lengths.new_empty((b, time), dtype=torch.bool)
+
+
+def _meta_small_linear(x, weight, bias=None):
+    return x.new_empty((x.shape[0], weight.shape[0]), dtype=torch.float32)
+
+
 # ---- CPU kernels: loud failure, no fallback ----
 
 
@@ -203,6 +261,11 @@ _KERNELS = {
     "time_mask": (_cuda_time_mask, _meta_time_mask),
     "reverse_valid": (_cuda_reverse_valid, _meta_reverse_valid),
     "mean_rms_norm": (_cuda_mean_rms_norm, _meta_mean_rms_norm),
+    "mask_rms_norm": (_cuda_mask_rms_norm, _meta_mask_rms_norm),
+    "rms_norm_pair": (_cuda_rms_norm_pair, _meta_rms_norm_pair),
+    "frame_audio": (_cuda_frame_audio, _meta_frame_audio),
+    "frames_mask": (_cuda_frames_mask, _meta_frames_mask),
+    "small_linear": (_cuda_small_linear, _meta_small_linear),
 }
 
 _LIBRARY = torch.library.Library(NAMESPACE, "DEF")
