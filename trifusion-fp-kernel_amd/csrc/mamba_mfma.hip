@@ -434,6 +434,11 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
 
   lds_barrier();
 
+  // Half 0's q/k/v rows of the next super-chunk, issued before the output phase
+  // of this one (the output phase covers their latency; the live range is short
+  // enough to cost two registers). Half 1 keeps loading its rows after phase
+  // pass 1, which staggers the two halves' bursts.
+  HalfRows<KS, PS> pre = {};
   for (int g0 = c_begin; g0 < c_stop; g0 += CW) {
     // Lane-derived indices are rebuilt from an index the compiler cannot see
     // through each iteration: hoisted out of the loop, the dozens of per-lane
@@ -459,7 +464,12 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
     // pass 1. Load issue stalls while the chip-wide burst drains; staggered, one
     // wave of each SIMD computes while the other waits.
     HalfRows<KS, PS> rows = {};
-    if (active && hf == 0) load_rows<MODE == 0>(P, rows, qbase, kbase, vbase, t0, t, L, hh);
+    if (active && hf == 0) {
+      if (g0 == c_begin)
+        load_rows<MODE == 0>(P, rows, qbase, kbase, vbase, t0, t, L, hh);
+      else
+        rows = pre;
+    }
     u32x4 (&q)[KS] = rows.q;
     u32x4 (&k)[KS] = rows.k;
     u32x4 (&v)[PS] = rows.v;
@@ -756,6 +766,11 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
       }
     }
     lds_barrier();  // barrier 4: exclusive states in LDS
+    pre = {};
+    if (hf == 0 && g0 + CW + cw < c_stop) {
+      const int t0n = (g0 + CW + cw) * kChunk;
+      load_rows<MODE == 0>(P, pre, qbase, kbase, vbase, t0n, t0n + c32, L, hh);
+    }
 
     // ---------------- inter-chunk term, gate, store ----------------
     if (MODE == 0 && active) {
