@@ -270,7 +270,8 @@ def main():
     if args.gpus != 1:
         print(
             f"bench.py runs on one GPU only: --gpus {args.gpus} is not supported "
-            "(the fused recurrence shards over (batch, head) units without collectives; see DESIGN.md)",
+            "(this build measures one GPU; the fused recurrence would shard over (batch, head) units "
+            "without collectives)",
             file=sys.stderr,
         )
         sys.exit(2)
