@@ -270,7 +270,7 @@ def main():
     if args.gpus != 1:
         print(
             f"bench.py runs on one GPU only: --gpus {args.gpus} is not supported "
-            "(this build measures one GPU; the fused recurrence would shard over (batch, head) units "
+            "(the benchmark measures one GPU; the fused recurrence would shard over (batch, head) units "
             "without collectives)",
             file=sys.stderr,
         )
