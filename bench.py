@@ -5,7 +5,10 @@ N=64 (R=16, Hq=1; bf16 x/B/C/z, fp32 dt/adt/trap/angles), synthetic seeded
 inputs resident in HBM. A step is one call over the batch; the timed region
 replays a HIP graph holding ``--steps`` back-to-back calls so host dispatch does
 not stall the GPU between calls, bracketed by device synchronisation and timed
-with HIP events on the launch stream.
+with HIP events on the launch stream. The calls cycle through copies of the
+inputs (each with its own output) whose total exceeds twice the 256 MB
+last-level cache, so every call reads its operands from HBM; the single-set,
+cache-warm time is reported beside it.
 
 Printed as one JSON line: ``value`` is the algorithmic GB/s (unique input bytes +
 output bytes per call / average call time), ``roofline`` compares it with the
@@ -28,6 +31,7 @@ for _p in (ROOT, ROOT / "trifusion-fp-kernel_amd"):
         sys.path.insert(0, str(_p))
 
 HBM_PEAK_GBS = 8000.0
+LLC_BYTES = 256 * 2**20  # MI355X last-level (Infinity) cache
 WORKLOAD = dict(batch=16, time=400, heads=16, head_dim=64, state=64, rotary=16, qk_heads=1)
 # other workloads are parity-test shapes; --workload times one of them instead
 WORKLOADS = {
@@ -57,6 +61,11 @@ def parse_args():
     p.add_argument("--workload", default="clip", choices=sorted(WORKLOADS),
                    help="shape to time (clip: the headline B16 L400 workload)")
     p.add_argument("--eager", action="store_true", help="time Python-dispatched calls instead of graph replay")
+    p.add_argument("--sets", type=int, default=0,
+                   help="input sets the timed calls cycle through (0: enough to exceed twice the 256 MB "
+                   "last-level cache, so operands come from HBM; 1: one set, cache-warm)")
+    p.add_argument("--no-warm", action="store_true",
+                   help="skip the single-set cache-warm timing (profiling aid: only cache-cold calls)")
     p.add_argument(
         "--calibrate-copy",
         type=int,
@@ -88,20 +97,26 @@ def traffic_bytes():
     return None
 
 
-def time_fused_mamba(args, torch, fused_mamba, dargs, steps, warmup, variant, eager, lengths=None):
+def time_fused_mamba(args, torch, fused_mamba, sets, steps, warmup, variant, eager, lengths=None):
+    """Average ms per call; call i reads input set i % len(sets) and writes its
+    own output, so with enough sets no call finds its operands in the caches."""
     stream = torch.cuda.current_stream()
     with torch.inference_mode():
-        out = torch.empty_like(dargs[2])
-        for _ in range(warmup):
-            fused_mamba(*dargs, out=out, variant=variant, lengths=lengths)
+        outs = [torch.empty_like(d[2]) for d in sets]
+
+        def call(i):
+            fused_mamba(*sets[i % len(sets)], out=outs[i % len(sets)], variant=variant, lengths=lengths)
+
+        for i in range(warmup):
+            call(i)
         torch.cuda.synchronize()
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
         if eager:
             torch.cuda.synchronize()
             start.record(stream)
-            for _ in range(steps):
-                fused_mamba(*dargs, out=out, variant=variant, lengths=lengths)
+            for i in range(steps):
+                call(i)
             end.record(stream)
             torch.cuda.synchronize()
             return start.elapsed_time(end) / steps
@@ -110,8 +125,8 @@ def time_fused_mamba(args, torch, fused_mamba, dargs, steps, warmup, variant, ea
         side.wait_stream(stream)
         with torch.cuda.stream(side):
             with torch.cuda.graph(graph, stream=side):
-                for _ in range(steps):
-                    fused_mamba(*dargs, out=out, variant=variant, lengths=lengths)
+                for i in range(steps):
+                    call(i)
         stream.wait_stream(side)
         graph.replay()  # warm replay
         torch.cuda.synchronize()
@@ -301,8 +316,15 @@ def main():
         lengths = clip_lengths(w["batch"], w["time"], varlen[0], seed=varlen[1]).cuda()
     nbytes = algorithmic_bytes(host, lengths=None if lengths is None else lengths.cpu())
     kernel = selected_variant(*dargs, variant=args.variant)
-    ms = time_fused_mamba(args, torch, fused_mamba, dargs, args.steps, args.warmup, args.variant, args.eager,
+    nsets = args.sets or max(1, -(-2 * LLC_BYTES // nbytes))
+    sets = [dargs] + [tuple(x.clone() for x in dargs) for _ in range(nsets - 1)]
+    ms = time_fused_mamba(args, torch, fused_mamba, sets, args.steps, args.warmup, args.variant, args.eager,
                           lengths)
+    warm_ms = None
+    if nsets > 1 and not args.no_warm:
+        warm_ms = time_fused_mamba(args, torch, fused_mamba, [dargs], args.steps, args.warmup, args.variant,
+                                   args.eager, lengths)
+    del sets
     gbs = nbytes / (ms * 1e-3) / 1e9
     line = {
         "metric": METRIC,
@@ -320,7 +342,9 @@ def main():
         "config": {
             "workload": label,
             "kernel": kernel,
-            "timing": "eager calls" if args.eager else f"HIP graph of {args.steps} calls, HIP events on the launch stream",
+            "timing": ("eager calls" if args.eager else f"HIP graph of {args.steps} calls, HIP events on the launch stream")
+            + f", cycling through {nsets} input sets ({nsets * nbytes / 2**20:.0f} MiB)",
+            "cache_warm_ms_per_step": None if warm_ms is None else round(warm_ms, 6),
             "algorithmic_bytes_per_call": nbytes,
             **w,
         },
