@@ -273,6 +273,85 @@ int tf_frames_mask(const int64_t *lengths, int64_t stride, int64_t *frames, uint
 int tf_small_linear(const float *x, const void *w, const void *bias, int32_t w_dtype, float *y,
                     int64_t batch, int64_t out_features, int64_t in_features, void *stream);
 
+/* ---- Kernels of the TriFusion block and front end (reference model path) ---- */
+
+/*
+ * Masked depthwise convolution over time, "same" padding:
+ *   y[b, t, c] = t < L_b ? sum_k x[b, t + k - K/2, c] * w[c, k] + bias[c] : 0
+ * (sources outside [0, T) read 0; fp32 products and sums, each rounded; stored
+ * in dtype). x, y contiguous [B, T, D]; w [D, K] (the Conv1d weight [D, 1, K]),
+ * bias [D], both of dtype. Replaces depthwise_masked/_dw_forward
+ * (src/trifusion_l4/kernels/buffers.py:13-32, kernels/primitives.py:74-88).
+ */
+int tf_depthwise_masked(const void *x, const void *w, const void *bias, int32_t dtype,
+                        const int64_t *lengths, void *y, int64_t batch, int64_t time, int64_t d,
+                        int64_t k, void *stream);
+
+/*
+ * 4:1 masked average over time: y[b, j, c] = sum_{k<4, 4j+k < L_b} x[b, 4j+k, c] /
+ * max(min(L_b - 4j, 4), 1), y contiguous [B, ceil(T/4), D]. Replaces Pool4
+ * (src/trifusion_l4/kernels/buffers.py:35-44, kernels/primitives.py:91-114).
+ */
+int tf_pool4(const void *x, int32_t dtype, const int64_t *lengths, void *y, int64_t batch, int64_t time,
+             int64_t d, void *stream);
+
+/*
+ * Rotary Q/K/V packing: x contiguous [B, T, 3 H D] -> y [3, B, H, T, D]; for q and
+ * k each interleaved pair (a, z) becomes (a cos - z sin, a sin + z cos) with
+ * cos/sin fp32 [T, D/2]; v is copied. Replaces RotaryQKV/_rotary_qkv
+ * (src/trifusion_l4/kernels/buffers.py:46-56, kernels/primitives.py:117-151).
+ */
+int tf_rotary_qkv(const void *x, int32_t dtype, const float *cos_t, const float *sin_t, void *y,
+                  int64_t batch, int64_t time, int64_t heads, int64_t head_dim, void *stream);
+
+/*
+ * Channel RMSNorm of a [B, C, T, F] map with element strides strides[4], written
+ * contiguous [B, T, F, C]: rows with t >= L_b are 0; y = round(x r w) and, when
+ * silu is non-zero, y * sigmoid(y) (C <= 256). Replaces front_norm/_front_norm
+ * (src/trifusion_l4/kernels/buffers.py:58-80, kernels/primitives.py:154-188).
+ */
+int tf_front_norm(const void *x, int32_t dtype, const int64_t *strides, const float *w,
+                  const int64_t *lengths, void *y, int64_t batch, int64_t chans, int64_t time,
+                  int64_t freq, float eps, int32_t silu, void *stream);
+
+/*
+ * Linear interpolation from the pooled grid back to frames:
+ *   y[b, t, c] = t < L_b ? a + (z - a) * alpha[b, t] : 0,
+ *   a = low[b, left[b, t], c], z = low[b, right[b, t], c]
+ * low [B, LT, D], left/right int64 [B, T], alpha fp32 [B, T], y [B, T, D].
+ * Replaces interpolate/_interpolate (src/trifusion_l4/kernels/native.py:104-133).
+ */
+int tf_interpolate(const void *low, int32_t dtype, const int64_t *left, const int64_t *right,
+                   const float *alpha, const int64_t *lengths, void *y, int64_t batch, int64_t time,
+                   int64_t low_time, int64_t d, void *stream);
+
+/*
+ * Eight frequency bands of a [B, C, T, F] map (strides[4]), written contiguous
+ * [B, T, 8, C]: band i averages frequencies floor(i F/8) .. ceil((i+1) F/8) - 1,
+ * the adaptive average pool of src/trifusion_l4/front.py:94-101. Replaces
+ * bands/_bands (src/trifusion_l4/kernels/native.py:142-163). F >= 8.
+ */
+int tf_bands(const void *x, int32_t dtype, const int64_t *strides, void *y, int64_t batch, int64_t chans,
+             int64_t time, int64_t freq, void *stream);
+
+/*
+ * Evidence-gated RMSNorm: s = mask[r] ? x + a * 2 sigmoid(g) : 0 (fp32),
+ * y = s rsqrt(mean(s^2) + eps) w (fp32); x fp32, a and g of ag_dtype, all
+ * contiguous [rows, d]; mask uint8 [rows] or NULL. Replaces evidence_norm
+ * (`_norm` MODE 1, src/trifusion_l4/kernels/native.py:9-39,73-74).
+ */
+int tf_evidence_norm(const float *x, const void *a, const void *g, int32_t ag_dtype, const uint8_t *mask,
+                     const float *w, float *y, int64_t rows, int64_t d, float eps, void *stream);
+
+/*
+ * Sigmoid-gated concatenation: y[r, k d + j] = x[r, k d + j] * 2 sigmoid(gate[r, k])
+ * for the three branches k < 3; x, y [rows, 3 d], gate [rows, 3], one dtype.
+ * Replaces gated_concat/_gate (src/trifusion_l4/kernels/__init__.py:58-82,
+ * kernels/primitives.py:51-63).
+ */
+int tf_gated_concat(const void *x, const void *gate, int32_t dtype, void *y, int64_t rows, int64_t d,
+                    void *stream);
+
 /* Library version string (static storage). */
 const char *tf_version(void);
 

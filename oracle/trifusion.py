@@ -1,0 +1,107 @@
+"""CPU restatements of the TriFusion block and front-end kernels (oracle).
+
+Test infrastructure only (see ``oracle/__init__.py``). Each function restates
+the reference model's unfused PyTorch formulation, which its fused kernels
+replace:
+
+* ``depthwise_masked``: ``masked(merge_dw(v.transpose(1, 2)).transpose(1, 2))``
+  (``src/trifusion_l4/model.py:188-190``), a grouped ``F.conv1d``;
+* ``pool4`` and ``interpolate``: ``Grids.pool`` / ``Grids.interpolate``
+  (``src/trifusion_l4/masking.py:59-80``) on grids built as ``Grids.make``
+  builds them (``:29-57``);
+* ``rotary_qkv``: the reference branch of ``GlobalAttention`` with ``rope``
+  (``src/trifusion_l4/model.py:40-48,84-89``);
+* ``front_norm``: the unfused CNN-stage norm ``silu(norm(clean(h)))``
+  (``src/trifusion_l4/front.py:36-37``) with the RMSNorm output in the
+  activation dtype;
+* ``bands``: ``adaptive_avg_pool2d`` over frequency (``front.py:94-101``);
+* ``evidence_norm``: ``masked(u_norm(x + value * 2 sigmoid(gate)))``
+  (``src/trifusion_l4/model.py:166-167``);
+* ``gated_concat``: the reference branch (``kernels/__init__.py:59-63``).
+
+Pinning (tests/test_oracle_trifusion.py): each against an explicit loop or
+closed form on small inputs.
+"""
+
+import torch
+import torch.nn.functional as F
+
+from .elementwise import mask_rows, time_mask
+
+
+def depthwise_masked(x, weight, bias, lengths):
+    """``[B, T, D]`` masked depthwise conv, same padding, fp32 math, x's dtype."""
+    d, k = x.shape[-1], weight.shape[-1]
+    y = F.conv1d(x.float().transpose(1, 2), weight.float().reshape(d, 1, k), bias.float(), padding=k // 2, groups=d)
+    return mask_rows(y.transpose(1, 2), time_mask(lengths, x.shape[1])).to(x.dtype)
+
+
+def grids(lengths, time):
+    """``low_lengths``, ``left``, ``right``, ``alpha`` of the 4:1 attention grid
+    (``masking.py:29-41``)."""
+    low_lengths = (lengths + 3) // 4
+    pos = torch.arange(time)[None, :].float() + 0.5
+    pos = (pos * low_lengths[:, None] / lengths[:, None] - 0.5).clamp_min(0)
+    pos = torch.minimum(pos, (low_lengths - 1)[:, None])
+    left = pos.long()
+    right = torch.minimum(left + 1, (low_lengths - 1)[:, None])
+    return low_lengths, left, right, pos - left
+
+
+def pool4(x, lengths):
+    """Masked 4:1 time average; the last partial group divided by its valid count."""
+    b, t, d = x.shape
+    mask = time_mask(lengths, t)
+    xp = F.pad(mask_rows(x, mask), (0, 0, 0, (-t) % 4))
+    mp = F.pad(mask, (0, (-t) % 4)).view(b, -1, 4)
+    y = xp.float().view(b, -1, 4, d).sum(2) / mp.sum(2).clamp_min(1)[..., None]
+    return y.to(x.dtype)
+
+
+def interpolate(low, left, right, alpha, lengths):
+    """Linear interpolation of the pooled grid back to frames, masked rows 0."""
+    shape = (*left.shape, low.shape[-1])
+    a = low.gather(1, left[..., None].expand(shape))
+    b = low.gather(1, right[..., None].expand(shape))
+    y = a.float() + (b.float() - a.float()) * alpha[..., None]
+    return mask_rows(y.to(low.dtype), time_mask(lengths, left.shape[1]))
+
+
+def rotary_qkv(x, cos, sin, heads):
+    """``[B, T, 3 H D]`` -> ``[3, B, H, T, D]``, q and k rotated by interleaved
+    pairs with the [T, D/2] tables, v unchanged."""
+    b, t, width = x.shape
+    d = width // (3 * heads)
+    qkv = x.view(b, t, 3, heads, d).permute(2, 0, 3, 1, 4)
+    a, z = qkv.float().reshape(3, b, heads, t, d // 2, 2).unbind(-1)
+    rot = torch.stack((a * cos - z * sin, a * sin + z * cos), -1).flatten(-2).to(x.dtype)
+    return torch.stack((rot[0], rot[1], qkv[2]))
+
+
+def front_norm(x, lengths, weight, eps=1e-5, silu=False):
+    """``[B, C, T, F]`` -> ``[B, T, F, C]``: rows past the length cleared, RMSNorm
+    over channels rounded to x's dtype, then SiLU when asked."""
+    b, c, t, f = x.shape
+    clean = x.masked_fill(~time_mask(lengths, t)[:, None, :, None], 0)
+    h = clean.permute(0, 2, 3, 1).float()
+    y = (h * torch.rsqrt(h.square().mean(-1, keepdim=True) + eps) * weight.float()).to(x.dtype)
+    return F.silu(y.float()).to(x.dtype) if silu else y
+
+
+def bands(x):
+    """``[B, C, T, F]`` -> ``[B, T, 8, C]`` adaptive frequency average."""
+    return F.adaptive_avg_pool2d(x.float(), (x.shape[2], 8)).to(x.dtype).permute(0, 2, 3, 1).contiguous()
+
+
+def evidence_norm(x, value, gate, weight, mask, eps=1e-5):
+    """fp32 ``rms(mask ? x + value * 2 sigmoid(gate) : 0) * weight``."""
+    s = x.float() + value.float() * (2 * torch.sigmoid(gate.float()))
+    y = s * torch.rsqrt(s.square().mean(-1, keepdim=True) + eps) * weight.float()
+    return y if mask is None else mask_rows(y, mask)
+
+
+def gated_concat(x, gate):
+    """Each third of the last dim scaled by ``2 sigmoid`` of its gate column."""
+    return (x.float().reshape(*x.shape[:-1], 3, -1) * (2 * gate.float().sigmoid())[..., None]).reshape_as(x).to(
+        x.dtype
+    )

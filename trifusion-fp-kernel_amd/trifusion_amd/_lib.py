@@ -97,6 +97,17 @@ _SIGNATURES = {
     "tf_frame_audio": ([c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_ptr], c_i32),
     "tf_frames_mask": ([c_ptr, c_i64, c_ptr, c_ptr, c_i64, c_i64, c_ptr], c_i32),
     "tf_small_linear": ([c_ptr, c_ptr, c_ptr, c_i32, c_ptr, c_i64, c_i64, c_i64, c_ptr], c_i32),
+    "tf_depthwise_masked": ([c_ptr, c_ptr, c_ptr, c_i32, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_ptr], c_i32),
+    "tf_pool4": ([c_ptr, c_i32, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_ptr], c_i32),
+    "tf_rotary_qkv": ([c_ptr, c_i32, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_ptr], c_i32),
+    "tf_front_norm": (
+        [c_ptr, c_i32, ctypes.POINTER(c_i64), c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_f32, c_i32, c_ptr],
+        c_i32,
+    ),
+    "tf_interpolate": ([c_ptr, c_i32, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_ptr], c_i32),
+    "tf_bands": ([c_ptr, c_i32, ctypes.POINTER(c_i64), c_ptr, c_i64, c_i64, c_i64, c_i64, c_ptr], c_i32),
+    "tf_evidence_norm": ([c_ptr, c_ptr, c_ptr, c_i32, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_f32, c_ptr], c_i32),
+    "tf_gated_concat": ([c_ptr, c_ptr, c_i32, c_ptr, c_i64, c_i64, c_ptr], c_i32),
     "tf_version": ([], ctypes.c_char_p),
 }
 

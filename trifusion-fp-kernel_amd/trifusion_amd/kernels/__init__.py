@@ -71,4 +71,6 @@ def launch_reverse_valid(x, lengths):
     return y
 
 
-__all__ = ["RMSNorm", "swiglu", "rms", "reverse_valid"]
+from .block import gated_concat  # noqa: E402  (kernels/__init__.py:58-82)
+
+__all__ = ["RMSNorm", "swiglu", "rms", "reverse_valid", "gated_concat"]

@@ -1,0 +1,221 @@
+"""Kernels of the TriFusion block and front end on gfx950.
+
+The reference model's buffer and native kernels, each one C-ABI launch
+(``csrc/trifusion_block.hip``) behind a ``trifusion_amd::*`` operator:
+
+* ``depthwise_masked`` (``src/trifusion_l4/kernels/buffers.py:13-32``);
+* ``Pool4.apply`` (``buffers.py:35-44``) and ``interpolate``
+  (``src/trifusion_l4/kernels/native.py:119-133``), the 4:1 pooled attention
+  grid and the way back to frames;
+* ``RotaryQKV.apply`` (``buffers.py:46-56``);
+* ``front_norm`` (``buffers.py:58-80``) and ``bands`` (``native.py:157-163``)
+  of the CNN front end;
+* ``evidence_norm`` (``native.py:73-74``) and ``gated_concat``
+  (``src/trifusion_l4/kernels/__init__.py:58-82``) of the block's merge.
+
+They are re-exported under the reference's module paths
+(``kernels.buffers``, ``kernels.native``, ``kernels``).
+"""
+
+import ctypes
+
+import torch
+
+from .. import _lib
+from ..ops import ops
+
+
+def _autocast_dtype(x):
+    if torch.is_autocast_enabled("cuda"):
+        return torch.get_autocast_dtype("cuda")
+    return x.dtype
+
+
+def _strides(x):
+    return (ctypes.c_int64 * 4)(*x.stride())
+
+
+def depthwise_masked(x, layer, lengths):
+    """Masked depthwise Conv1d over time (``layer``: ``Conv1d(D, D, K,
+    padding=K//2, groups=D)``) on ``[B, T, D]``; rows past each length are 0.
+    Computes in the autocast dtype like the reference (``trifusion_amd::depthwise_masked``)."""
+    dtype = _autocast_dtype(x)
+    return ops.depthwise_masked(x.to(dtype), layer.weight.to(dtype), layer.bias.to(dtype), lengths)
+
+
+def launch_depthwise_masked(x, weight, bias, lengths):
+    lib = _lib.load()
+    _lib.require_cuda(x, weight, bias, lengths, what="depthwise_masked")
+    b, t, d = x.shape
+    k = weight.shape[-1]
+    if weight.numel() != d * k or bias.shape != (d,) or weight.dtype != x.dtype or bias.dtype != x.dtype:
+        raise ValueError("depthwise_masked: weight must be [D, 1, K] and bias [D], both of x's dtype")
+    if k % 2 == 0:
+        raise ValueError("depthwise_masked: odd kernel sizes only (same padding)")
+    x = x.contiguous()
+    y = torch.empty_like(x)
+    status = lib.tf_depthwise_masked(
+        x.data_ptr(), weight.contiguous().data_ptr(), bias.contiguous().data_ptr(),
+        _lib.dtype_code(x, "depthwise_masked"), lengths.to(torch.int64).contiguous().data_ptr(), y.data_ptr(),
+        b, t, d, k, _lib.stream_of(x),
+    )
+    _lib.check(status, "depthwise_masked")
+    return y
+
+
+class Pool4:
+    @staticmethod
+    def apply(x, lengths):
+        """Masked 4:1 average over time, ``[B, T, D] -> [B, ceil(T/4), D]``
+        (``trifusion_amd::pool4``)."""
+        return ops.pool4(x, lengths)
+
+
+def launch_pool4(x, lengths):
+    lib = _lib.load()
+    _lib.require_cuda(x, lengths, what="pool4")
+    x = x.contiguous()
+    b, t, d = x.shape
+    y = x.new_empty((b, (t + 3) // 4, d))
+    status = lib.tf_pool4(x.data_ptr(), _lib.dtype_code(x, "pool4"), lengths.to(torch.int64).contiguous().data_ptr(),
+                          y.data_ptr(), b, t, d, _lib.stream_of(x))
+    _lib.check(status, "pool4")
+    return y
+
+
+class RotaryQKV:
+    @staticmethod
+    def apply(x, cos, sin, heads):
+        """``[B, T, 3 H D]`` projection -> rotated ``[3, B, H, T, D]`` (q and k
+        rotated by interleaved pairs, v copied) (``trifusion_amd::rotary_qkv``)."""
+        return ops.rotary_qkv(x, cos, sin, int(heads))
+
+
+def launch_rotary_qkv(x, cos, sin, heads):
+    lib = _lib.load()
+    _lib.require_cuda(x, cos, sin, what="rotary_qkv")
+    x = x.contiguous()
+    b, t, width = x.shape
+    d = width // (3 * heads)
+    if 3 * heads * d != width or d % 2:
+        raise ValueError("rotary_qkv: width must be 3 * heads * head_dim with an even head_dim")
+    cos = cos.float().contiguous()
+    sin = sin.float().contiguous()
+    if cos.shape != (t, d // 2) or sin.shape != (t, d // 2):
+        raise ValueError(f"rotary_qkv: cos/sin must be [{t}, {d // 2}]")
+    y = x.new_empty((3, b, heads, t, d))
+    status = lib.tf_rotary_qkv(x.data_ptr(), _lib.dtype_code(x, "rotary_qkv"), cos.data_ptr(), sin.data_ptr(),
+                               y.data_ptr(), b, t, heads, d, _lib.stream_of(x))
+    _lib.check(status, "rotary_qkv")
+    return y
+
+
+def front_norm(x, lengths, norm, silu=False):
+    """Channel RMSNorm of a ``[B, C, T, F]`` map (rows ``t >= lengths`` zero,
+    optional SiLU after the rounding), returned as the ``[B, C, T, F]`` view of
+    a channels-last buffer (``trifusion_amd::front_norm``)."""
+    return ops.front_norm(x, lengths, norm.weight, float(norm.eps), bool(silu)).permute(0, 3, 1, 2)
+
+
+def launch_front_norm(x, lengths, weight, eps, silu):
+    lib = _lib.load()
+    _lib.require_cuda(x, lengths, weight, what="front_norm")
+    b, c, t, f = x.shape
+    y = x.new_empty((b, t, f, c))
+    status = lib.tf_front_norm(
+        x.data_ptr(), _lib.dtype_code(x, "front_norm"), _strides(x), weight.float().contiguous().data_ptr(),
+        lengths.to(torch.int64).contiguous().data_ptr(), y.data_ptr(), b, c, t, f, float(eps), int(silu),
+        _lib.stream_of(x),
+    )
+    _lib.check(status, "front_norm")
+    return y
+
+
+def interpolate(low, grids):
+    """Pooled grid -> frames by the grid's left/right/alpha, rows past the
+    lengths zero (``trifusion_amd::interpolate``)."""
+    return ops.interpolate(low, grids.left, grids.right, grids.alpha, grids.lengths)
+
+
+def launch_interpolate(low, left, right, alpha, lengths):
+    lib = _lib.load()
+    _lib.require_cuda(low, left, right, alpha, lengths, what="interpolate")
+    low = low.contiguous()
+    b, lt, d = low.shape
+    t = left.shape[1]
+    y = low.new_empty((b, t, d))
+    status = lib.tf_interpolate(
+        low.data_ptr(), _lib.dtype_code(low, "interpolate"), left.to(torch.int64).contiguous().data_ptr(),
+        right.to(torch.int64).contiguous().data_ptr(), alpha.float().contiguous().data_ptr(),
+        lengths.to(torch.int64).contiguous().data_ptr(), y.data_ptr(), b, t, lt, d, _lib.stream_of(low),
+    )
+    _lib.check(status, "interpolate")
+    return y
+
+
+def bands(x):
+    """``[B, C, T, F]`` -> ``[B, T, 8, C]`` frequency-band means (``trifusion_amd::bands``)."""
+    return ops.bands(x)
+
+
+def launch_bands(x):
+    lib = _lib.load()
+    _lib.require_cuda(x, what="bands")
+    b, c, t, f = x.shape
+    y = x.new_empty((b, t, 8, c))
+    status = lib.tf_bands(x.data_ptr(), _lib.dtype_code(x, "bands"), _strides(x), y.data_ptr(), b, c, t, f,
+                          _lib.stream_of(x))
+    _lib.check(status, "bands")
+    return y
+
+
+def evidence_norm(x, value, gate, weight, mask, eps=1e-5):
+    """``rms(mask ? x + value * 2 sigmoid(gate) : 0) * weight`` in fp32
+    (``trifusion_amd::evidence_norm``)."""
+    return ops.evidence_norm(x, value, gate, weight, mask, float(eps))
+
+
+def launch_evidence_norm(x, value, gate, weight, mask, eps=1e-5):
+    lib = _lib.load()
+    _lib.require_cuda(x, value, gate, weight, mask, what="evidence_norm")
+    x = x.float().contiguous()
+    if value.dtype != gate.dtype:
+        gate = gate.to(value.dtype)
+    value = value.contiguous()
+    gate = gate.contiguous()
+    d = x.shape[-1]
+    rows = x.numel() // d
+    if value.numel() != x.numel() or gate.numel() != x.numel():
+        raise ValueError("evidence_norm: value and gate must match x")
+    m = None
+    if mask is not None:
+        if mask.dtype != torch.bool or mask.numel() != rows:
+            raise ValueError("evidence_norm: mask must be bool with one entry per row")
+        m = mask.contiguous().data_ptr()
+    y = torch.empty(x.shape, device=x.device, dtype=torch.float32)
+    status = lib.tf_evidence_norm(x.data_ptr(), value.data_ptr(), gate.data_ptr(),
+                                  _lib.dtype_code(value, "evidence_norm"), m, weight.float().contiguous().data_ptr(),
+                                  y.data_ptr(), rows, d, float(eps), _lib.stream_of(x))
+    _lib.check(status, "evidence_norm")
+    return y
+
+
+def gated_concat(x, gate):
+    """``x [..., 3d]`` with each third scaled by ``2 sigmoid(gate[..., k])``
+    (``trifusion_amd::gated_concat``)."""
+    return ops.gated_concat(x, gate)
+
+
+def launch_gated_concat(x, gate):
+    lib = _lib.load()
+    _lib.require_cuda(x, gate, what="gated_concat")
+    x = x.contiguous()
+    gate = gate.to(x.dtype).contiguous()
+    if x.shape[-1] % 3 or gate.shape[-1] != 3 or gate.numel() * (x.shape[-1] // 3) != x.numel():
+        raise ValueError("gated_concat: x [..., 3d] and gate [..., 3]")
+    d = x.shape[-1] // 3
+    y = torch.empty_like(x)
+    status = lib.tf_gated_concat(x.data_ptr(), gate.data_ptr(), _lib.dtype_code(x, "gated_concat"), y.data_ptr(),
+                                 gate.numel() // 3, d, _lib.stream_of(x))
+    _lib.check(status, "gated_concat")
+    return y

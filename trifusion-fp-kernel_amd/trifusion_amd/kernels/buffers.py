@@ -2,13 +2,15 @@
 
 ``mask_buffer`` replaces ``buffers.py:6-10`` (``_mask``, ``primitives.py:65-70``)
 and ``mamba_controls`` replaces ``buffers.py:82-101`` (``_controls``,
-``primitives.py:190-216``).
+``primitives.py:190-216``); ``depthwise_masked``, ``Pool4``, ``RotaryQKV`` and
+``front_norm`` (``buffers.py:13-80``) live in ``kernels.block``.
 """
 
 import torch
 
 from .. import _lib
 from ..ops import ops
+from .block import Pool4, RotaryQKV, depthwise_masked, front_norm  # noqa: F401  (buffers.py:13-80)
 
 
 def mask_buffer(x, mask):

@@ -12,6 +12,7 @@ import torch
 
 from .. import _lib
 from ..ops import ops
+from .block import bands, evidence_norm, interpolate  # noqa: F401  (native.py:73-74,104-163)
 
 
 def _row_view(x):

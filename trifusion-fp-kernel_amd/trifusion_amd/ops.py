@@ -46,6 +46,14 @@ _SCHEMAS = {
     "frame_audio": "frame_audio(Tensor audio, Tensor channels, int kernel, int stride, int pad, int width) -> Tensor",
     "frames_mask": "frames_mask(Tensor lengths, int stride, int time) -> (Tensor, Tensor)",
     "small_linear": "small_linear(Tensor x, Tensor weight, Tensor? bias=None) -> Tensor",
+    "depthwise_masked": "depthwise_masked(Tensor x, Tensor weight, Tensor bias, Tensor lengths) -> Tensor",
+    "pool4": "pool4(Tensor x, Tensor lengths) -> Tensor",
+    "rotary_qkv": "rotary_qkv(Tensor x, Tensor cos, Tensor sin, int heads) -> Tensor",
+    "front_norm": "front_norm(Tensor x, Tensor lengths, Tensor weight, float eps, bool silu) -> Tensor",
+    "interpolate": "interpolate(Tensor low, Tensor left, Tensor right, Tensor alpha, Tensor lengths) -> Tensor",
+    "bands": "bands(Tensor x) -> Tensor",
+    "evidence_norm": "evidence_norm(Tensor x, Tensor value, Tensor gate, Tensor weight, Tensor? mask, float eps) -> Tensor",
+    "gated_concat": "gated_concat(Tensor x, Tensor gate) -> Tensor",
 }
 
 OPERATORS = tuple(_SCHEMAS)
@@ -159,6 +167,15 @@ def _cuda_small_linear(x, weight, bias=None):
     return launch_small_linear(x, weight, bias)
 
 
+def _block(name):
+    def kernel(*args):
+        from .kernels import block
+
+        return getattr(block, "launch_" + name)(*args)
+
+    return kernel
+
+
 # ---- Meta kernels: output shapes and dtypes only ----
 
 
@@ -235,6 +252,42 @@ def _meta_small_linear(x, weight, bias=None):
     return x.new_empty((x.shape[0], weight.shape[0]), dtype=torch.float32)
 
 
+def _meta_depthwise_masked(x, weight, bias, lengths):
+    return torch.empty_like(x, memory_format=torch.contiguous_format)
+
+
+def _meta_pool4(x, lengths):
+    b, t, d = x.shape
+    return x.new_empty((b, (t + 3) // 4, d))
+
+
+def _meta_rotary_qkv(x, cos, sin, heads):
+    b, t, width = x.shape
+    return x.new_empty((3, b, heads, t, width // (3 * heads)))
+
+
+def _meta_front_norm(x, lengths, weight, eps, silu):
+    b, c, t, f = x.shape
+    return x.new_empty((b, t, f, c))
+
+
+def _meta_interpolate(low, left, right, alpha, lengths):
+    return low.new_empty((low.shape[0], left.shape[1], low.shape[2]))
+
+
+def _meta_bands(x):
+    b, c, t, f = x.shape
+    return x.new_empty((b, t, 8, c))
+
+
+def _meta_evidence_norm(x, value, gate, weight, mask, eps):
+    return x.new_empty(x.shape, dtype=torch.float32)
+
+
+def _meta_gated_concat(x, gate):
+    return torch.empty_like(x, memory_format=torch.contiguous_format)
+
+
 # ---- CPU kernels: loud failure, no fallback ----
 
 
@@ -266,6 +319,11 @@ _KERNELS = {
     "frame_audio": (_cuda_frame_audio, _meta_frame_audio),
     "frames_mask": (_cuda_frames_mask, _meta_frames_mask),
     "small_linear": (_cuda_small_linear, _meta_small_linear),
+    **{
+        name: (_block(name), globals()["_meta_" + name])
+        for name in ("depthwise_masked", "pool4", "rotary_qkv", "front_norm", "interpolate", "bands",
+                     "evidence_norm", "gated_concat")
+    },
 }
 
 _LIBRARY = torch.library.Library(NAMESPACE, "DEF")
