@@ -13,9 +13,10 @@ cache-warm time is reported beside it.
 Printed as one JSON line: ``value`` is the algorithmic GB/s (unique input bytes +
 output bytes per call / average call time), ``roofline`` compares it with the
 8 TB/s HBM peak, ``cpu_baseline`` times the CPU oracle (chunked fp32 PyTorch) on
-the same workload on the host cores, and ``encoder`` reports the ms per forward
+the same workload on the host cores, ``encoder`` reports the ms per forward
 of the 8-block encoder at 4 s mono x 16 with graph replay (``--no-encoder`` to
-skip).
+skip), and ``trifusion_model`` the same for the full TriFusion-FP model at the
+reference configuration (random init; ``--no-trifusion`` to skip).
 """
 
 import argparse
@@ -57,6 +58,9 @@ def parse_args():
     p.add_argument("--kernels-only", action="store_true",
                    help="only time the bandwidth kernels at the encoder shapes (profiling aid)")
     p.add_argument("--encoder-only", action="store_true", help="only time the encoder forward (profiling aid)")
+    p.add_argument("--trifusion-only", action="store_true",
+                   help="only time the full TriFusion-FP model forward at 4 s mono x 16 (profiling aid)")
+    p.add_argument("--no-trifusion", action="store_true", help="skip the full TriFusion-FP model timing")
     p.add_argument("--variant", default="auto", choices=["auto", "mfma", "generic"])
     p.add_argument("--workload", default="clip", choices=sorted(WORKLOADS),
                    help="shape to time (clip: the headline B16 L400 workload)")
@@ -251,13 +255,21 @@ def bandwidth_kernels(torch):
     return out
 
 
-def encoder_ms(torch):
+def encoder_ms(torch, trifusion=False):
+    """ms per forward at 4 s mono x 16 through the graph engine: the benchmark
+    encoder, or with ``trifusion`` the full TriFusion-FP model at the reference
+    configuration (dim 1024, 16 blocks, N=128; random init)."""
     from trifusion_amd.runtime import InferenceEngine
     from trifusion_amd.model import Encoder, ModelConfig
     from trifusion_amd.runtime import prepare_static_weights
+    from trifusion_amd.trifusion import TriFusion, TriFusionConfig
 
     torch.manual_seed(0)
-    model = Encoder(ModelConfig()).eval().requires_grad_(False)
+    if trifusion:
+        model = TriFusion(TriFusionConfig()).eval().requires_grad_(False)
+        del model.memory_head
+    else:
+        model = Encoder(ModelConfig()).eval().requires_grad_(False)
     prepare_static_weights(model)
     model = model.cuda()
     g = torch.Generator().manual_seed(551)
@@ -276,8 +288,12 @@ def encoder_ms(torch):
         torch.cuda.synchronize()
         times.append(time.perf_counter() - t0)
     times.sort()
-    return {"ms_per_forward": round(times[len(times) // 2] * 1e3, 4), "graph_hits": engine.graph_hits,
+    line = {"ms_per_forward": round(times[len(times) // 2] * 1e3, 4), "graph_hits": engine.graph_hits,
             "protocol": "3 warm-ups, median of 11, perf_counter + synchronize, graph replay"}
+    if trifusion:
+        line["model"] = "TriFusion-FP, dim 1024, 16 blocks, N=128 (528M parameters, random init, bf16 GEMMs)"
+        line["reference_l4_ms_per_forward"] = 79.70  # README.md:112, an NVIDIA L4, real checkpoint
+    return line
 
 
 def main():
@@ -303,6 +319,9 @@ def main():
         return
     if args.encoder_only:
         print(json.dumps({"encoder": encoder_ms(torch)}), flush=True)
+        return
+    if args.trifusion_only:
+        print(json.dumps({"trifusion_model": encoder_ms(torch, trifusion=True)}), flush=True)
         return
     if args.kernels_only:
         print(json.dumps({"bandwidth_kernels": bandwidth_kernels(torch)}), flush=True)
@@ -364,6 +383,8 @@ def main():
             line["encoder"] = encoder_ms(torch)
         except ImportError as err:  # encoder not built yet
             line["encoder"] = {"error": str(err)}
+    if not args.no_encoder and not args.no_trifusion:
+        line["trifusion_model"] = encoder_ms(torch, trifusion=True)
     if not args.no_cpu_baseline and args.workload == "clip":  # the baseline times the clip workload
         line["cpu_baseline"] = cpu_baseline(torch, args.cpu_seconds)
     print(json.dumps(line), flush=True)

@@ -28,20 +28,36 @@ from dataclasses import fields
 import torch
 
 from .model import Encoder, ModelConfig
+from .trifusion import TriFusion, TriFusionConfig
+
+
+def _model_kind(config):
+    """The TriFusion layout when the configuration's fields are those of the
+    reference model (``model.py:14-34``), else the benchmark encoder."""
+    keys = set(config)
+    if keys <= {f.name for f in fields(TriFusionConfig)} and keys & {"heads", "evidence_rank", "backend"}:
+        return TriFusion, TriFusionConfig
+    if keys <= {f.name for f in fields(ModelConfig)}:
+        return Encoder, ModelConfig
+    raise ValueError("Unsupported model configuration fields")
 
 
 def load_student(path, optimized=True, device="cuda"):
     saved = torch.load(path, map_location="cpu", weights_only=True, mmap=True)
     config = dict(saved["model_config"])
-    known = {f.name for f in fields(ModelConfig)}
-    if set(config) - known:
-        raise ValueError("Unsupported model configuration fields")
+    cls, cfg = _model_kind(config)
     with torch.device("meta"):
-        model = Encoder(ModelConfig(**config))
+        model = cls(cfg(**config))
+    if cls is TriFusion:
+        # the training-only head is not part of the deployed network (runtime.py:33-40)
+        del model.memory_head
     state = {
         k: v for k, v in saved["model"].items() if not k.startswith(("kd_features.", "memory_head."))
     }
     model.load_state_dict(state, strict=True, assign=True)
+    if cls is TriFusion:
+        # the STFT window is a non-persistent buffer: materialise it (runtime.py:41-42)
+        model.front.window = torch.hann_window(400, periodic=True)
     model.eval().requires_grad_(False)
     model.set_variant("auto" if optimized else "generic")
     if optimized:
@@ -51,7 +67,7 @@ def load_student(path, optimized=True, device="cuda"):
 
 def save_student(model, path):
     """Write a model-only checkpoint in the format ``load_student`` reads."""
-    config = {f.name: getattr(model.config, f.name) for f in fields(ModelConfig)}
+    config = {f.name: getattr(model.config, f.name) for f in fields(type(model.config))}
     torch.save({"model_config": config, "model": model.state_dict()}, path)
 
 

@@ -1,0 +1,379 @@
+"""The TriFusion-FP model on the MI355X kernels.
+
+The reference model's layout and forward (``src/trifusion_l4/model.py``,
+``front.py``, ``decoder.py``, ``masking.py``, ``attention.py``) with the same
+parameter names, so a checkpoint saved from either loads into the other:
+
+* ``Frontend``: log power STFT (``torch.stft``, 512-point, hop 160, Hann 400),
+  three CNN stages (Conv2d + channel RMSNorm, ``tf_front_norm``) and 8
+  frequency bands (``tf_bands``) (``front.py:8-114``);
+* ``TriFusionBlock``: LocalCNN (GLU, masked depthwise conv ``tf_depthwise_masked``,
+  RMSNorm), attention on the 4:1 pooled grid (``tf_pool4``, ``tf_rotary_qkv``,
+  fp32 SDPA, ``tf_interpolate``), the evidence-gated norm (``tf_evidence_norm``),
+  bidirectional Mamba-3 (the fused recurrence forward and with ``reverse=True``,
+  its controls computed in the prologue) merged by ``tf_mean_rmsnorm``, the
+  gated concatenation (``tf_gated_concat``) with a masked depthwise merge, and a
+  SwiGLU FFN (``model.py:51-200``);
+* ``Decoder``: learned queries read the deep and fine features with masked
+  attention, global and memory features, top-k local evidence, and the five
+  logits (``decoder.py:8-96``).
+
+The forward runs under bf16 autocast, as the reference's engine runs it
+(``runtime.py:79-82``). Dropout is identity at inference.
+"""
+
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+from torch.nn.attention import SDPBackend, sdpa_kernel
+
+from .kernels import RMSNorm, gated_concat, swiglu
+from .kernels.block import (
+    Pool4,
+    RotaryQKV,
+    bands,
+    depthwise_masked,
+    evidence_norm,
+    front_norm,
+    interpolate,
+)
+from .kernels.buffers import mask_buffer
+from .kernels.native import add, mean_norm
+from .mamba import Mamba3Inference
+from .masking import time_mask
+
+
+@dataclass
+class TriFusionConfig:
+    """Model configuration; the fields and defaults of the reference's
+    ``ModelConfig`` (``model.py:14-34``), training-only flags included so saved
+    configurations load unchanged."""
+
+    dim: int = 1024
+    depth: int = 16
+    ffn_dim: int = 2816
+    heads: int = 16
+    state_dim: int = 128
+    evidence_rank: int = 64
+    dropout: float = 0.1
+    backend: str = "l4"
+    checkpoint_blocks: bool = False
+    checkpoint_frontend: bool = False
+    channels_last: bool = False
+    buffer_fusion: bool = True
+    native_kernels: bool = True
+    mamba_packed: bool = True
+    paired_mamba: bool = False
+    mamba_parallel_bwd: bool = True
+    mamba_fast_launch: bool = True
+    paired_mamba_grid_limit: int = 64
+
+
+class _MambaShape:
+    """What ``Mamba3Inference`` reads from a config: 64-wide heads."""
+
+    def __init__(self, c):
+        self.dim, self.state_dim, self.head_dim = c.dim, c.state_dim, 64
+
+
+def masked_attention(q, k, v, mask):
+    """fp32 scaled-dot-product attention with a boolean key mask, result in q's
+    dtype (``attention.py:8-18``)."""
+    dtype = q.dtype
+    with torch.autocast("cuda", enabled=False), sdpa_kernel([SDPBackend.EFFICIENT_ATTENTION, SDPBackend.MATH]):
+        y = F.scaled_dot_product_attention(q.float(), k.float(), v.float(), attn_mask=mask, dropout_p=0.0)
+    return y.to(dtype)
+
+
+class Grids:
+    """Frame grid, its 4:1 pooled grid and the interpolation back
+    (``masking.py:14-57``): per clip the frame and pooled lengths and masks,
+    the left/right pooled neighbours and weight of every frame, and the rotary
+    tables of the pooled positions."""
+
+    def __init__(self, lengths, time, head_dim):
+        dev = lengths.device
+        self.lengths = lengths
+        self.mask = time_mask(lengths, time)
+        self.low_lengths = (lengths + 3) // 4
+        low_t = (time + 3) // 4
+        self.low_mask = time_mask(self.low_lengths, low_t)
+        centre = torch.arange(time, device=dev)[None, :].float() + 0.5
+        pos = (centre * self.low_lengths[:, None] / lengths[:, None] - 0.5).clamp_min(0)
+        pos = torch.minimum(pos, (self.low_lengths - 1)[:, None])
+        self.left = pos.long()
+        self.right = torch.minimum(self.left + 1, (self.low_lengths - 1)[:, None])
+        self.alpha = pos - self.left
+        freq = 10000.0 ** (-torch.arange(0, head_dim, 2, device=dev).float() / head_dim)
+        phase = torch.arange(low_t, device=dev).float()[:, None] * freq[None, :]
+        self.rope_cos, self.rope_sin = phase.cos(), phase.sin()
+
+    def pool(self, x):
+        return Pool4.apply(x.contiguous(), self.lengths)
+
+    def interpolate(self, low):
+        return interpolate(low, self)
+
+
+class CNNStage(nn.Module):
+    """Residual Conv2d stage: conv (time stride s, frequency stride 2) -> norm ->
+    SiLU -> conv -> norm, plus a 1x1 strided skip (``front.py:8-43``)."""
+
+    def __init__(self, cin, cout, stride):
+        super().__init__()
+        self.stride = stride
+        self.conv1 = nn.Conv2d(cin, cout, 3, stride=(stride, 2), padding=1, bias=False)
+        self.conv2 = nn.Conv2d(cout, cout, 3, padding=1, bias=False)
+        self.skip = nn.Conv2d(cin, cout, 1, stride=(stride, 2), bias=False)
+        self.norm1, self.norm2 = RMSNorm(cout), RMSNorm(cout)
+
+    def forward(self, x, lengths):
+        lengths = (lengths + self.stride - 1) // self.stride
+        h = front_norm(self.conv1(x), lengths, self.norm1, silu=True)
+        h = front_norm(self.conv2(h), lengths, self.norm2)
+        valid = time_mask(lengths, h.shape[2])[:, None, :, None]
+        return F.silu(h + self.skip(x).masked_fill(~valid, 0)).masked_fill(~valid, 0)
+
+
+class Frontend(nn.Module):
+    """Log power spectrogram -> three CNN stages -> frequency bands
+    (``front.py:46-114``)."""
+
+    def __init__(self, channels_last=True):
+        super().__init__()
+        self.register_buffer("window", torch.hann_window(400, periodic=True), persistent=False)
+        self.stages = nn.ModuleList([CNNStage(1, 32, 1), CNNStage(32, 64, 2), CNNStage(64, 128, 2)])
+        self.channels_last = channels_last
+        if channels_last:
+            self.to(memory_format=torch.channels_last)
+
+    def spectrogram(self, audio, sample_lengths, channels):
+        b, c, n = audio.shape
+        with torch.autocast("cuda", enabled=False):
+            keep = time_mask(sample_lengths, n)[:, None, :] & (torch.arange(c, device=audio.device)[None, :]
+                                                               < channels[:, None])[..., None]
+            wave = audio.float().masked_fill(~keep, 0)
+            spec = torch.stft(wave.reshape(b * c, n), n_fft=512, hop_length=160, win_length=400,
+                              window=self.window.float(), center=True, pad_mode="constant", return_complex=True)
+            power = (spec.real.square() + spec.imag.square()).reshape(b, c, 257, -1).sum(1)
+            power = power / channels[:, None, None]
+            log = torch.log(1e-6 + power).transpose(1, 2).unsqueeze(1)
+            lengths = sample_lengths // 160 + 1
+            log = log.masked_fill(~time_mask(lengths, log.shape[2])[:, None, :, None], 0)
+        return log, lengths
+
+    def forward(self, audio, sample_lengths, channels):
+        x, lengths = self.spectrogram(audio, sample_lengths, channels)
+        if self.channels_last:
+            x = x.contiguous(memory_format=torch.channels_last)
+        fine = fine_lengths = None
+        # deterministic convolution algorithms: some of the library's faster
+        # ones accumulate in a run-dependent order, and repeated forwards (and
+        # graph replays against eager calls) must give the same bits
+        with torch.backends.cudnn.flags(enabled=torch.backends.cudnn.enabled, benchmark=False, deterministic=True,
+                                        allow_tf32=False):
+            for i, stage in enumerate(self.stages):
+                x = stage(x, lengths)
+                lengths = (lengths + stage.stride - 1) // stage.stride
+                if i == 1:
+                    fine, fine_lengths = bands(x), lengths
+        return bands(x).flatten(2), fine, lengths, fine_lengths
+
+
+class LocalCNN(nn.Module):
+    """GLU -> masked depthwise conv (7) -> RMSNorm -> SiLU -> linear (``model.py:51-75``)."""
+
+    def __init__(self, c):
+        super().__init__()
+        self.up = nn.Linear(c.dim, 2 * c.dim, bias=False)
+        self.dw = nn.Conv1d(c.dim, c.dim, 7, padding=3, groups=c.dim)
+        self.norm = RMSNorm(c.dim)
+        self.out = nn.Linear(c.dim, c.dim, bias=False)
+
+    def forward(self, x, mask, lengths):
+        h = depthwise_masked(F.glu(self.up(x), dim=-1), self.dw, lengths)
+        return self.out(F.silu(self.norm(h)))
+
+
+class GlobalAttention(nn.Module):
+    """Rotary multi-head attention on the 4:1 pooled grid, interpolated back to
+    frames (``model.py:78-98``)."""
+
+    def __init__(self, c):
+        super().__init__()
+        self.heads, self.head_dim = c.heads, c.dim // c.heads
+        self.qkv = nn.Linear(c.dim, 3 * c.dim, bias=False)
+        self.out = nn.Linear(c.dim, c.dim, bias=False)
+
+    def forward(self, x, grids):
+        p = grids.pool(x)
+        q, k, v = RotaryQKV.apply(self.qkv(p), grids.rope_cos, grids.rope_sin, self.heads).unbind(0)
+        y = masked_attention(q, k, v, grids.low_mask[:, None, None, :])
+        return grids.interpolate(self.out(y.transpose(1, 2).reshape(p.shape)))
+
+
+class TriFusionBlock(nn.Module):
+    """Local CNN, pooled attention and bidirectional Mamba-3 mixed by an
+    evidence gate and a gated, depthwise-merged concatenation, then a SwiGLU
+    FFN (``model.py:101-200``)."""
+
+    def __init__(self, c):
+        super().__init__()
+        d, r = c.dim, c.evidence_rank
+        self.pre = RMSNorm(d)
+        self.local, self.attention = LocalCNN(c), GlobalAttention(c)
+        self.cn, self.an, self.mn = RMSNorm(d), RMSNorm(d), RMSNorm(d)
+        self.e_down = nn.Linear(2 * d, r)
+        self.e_value, self.e_gate = nn.Linear(r, d), nn.Linear(r, d)
+        self.u_norm = RMSNorm(d)
+        shape = _MambaShape(c)
+        self.forward_mamba, self.backward_mamba = Mamba3Inference(shape), Mamba3Inference(shape)
+        self.gate = nn.Linear(3 * d, 3)
+        self.merge_dw = nn.Conv1d(3 * d, 3 * d, 3, padding=1, groups=3 * d)
+        self.merge = nn.Linear(3 * d, d, bias=False)
+        self.ff_norm = RMSNorm(d)
+        self.gate_up = nn.Linear(d, 2 * c.ffn_dim, bias=False)
+        self.down = nn.Linear(c.ffn_dim, d, bias=False)
+        nn.init.zeros_(self.e_gate.weight)
+        nn.init.zeros_(self.e_gate.bias)
+        nn.init.normal_(self.e_value.weight, std=1e-3)
+        nn.init.zeros_(self.e_value.bias)
+        nn.init.zeros_(self.gate.weight)
+        nn.init.zeros_(self.gate.bias)
+        with torch.no_grad():
+            self.merge.weight.mul_(1 / math.sqrt(2 * c.depth))
+            self.down.weight.mul_(1 / math.sqrt(2 * c.depth))
+
+    def forward(self, x, grids):
+        mask, lengths = grids.mask, grids.lengths
+        x = mask_buffer(x, mask)
+        h = self.pre(x)
+        cn = self.cn(self.local(h, mask, lengths))
+        an = self.an(self.attention(h, grids))
+        z = F.silu(self.e_down(torch.cat((cn, an), -1)))
+        u = evidence_norm(x, self.e_value(z), self.e_gate(z), self.u_norm.weight, mask, self.u_norm.eps)
+        # rows past each length come out of the recurrence as zeros in both directions
+        mf = self.forward_mamba(u, lengths)
+        mb = self.backward_mamba(u, lengths, reverse=True)
+        mn = mean_norm(mf, mb, self.mn.weight, self.mn.eps)
+        s = torch.cat((cn, mn, an), -1)
+        v = gated_concat(s, self.gate(s))
+        conv = depthwise_masked(v, self.merge_dw, lengths)
+        bf16 = torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16
+        r = x + self.merge(add(v, conv, bf16=bf16))
+        f = swiglu(self.gate_up(self.ff_norm(r)))
+        return add(r, self.down(f), mask), mf, mb
+
+
+def sin_position(time, dim, device):
+    """Interleaved sin/cos positions ``[time, dim]`` (``decoder.py:9-14``)."""
+    phase = torch.arange(time, device=device).float()[:, None] * (
+        10000.0 ** (-torch.arange(0, dim, 2, device=device).float() / dim)
+    )[None, :]
+    return torch.stack((phase.sin(), phase.cos()), -1).flatten(-2)
+
+
+class QueryRead(nn.Module):
+    """Ten learned 256-wide queries read a sequence with 8-head masked attention;
+    returns the means of queries 0-3, 4-7 and 8-9 (``decoder.py:17-32``)."""
+
+    def __init__(self, input_dim):
+        super().__init__()
+        self.kv = nn.Linear(input_dim, 512, bias=False)
+        self.q = nn.Linear(256, 256, bias=False)
+        self.out = nn.Linear(256, 256, bias=False)
+
+    def forward(self, query, x, mask):
+        b, t, _ = x.shape
+        k, v = self.kv(x).view(b, t, 2, 8, 32).permute(2, 0, 3, 1, 4).unbind(0)
+        q = self.q(query).view(10, 8, 32).transpose(0, 1).unsqueeze(0).expand(b, -1, -1, -1)
+        h = self.out(masked_attention(q, k, v, mask[:, None, None, :]).transpose(1, 2).reshape(b, 10, 256))
+        return h[:, :4].mean(1), h[:, 4:8].mean(1), h[:, 8:].mean(1)
+
+
+class Decoder(nn.Module):
+    """Deep and fine query reads, global and memory features and top-25 local
+    evidence into file, voice and music logits (``decoder.py:35-96``)."""
+
+    def __init__(self, dim):
+        super().__init__()
+        self.query = nn.Parameter(torch.randn(10, 256) * 0.02)
+        self.band = nn.Parameter(torch.randn(8, 64) * 0.02)
+        self.deep_read, self.fine_read = QueryRead(dim), QueryRead(64)
+        self.global_proj, self.memory_proj = nn.Linear(dim, 256), nn.Linear(2 * dim, 256)
+        self.local_logits = nn.Linear(512, 2)
+        self.local_features = nn.Linear(512, 256)
+        self.voice_lat = nn.Sequential(nn.Linear(1280, 256), nn.SiLU())
+        self.music_lat = nn.Sequential(nn.Linear(1280, 256), nn.SiLU())
+        self.voice_head, self.music_head = nn.Linear(256, 2), nn.Linear(256, 2)
+        self.file_head = nn.Sequential(nn.Linear(1536, 256), nn.SiLU(), nn.Linear(256, 1))
+
+    def forward(self, x, fine, grids, fine_lengths, mf, mb):
+        b, tf, _, _ = fine.shape
+        dev = x.device
+        fm = time_mask(fine_lengths, tf)
+        deep = self.deep_read(self.query, x, grids.mask)
+        fp = fine + sin_position(tf, 64, dev)[None, :, None, :].to(fine.dtype) + self.band.to(fine.dtype)[None, None]
+        fine_q = self.fine_read(self.query, fp.flatten(1, 2), fm[:, :, None].expand(b, tf, 8).reshape(b, -1))
+        global_feature = self.global_proj((x.float() * grids.mask[..., None]).sum(1) / grids.lengths[:, None])
+        end = mf[torch.arange(b, device=dev), grids.lengths - 1]
+        memory = self.memory_proj(torch.cat((end, mb[:, 0]), -1))
+        flat = fine.flatten(2)
+        local, features = self.local_logits(flat), self.local_features(flat)
+        k = min(25, tf)
+        idx = local.float().masked_fill(~fm[..., None], -torch.inf).transpose(1, 2).topk(k, -1).indices
+        picked = features[:, None].expand(-1, 2, -1, -1).gather(2, idx[..., None].expand(-1, -1, -1, 256))
+        valid_k = torch.arange(k, device=dev)[None, :] < fine_lengths.clamp_max(k)[:, None]
+        top = (picked.float() * valid_k[:, None, :, None]).sum(2) / valid_k.sum(1)[:, None, None]
+        voice = self.voice_lat(torch.cat((deep[0], fine_q[0], global_feature, top[:, 0], memory), -1))
+        music = self.music_lat(torch.cat((deep[1], fine_q[1], global_feature, top[:, 1], memory), -1))
+        v, m = self.voice_head(voice), self.music_head(music)
+        f = self.file_head(torch.cat((deep[2], fine_q[2], global_feature, memory, voice, music), -1))
+        logits = torch.cat((f, v[:, :1], m[:, :1], v[:, 1:], m[:, 1:]), -1).float()
+        return {
+            "logits": logits,
+            "local_logits": local.float(),
+            "local_mask": fm,
+            "features": x,
+            "feature_mask": grids.mask,
+            "embedding": global_feature.float(),
+        }
+
+
+class TriFusion(nn.Module):
+    """Front end -> projection -> TriFusion blocks -> decoder (``model.py:203-260``)."""
+
+    def __init__(self, config=None):
+        super().__init__()
+        self.config = c = config or TriFusionConfig()
+        if c.dim % c.heads or c.dim % 32:
+            raise ValueError("dim must divide attention heads and Mamba headdim")
+        self.front = Frontend(c.channels_last)
+        self.front_projection = nn.Identity() if c.dim == 1024 else nn.Linear(1024, c.dim, bias=False)
+        self.blocks = nn.ModuleList([TriFusionBlock(c) for _ in range(c.depth)])
+        self.decoder = Decoder(c.dim)
+        self.memory_head = nn.Linear(c.dim, 2)
+
+    def set_variant(self, variant):
+        """Select the recurrence kernel ("auto", "mfma" or "generic") of every Mamba."""
+        for m in self.modules():
+            if isinstance(m, Mamba3Inference):
+                m.variant = variant
+
+    def encode(self, audio, lengths, channels):
+        x, fine, main_lengths, fine_lengths = self.front(audio, lengths, channels)
+        x = self.front_projection(x).float()
+        grids = Grids(main_lengths, x.shape[1], self.config.dim // self.config.heads)
+        mf = mb = None
+        for block in self.blocks:
+            x, mf, mb = block(x, grids)
+        return x, fine, grids, fine_lengths, mf, mb
+
+    def forward(self, audio, lengths, channels):
+        return self.decoder(*self.encode(audio, lengths, channels))
+
+
+__all__ = ["TriFusion", "TriFusionConfig", "TriFusionBlock", "Frontend", "Decoder", "Grids"]
