@@ -352,6 +352,35 @@ int tf_evidence_norm(const float *x, const void *a, const void *g, int32_t ag_dt
 int tf_gated_concat(const void *x, const void *gate, int32_t dtype, void *y, int64_t rows, int64_t d,
                     void *stream);
 
+/*
+ * First half of a front-end CNN stage, channels-last: y = silu(norm(mask(conv(x))))
+ * with conv the 3x3 convolution of stride (stride, 2) and padding 1 and norm the
+ * channel RMSNorm with weight norm_w and eps; rows t >= L_b of the output grid are 0.
+ * The convolution output and the norm output are rounded to bf16, as in the bf16
+ * autocast forward. x is fp32 [B, Ti, Fi] (cin == 1, rounded to bf16 on read) or bf16
+ * [B, Ti, Fi, cin] (cin 32 or 64); w bf16 [9, cout, cin] (tap-major: tap = 3 dy + dx);
+ * y bf16 [B, To, Fo, cout], To = (Ti - 1) / stride + 1, Fo = (Fi - 1) / 2 + 1;
+ * cout 32 (cin 1) or 32, 64, 128. Replaces conv1 + front_norm(silu=True) of
+ * CNNStage.forward (src/trifusion_l4/front.py:19-36, kernels/buffers.py:58-80).
+ */
+int tf_front_conv1(const void *x, int32_t x_dtype, const void *w, const float *norm_w,
+                   const int64_t *lengths, void *y, int64_t batch, int64_t time_in, int64_t freq_in,
+                   int64_t cin, int64_t cout, int64_t stride, float eps, void *stream);
+
+/*
+ * Second half of a front-end CNN stage: y = mask(silu(norm(mask(conv(h))) + mask(skip(x))))
+ * with conv the 3x3 convolution (stride 1, padding 1) of h, the first half's output
+ * [B, To, Fo, cout] bf16 with weight w bf16 [9, cout, cout], and skip the 1x1
+ * convolution of stride (stride, 2) of the stage input x (fp32 [B, Ti, Fi] with cin 1,
+ * or bf16 [B, Ti, Fi, cin] with cin 32 or 64) with weight w_skip bf16 [cout, cin].
+ * Every intermediate is rounded to bf16 as in the autocast forward; y bf16
+ * [B, To, Fo, cout], cout 32, 64 or 128. Replaces conv2 + front_norm + the skip,
+ * residual and SiLU of CNNStage.forward (src/trifusion_l4/front.py:19-43).
+ */
+int tf_front_conv2(const void *h, const void *w, const float *norm_w, const void *x, int32_t x_dtype,
+                   const void *w_skip, const int64_t *lengths, void *y, int64_t batch, int64_t time_in,
+                   int64_t freq_in, int64_t cin, int64_t cout, int64_t stride, float eps, void *stream);
+
 /* Library version string (static storage). */
 const char *tf_version(void);
 

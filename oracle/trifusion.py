@@ -17,7 +17,10 @@ replace:
 * ``bands``: ``adaptive_avg_pool2d`` over frequency (``front.py:94-101``);
 * ``evidence_norm``: ``masked(u_norm(x + value * 2 sigmoid(gate)))``
   (``src/trifusion_l4/model.py:166-167``);
-* ``gated_concat``: the reference branch (``kernels/__init__.py:59-63``).
+* ``gated_concat``: the reference branch (``kernels/__init__.py:59-63``);
+* ``front_stage``: a whole CNN stage (``front.py:19-43``) under bf16 autocast:
+  ``F.conv2d`` on bf16-rounded operands with bf16 outputs, ``front_norm``, the
+  1x1 skip, the bf16 residual sum and SiLU, rows past the length cleared.
 
 Pinning (tests/test_oracle_trifusion.py): each against an explicit loop or
 closed form on small inputs.
@@ -105,3 +108,22 @@ def gated_concat(x, gate):
     return (x.float().reshape(*x.shape[:-1], 3, -1) * (2 * gate.float().sigmoid())[..., None]).reshape_as(x).to(
         x.dtype
     )
+
+
+def _bf(x):
+    return x.to(torch.bfloat16).float()
+
+
+def front_stage(x, lengths, conv1, conv2, skip, norm1, norm2, stride, eps=1e-5):
+    """CNN stage ``[B, C, T, F] -> [B, T', F', C']`` (bf16), ``lengths`` the
+    stage's output lengths; ``conv1``/``conv2``/``skip`` the ``Conv2d`` weights
+    ``[cout, cin, k, k]``, ``norm1``/``norm2`` the RMSNorm weights."""
+    def conv(v, w, s, pad):
+        return _bf(F.conv2d(_bf(v), _bf(w), stride=s, padding=pad))
+
+    h = conv(x, conv1, (stride, 2), 1)
+    h = front_norm(h.to(torch.bfloat16), lengths, norm1, eps, silu=True).permute(0, 3, 1, 2)
+    h = front_norm(conv(h, conv2, 1, 1).to(torch.bfloat16), lengths, norm2, eps).float()
+    valid = time_mask(lengths, h.shape[1])[:, :, None, None]
+    sk = conv(x, skip, (stride, 2), 0).permute(0, 2, 3, 1).masked_fill(~valid, 0)
+    return F.silu(_bf(h + sk)).masked_fill(~valid, 0).to(torch.bfloat16)

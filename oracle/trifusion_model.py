@@ -26,10 +26,6 @@ from .encoder import _bf, _linear, mamba_block
 BF16 = torch.bfloat16
 
 
-def _conv2d(x, w, stride=1, padding=0):
-    return _bf(F.conv2d(_bf(x), w.float(), stride=stride, padding=padding))
-
-
 def _rms_bf(x, w, eps=1e-5):
     """RMSNorm of a bf16-valued tensor, bf16 result."""
     return E.rms_norm(x.to(BF16), w, eps).float()
@@ -41,13 +37,9 @@ def _attention(q, k, v, mask):
 
 def _stage(sd, pre, x, lengths, stride):
     lengths = (lengths + stride - 1) // stride
-    h = _conv2d(x, sd[pre + "conv1.weight"], (stride, 2), 1)
-    h = K.front_norm(h.to(BF16), lengths, sd[pre + "norm1.weight"], silu=True).float().permute(0, 3, 1, 2)
-    h = _conv2d(h, sd[pre + "conv2.weight"], 1, 1)
-    h = K.front_norm(h.to(BF16), lengths, sd[pre + "norm2.weight"]).float().permute(0, 3, 1, 2)
-    valid = E.time_mask(lengths, h.shape[2])[:, None, :, None]
-    skip = _conv2d(x, sd[pre + "skip.weight"], (stride, 2), 0).masked_fill(~valid, 0)
-    return _bf(F.silu(_bf(h + skip))).masked_fill(~valid, 0), lengths
+    y = K.front_stage(x, lengths, sd[pre + "conv1.weight"], sd[pre + "conv2.weight"], sd[pre + "skip.weight"],
+                      sd[pre + "norm1.weight"], sd[pre + "norm2.weight"], stride)
+    return y.float().permute(0, 3, 1, 2), lengths
 
 
 def frontend(sd, audio, sample_lengths, channels):

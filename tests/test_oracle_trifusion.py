@@ -3,6 +3,7 @@ explicit loops and library routines on small inputs."""
 
 import math
 
+import pytest
 import torch
 import torch.nn.functional as F
 
@@ -123,3 +124,54 @@ def test_evidence_norm_and_gated_concat():
     for r in range(4):
         for k in range(3):
             assert torch.allclose(gy[r, 4 * k : 4 * k + 4], gx[r, 4 * k : 4 * k + 4] * 2 * torch.sigmoid(gg[r, k]))
+
+
+def _bf_values(*shape, g):
+    return torch.randn(*shape, generator=g).to(torch.bfloat16).float()
+
+
+@pytest.mark.parametrize("s", [1, 2])
+def test_front_stage_matches_direct_loops(s):
+    """A CNN stage against direct float64 loops over taps: 3x3 conv of stride
+    (s, 2) with zero padding 1, norm, SiLU, second conv, norm, 1x1 strided skip,
+    residual, SiLU, rows past the length 0. The oracle rounds to bf16 at five
+    points, so values agree within a few bf16 steps; a wrong stride axis, padding
+    or weight orientation moves them by O(1)."""
+    g = torch.Generator().manual_seed(7)
+    b, cin, cout, t, f = 2, 3, 4, 7, 9
+    x = _bf_values(b, cin, t, f, g=g)
+    w1, w2, ws = _bf_values(cout, cin, 3, 3, g=g), _bf_values(cout, cout, 3, 3, g=g), _bf_values(cout, cin, 1, 1, g=g)
+    n1, n2 = torch.rand(cout, generator=g) + 0.5, torch.rand(cout, generator=g) + 0.5
+    lengths = torch.tensor([4, 2])
+    y = O.front_stage(x, lengths, w1, w2, ws, n1, n2, s).double()
+    to, fo = (t - 1) // s + 1, (f - 1) // 2 + 1
+    assert y.shape == (b, to, fo, cout)
+    xd = x.double()
+
+    def conv3(src, w, st, sf, ti_max, fi_max, i, tt, ff):
+        acc = torch.zeros(w.shape[0], dtype=torch.float64)
+        for dy in range(3):
+            for dx in range(3):
+                ti, fi = tt * st + dy - 1, ff * sf + dx - 1
+                if 0 <= ti < ti_max and 0 <= fi < fi_max:
+                    acc += w[:, :, dy, dx].double() @ src[i, :, ti, fi]
+        return acc
+
+    def rms(v, w):
+        return v / torch.sqrt((v * v).mean() + 1e-5) * w.double()
+
+    h = torch.zeros(b, cout, to, fo, dtype=torch.float64)
+    for i in range(b):
+        for tt in range(int(lengths[i])):
+            for ff in range(fo):
+                h[i, :, tt, ff] = F.silu(rms(conv3(xd, w1, s, 2, t, f, i, tt, ff), n1))
+    for i in range(b):
+        for tt in range(to):
+            for ff in range(fo):
+                if tt >= lengths[i]:
+                    assert not y[i, tt, ff].any()
+                    continue
+                main = rms(conv3(h, w2, 1, 1, to, fo, i, tt, ff), n2)
+                skip = ws[:, :, 0, 0].double() @ xd[i, :, tt * s, ff * 2]
+                want = F.silu(main + skip)
+                assert torch.allclose(y[i, tt, ff], want, rtol=0.03, atol=0.03), (i, tt, ff)

@@ -9,7 +9,8 @@ The reference model's buffer and native kernels, each one C-ABI launch
   grid and the way back to frames;
 * ``RotaryQKV.apply`` (``buffers.py:46-56``);
 * ``front_norm`` (``buffers.py:58-80``) and ``bands`` (``native.py:157-163``)
-  of the CNN front end;
+  of the CNN front end, and ``front_stage``: a whole CNN stage (``front.py:19-43``:
+  both convolutions, norms, skip, residual and SiLU) in two fused kernels;
 * ``evidence_norm`` (``native.py:73-74``) and ``gated_concat``
   (``src/trifusion_l4/kernels/__init__.py:58-82``) of the block's merge.
 
@@ -128,6 +129,94 @@ def launch_front_norm(x, lengths, weight, eps, silu):
         _lib.stream_of(x),
     )
     _lib.check(status, "front_norm")
+    return y
+
+
+def pack_conv3x3(weight):
+    """``Conv2d`` 3x3 weight ``[cout, cin, 3, 3]`` -> tap-major bf16 ``[9, cout, cin]``
+    (tap = 3 dy + dx), the layout the front-stage kernels read."""
+    cout, cin = weight.shape[:2]
+    return weight.detach().permute(2, 3, 0, 1).reshape(9, cout, cin).to(torch.bfloat16).contiguous()
+
+
+def _aligned16(t):
+    """``t`` contiguous at a 16-byte aligned address (the kernels load 16 bytes at a time)."""
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+def _stage_input(x, what):
+    """Stage input ``[B, C, T, F]`` as the kernels read it: fp32 ``[B, T, F]`` for
+    one channel, else bf16 channels-last ``[B, T, F, C]``."""
+    b, c, t, f = x.shape
+    if c == 1:
+        if x.dtype != torch.float32:
+            raise TypeError(f"{what}: a one-channel stage input is the fp32 log spectrogram, got {x.dtype}")
+        return x.reshape(b, t, f).contiguous()
+    if x.dtype != torch.bfloat16:
+        raise TypeError(f"{what}: stage input must be bf16, got {x.dtype}")
+    return _aligned16(x.permute(0, 2, 3, 1))
+
+
+def front_stage(stage, x, lengths):
+    """One CNN stage of the front end (``front.py:19-43``) in two fused kernels:
+    ``x [B, C, T, F]`` (fp32 with one channel, else bf16) -> bf16 ``[B, C', T', F']``
+    view of a channels-last buffer. ``lengths`` are the stage's output lengths.
+    ``stage`` provides ``stride``, ``packed()`` -> (conv1, conv2, skip) weights and
+    the two norms (``trifusion_amd::front_conv1`` / ``front_conv2``)."""
+    w1, w2, ws = stage.packed()
+    n1, n2 = stage.norm1, stage.norm2
+    h = ops.front_conv1(x, w1, n1.weight, lengths, int(stage.stride), float(n1.eps))
+    y = ops.front_conv2(h, w2, n2.weight, x, ws, lengths, int(stage.stride), float(n2.eps))
+    return y.permute(0, 3, 1, 2)
+
+
+def _out_grid(x, stride):
+    _, _, t, f = x.shape
+    return (t - 1) // stride + 1, (f - 1) // 2 + 1
+
+
+def launch_front_conv1(x, weight, norm_weight, lengths, stride, eps):
+    lib = _lib.load()
+    _lib.require_cuda(x, weight, norm_weight, lengths, what="front_conv1")
+    b, cin, t, f = x.shape
+    cout = weight.shape[1]
+    if weight.shape != (9, cout, cin) or weight.dtype != torch.bfloat16 or norm_weight.shape != (cout,):
+        raise ValueError("front_conv1: weight must be bf16 [9, cout, cin] and the norm weight [cout]")
+    xs = _stage_input(x, "front_conv1")
+    w = _aligned16(weight)
+    to, fo = _out_grid(x, stride)
+    y = torch.empty((b, to, fo, cout), device=x.device, dtype=torch.bfloat16)
+    status = lib.tf_front_conv1(
+        xs.data_ptr(), _lib.dtype_code(xs, "front_conv1"), w.data_ptr(), norm_weight.float().contiguous().data_ptr(),
+        lengths.to(torch.int64).contiguous().data_ptr(), y.data_ptr(), b, t, f, cin, cout, int(stride), float(eps),
+        _lib.stream_of(x),
+    )
+    _lib.check(status, "front_conv1")
+    return y
+
+
+def launch_front_conv2(h, weight, norm_weight, x, skip_weight, lengths, stride, eps):
+    lib = _lib.load()
+    _lib.require_cuda(h, weight, norm_weight, x, skip_weight, lengths, what="front_conv2")
+    b, cin, t, f = x.shape
+    to, fo = _out_grid(x, stride)
+    cout = h.shape[-1]
+    if h.shape != (b, to, fo, cout) or h.dtype != torch.bfloat16:
+        raise ValueError(f"front_conv2: h must be bf16 [{b}, {to}, {fo}, cout], got {tuple(h.shape)} {h.dtype}")
+    if weight.shape != (9, cout, cout) or weight.dtype != torch.bfloat16 or norm_weight.shape != (cout,):
+        raise ValueError("front_conv2: weight must be bf16 [9, cout, cout] and the norm weight [cout]")
+    if skip_weight.shape != (cout, cin) or skip_weight.dtype != torch.bfloat16:
+        raise ValueError("front_conv2: skip weight must be bf16 [cout, cin]")
+    xs = _stage_input(x, "front_conv2")
+    hc, w, ws = _aligned16(h), _aligned16(weight), _aligned16(skip_weight)
+    y = torch.empty_like(hc)
+    status = lib.tf_front_conv2(
+        hc.data_ptr(), w.data_ptr(), norm_weight.float().contiguous().data_ptr(), xs.data_ptr(),
+        _lib.dtype_code(xs, "front_conv2"), ws.data_ptr(), lengths.to(torch.int64).contiguous().data_ptr(),
+        y.data_ptr(), b, t, f, cin, cout, int(stride), float(eps), _lib.stream_of(x),
+    )
+    _lib.check(status, "front_conv2")
     return y
 
 

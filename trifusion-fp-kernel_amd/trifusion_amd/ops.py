@@ -54,6 +54,11 @@ _SCHEMAS = {
     "bands": "bands(Tensor x) -> Tensor",
     "evidence_norm": "evidence_norm(Tensor x, Tensor value, Tensor gate, Tensor weight, Tensor? mask, float eps) -> Tensor",
     "gated_concat": "gated_concat(Tensor x, Tensor gate) -> Tensor",
+    "front_conv1": "front_conv1(Tensor x, Tensor weight, Tensor norm_weight, Tensor lengths, int stride, float eps) -> Tensor",
+    "front_conv2": (
+        "front_conv2(Tensor h, Tensor weight, Tensor norm_weight, Tensor x, Tensor skip_weight, Tensor lengths, "
+        "int stride, float eps) -> Tensor"
+    ),
 }
 
 OPERATORS = tuple(_SCHEMAS)
@@ -288,6 +293,15 @@ def _meta_gated_concat(x, gate):
     return torch.empty_like(x, memory_format=torch.contiguous_format)
 
 
+def _meta_front_conv1(x, weight, norm_weight, lengths, stride, eps):
+    b, _, t, f = x.shape
+    return x.new_empty((b, (t - 1) // stride + 1, (f - 1) // 2 + 1, weight.shape[1]), dtype=torch.bfloat16)
+
+
+def _meta_front_conv2(h, weight, norm_weight, x, skip_weight, lengths, stride, eps):
+    return torch.empty_like(h, memory_format=torch.contiguous_format)
+
+
 # ---- CPU kernels: loud failure, no fallback ----
 
 
@@ -322,7 +336,7 @@ _KERNELS = {
     **{
         name: (_block(name), globals()["_meta_" + name])
         for name in ("depthwise_masked", "pool4", "rotary_qkv", "front_norm", "interpolate", "bands",
-                     "evidence_norm", "gated_concat")
+                     "evidence_norm", "gated_concat", "front_conv1", "front_conv2")
     },
 }
 

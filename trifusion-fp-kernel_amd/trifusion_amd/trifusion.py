@@ -5,8 +5,10 @@ The reference model's layout and forward (``src/trifusion_l4/model.py``,
 parameter names, so a checkpoint saved from either loads into the other:
 
 * ``Frontend``: log power STFT (``torch.stft``, 512-point, hop 160, Hann 400),
-  three CNN stages (Conv2d + channel RMSNorm, ``tf_front_norm``) and 8
-  frequency bands (``tf_bands``) (``front.py:8-114``);
+  three CNN stages and 8 frequency bands (``tf_bands``) (``front.py:8-114``);
+  under bf16 autocast each stage is two fused kernels (``tf_front_conv1``: 3x3
+  conv, channel RMSNorm, SiLU; ``tf_front_conv2``: 3x3 conv, RMSNorm, 1x1 skip
+  conv, residual, SiLU), otherwise Conv2d with ``tf_front_norm``;
 * ``TriFusionBlock``: LocalCNN (GLU, masked depthwise conv ``tf_depthwise_masked``,
   RMSNorm), attention on the 4:1 pooled grid (``tf_pool4``, ``tf_rotary_qkv``,
   fp32 SDPA, ``tf_interpolate``), the evidence-gated norm (``tf_evidence_norm``),
@@ -38,7 +40,9 @@ from .kernels.block import (
     depthwise_masked,
     evidence_norm,
     front_norm,
+    front_stage,
     interpolate,
+    pack_conv3x3,
 )
 from .kernels.buffers import mask_buffer
 from .kernels.native import add, mean_norm
@@ -129,9 +133,24 @@ class CNNStage(nn.Module):
         self.conv2 = nn.Conv2d(cout, cout, 3, padding=1, bias=False)
         self.skip = nn.Conv2d(cin, cout, 1, stride=(stride, 2), bias=False)
         self.norm1, self.norm2 = RMSNorm(cout), RMSNorm(cout)
+        self._packed, self._packed_key = None, None
+
+    def packed(self):
+        """bf16 weights in the fused kernels' layout: conv1 and conv2 tap-major
+        ``[9, cout, cin]``, the skip ``[cout, cin]``; rebuilt when a weight changes."""
+        ws = (self.conv1.weight, self.conv2.weight, self.skip.weight)
+        key = tuple((w.data_ptr(), w._version, w.device) for w in ws)
+        if self._packed_key != key:
+            with torch.no_grad():
+                skip = ws[2].detach().flatten(1).to(torch.bfloat16).contiguous()
+                self._packed = (pack_conv3x3(ws[0]), pack_conv3x3(ws[1]), skip)
+            self._packed_key = key
+        return self._packed
 
     def forward(self, x, lengths):
         lengths = (lengths + self.stride - 1) // self.stride
+        if x.is_cuda and torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16:
+            return front_stage(self, x, lengths)
         h = front_norm(self.conv1(x), lengths, self.norm1, silu=True)
         h = front_norm(self.conv2(h), lengths, self.norm2)
         valid = time_mask(lengths, h.shape[2])[:, None, :, None]
@@ -170,9 +189,10 @@ class Frontend(nn.Module):
         if self.channels_last:
             x = x.contiguous(memory_format=torch.channels_last)
         fine = fine_lengths = None
-        # deterministic convolution algorithms: some of the library's faster
-        # ones accumulate in a run-dependent order, and repeated forwards (and
-        # graph replays against eager calls) must give the same bits
+        # outside bf16 autocast the stages run the library's convolutions, with
+        # deterministic algorithms: some of the faster ones accumulate in a
+        # run-dependent order, and repeated forwards (and graph replays against
+        # eager calls) must give the same bits
         with torch.backends.cudnn.flags(enabled=torch.backends.cudnn.enabled, benchmark=False, deterministic=True,
                                         allow_tf32=False):
             for i, stage in enumerate(self.stages):
