@@ -336,12 +336,13 @@ int tf_bands(const void *x, int32_t dtype, const int64_t *strides, void *y, int6
 
 /*
  * Evidence-gated RMSNorm: s = mask[r] ? x + a * 2 sigmoid(g) : 0 (fp32),
- * y = s rsqrt(mean(s^2) + eps) w (fp32); x fp32, a and g of ag_dtype, all
- * contiguous [rows, d]; mask uint8 [rows] or NULL. Replaces evidence_norm
- * (`_norm` MODE 1, src/trifusion_l4/kernels/native.py:9-39,73-74).
+ * y = s rsqrt(mean(s^2) + eps) w, computed in fp32 and stored as y_dtype (fp32, or
+ * bf16 for a consumer that casts it); x fp32, a and g of ag_dtype, all contiguous
+ * [rows, d]; mask uint8 [rows] or NULL. Replaces evidence_norm (`_norm` MODE 1,
+ * src/trifusion_l4/kernels/native.py:9-39,73-74).
  */
 int tf_evidence_norm(const float *x, const void *a, const void *g, int32_t ag_dtype, const uint8_t *mask,
-                     const float *w, float *y, int64_t rows, int64_t d, float eps, void *stream);
+                     const float *w, void *y, int32_t y_dtype, int64_t rows, int64_t d, float eps, void *stream);
 
 /*
  * Sigmoid-gated concatenation: y[r, k d + j] = x[r, k d + j] * 2 sigmoid(gate[r, k])
@@ -380,6 +381,63 @@ int tf_front_conv1(const void *x, int32_t x_dtype, const void *w, const float *n
 int tf_front_conv2(const void *h, const void *w, const float *norm_w, const void *x, int32_t x_dtype,
                    const void *w_skip, const int64_t *lengths, void *y, int64_t batch, int64_t time_in,
                    int64_t freq_in, int64_t cin, int64_t cout, int64_t stride, float eps, void *stream);
+
+/*
+ * Start of a TriFusion block under bf16 autocast: xm = mask(x) (rows t >= L_b zero,
+ * fp32), h = bf16(RMSNorm(xm) w) [B, T, d], and the 4:1 pooled grid
+ * p = bf16(mean of the fp32 norm rows 4j .. 4j+3 below L_b) [B, ceil(T/4), d].
+ * d % 8 == 0, d <= 4096; 16-byte aligned pointers. Replaces mask_buffer + pre +
+ * Grids.pool and the casts before local.up and attention.qkv
+ * (src/trifusion_l4/model.py:144-160, masking.py:59-67, kernels/buffers.py:13-44).
+ */
+int tf_block_pre(const float *x, const int64_t *lengths, const float *w, float eps, float *xm, void *h, void *p,
+                 int64_t batch, int64_t time, int64_t d, void *stream);
+
+/*
+ * RMSNorm of bf16 rows [rows, d] rounded to bf16, then SiLU rounded to bf16.
+ * Replaces F.silu(self.norm(h)) of LocalCNN (src/trifusion_l4/model.py:74).
+ */
+int tf_norm_silu(const void *x, const float *w, void *y, int64_t rows, int64_t d, float eps, void *stream);
+
+/*
+ * F.glu over the last dim of up [B, T, 2d] (bf16(a sigmoid(b))), then the masked
+ * depthwise conv of kernel k (3 or 7, padding k/2; w bf16 [d, k], bias bf16 [d]):
+ * y [B, T, d] bf16, rows t >= L_b zero. Replaces F.glu + depthwise_masked of
+ * LocalCNN (src/trifusion_l4/model.py:73, kernels/buffers.py:13-32).
+ */
+int tf_glu_depthwise(const void *up, const void *w, const void *bias, const int64_t *lengths, void *y,
+                     int64_t batch, int64_t time, int64_t d, int64_t k, void *stream);
+
+/*
+ * Attention on the pooled grid: qkv bf16 [B, T, 3, H, D] (D 32 or 64); q and k
+ * rotated by interleaved pairs with cos/sin fp32 [T, D/2] and rounded to bf16;
+ * softmax(q k^T / sqrt(D)) v in fp32 over keys j < low_lengths[b]; y bf16
+ * [B, T, H D]. Replaces RotaryQKV + masked_attention + the head merge of
+ * GlobalAttention (src/trifusion_l4/model.py:84-104, attention.py:8-18).
+ */
+int tf_pooled_attention(const void *qkv, const float *cos_t, const float *sin_t, const int64_t *low_lengths,
+                        void *y, int64_t batch, int64_t low_time, int64_t heads, int64_t head_dim, void *stream);
+
+/*
+ * Merge of the two Mamba directions and the 3-way gate: mn = RMSNorm((mf + mb) / 2) w
+ * (fp32 [rows, d]), g = bf16(cat(cn, bf16(mn), an) gate_w^T + gate_b) (bf16
+ * [rows, 3]); cn, mf, mb, an bf16 [rows, d]; gate_w bf16 [3, 3d], gate_b bf16 [3].
+ * Replaces mean_norm + torch.cat + the gate linear (src/trifusion_l4/model.py:180-186).
+ */
+int tf_merge_gate(const void *cn, const void *mf, const void *mb, const void *an, const float *norm_w, float eps,
+                  const void *gate_w, const void *gate_b, float *mn, void *g, int64_t rows, int64_t d,
+                  void *stream);
+
+/*
+ * Gated concatenation, masked depthwise merge and residual add: v = cat(cn, mn, an)
+ * * 2 sigmoid(g) (fp32), c = masked depthwise conv (kernel k = 3; w bf16 [3d, k],
+ * bias bf16 [3d]) of bf16(v), rounded to bf16, zero at t >= L_b; y = bf16(v + c)
+ * [B, T, 3d]. Replaces gated_concat + merge_dw + add(bf16=True)
+ * (src/trifusion_l4/model.py:187-196).
+ */
+int tf_merge_conv(const void *cn, const float *mn, const void *an, const void *g, const void *w, const void *bias,
+                  const int64_t *lengths, void *y, int64_t batch, int64_t time, int64_t d, int64_t k,
+                  void *stream);
 
 /* Library version string (static storage). */
 const char *tf_version(void);

@@ -20,7 +20,13 @@ replace:
 * ``gated_concat``: the reference branch (``kernels/__init__.py:59-63``);
 * ``front_stage``: a whole CNN stage (``front.py:19-43``) under bf16 autocast:
   ``F.conv2d`` on bf16-rounded operands with bf16 outputs, ``front_norm``, the
-  1x1 skip, the bf16 residual sum and SiLU, rows past the length cleared.
+  1x1 skip, the bf16 residual sum and SiLU, rows past the length cleared;
+* the block's fused runs under bf16 autocast (``model.py:140-200``), each the
+  composition of the functions above and the elementwise oracle with the casts
+  autocast makes: ``block_pre`` (mask, pre norm, 4:1 pool), ``glu_depthwise``,
+  ``norm_silu``, ``pooled_attention`` (rotary, fp32 SDPA, head merge),
+  ``merge_gate`` (mean norm, gate linear) and ``merge_conv`` (gated concat,
+  depthwise merge, bf16 add).
 
 Pinning (tests/test_oracle_trifusion.py): each against an explicit loop or
 closed form on small inputs.
@@ -29,7 +35,7 @@ closed form on small inputs.
 import torch
 import torch.nn.functional as F
 
-from .elementwise import mask_rows, time_mask
+from .elementwise import mask_rows, mean_norm, rms_norm, time_mask
 
 
 def depthwise_masked(x, weight, bias, lengths):
@@ -127,3 +133,49 @@ def front_stage(x, lengths, conv1, conv2, skip, norm1, norm2, stride, eps=1e-5):
     valid = time_mask(lengths, h.shape[1])[:, :, None, None]
     sk = conv(x, skip, (stride, 2), 0).permute(0, 2, 3, 1).masked_fill(~valid, 0)
     return F.silu(_bf(h + sk)).masked_fill(~valid, 0).to(torch.bfloat16)
+
+
+BF16 = torch.bfloat16
+
+
+def block_pre(x, lengths, weight, eps=1e-5):
+    """``(mask(x), bf16(pre(x)), bf16(pool4(pre(x))))`` of the fp32 stream."""
+    xm = mask_rows(x.float(), time_mask(lengths, x.shape[1]))
+    h = rms_norm(xm, weight, eps)
+    return xm, h.to(BF16), pool4(h, lengths).to(BF16)
+
+
+def glu_depthwise(up, weight, bias, lengths):
+    """``depthwise_masked(F.glu(up))`` on bf16 values."""
+    return depthwise_masked(F.glu(up.float(), -1).to(BF16), weight.to(BF16), bias.to(BF16), lengths)
+
+
+def norm_silu(x, weight, eps=1e-5):
+    """``silu(rms_norm(x))`` of bf16 rows, each rounded to bf16."""
+    return F.silu(rms_norm(x.to(BF16), weight, eps).float()).to(BF16)
+
+
+def pooled_attention(qkv, cos, sin, low_lengths, heads):
+    """Rotary q/k (bf16), fp32 masked SDPA, heads merged: ``[B, T, H D]`` bf16."""
+    b, t, _ = qkv.shape
+    q, k, v = rotary_qkv(qkv.to(BF16), cos, sin, heads).float().unbind(0)
+    mask = time_mask(low_lengths, t)[:, None, None, :]
+    y = F.scaled_dot_product_attention(q, k, v, attn_mask=mask)
+    return y.transpose(1, 2).reshape(b, t, -1).to(BF16)
+
+
+def merge_gate(cn, mf, mb, an, weight, gate_w, gate_b, eps=1e-5):
+    """``mn = mean_norm(mf, mb)`` (fp32) and the gate linear of ``cat(cn, mn, an)``
+    under autocast (bf16 operands, fp32 sums, bf16 result)."""
+    mn = mean_norm(mf, mb, weight, eps)
+    s = torch.cat((cn.float(), mn, an.float()), -1).to(BF16).float()
+    g = s @ gate_w.to(BF16).float().t() + gate_b.to(BF16).float()
+    return mn, g.to(BF16)
+
+
+def merge_conv(cn, mn, an, g, weight, bias, lengths):
+    """``bf16(v + depthwise_masked(bf16(v)))`` with ``v = gated_concat(cat(cn, mn, an), g)``
+    in fp32."""
+    v = gated_concat(torch.cat((cn.float(), mn.float(), an.float()), -1), g)
+    conv = depthwise_masked(v.to(BF16), weight.to(BF16), bias.to(BF16), lengths).float()
+    return (v + conv).to(BF16)

@@ -1,0 +1,148 @@
+"""Fused TriFusion block kernels on MI355X against the oracle's compositions of
+the unfused reference ops (bf16 autocast values), and against the unfused GPU
+kernels the block otherwise runs. Tolerances: bf16 outputs within one bf16 step
+of the oracle (rtol 2^-7 plus 2^-7 of the largest magnitude; two steps where a
+bf16 value feeds a second rounding), fp32 outputs within 1e-5 of the largest
+magnitude. Against the unfused GPU kernels, outputs with the same per-element
+arithmetic are bit-identical; the gate dot product and the attention sum in a
+different order and are held to the oracle's tolerance."""
+
+from types import SimpleNamespace
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import trifusion as O
+from oracle.elementwise import mean_norm as o_mean_norm
+from oracle.elementwise import time_mask
+from trifusion_amd.kernels import RMSNorm, gated_concat
+from trifusion_amd.kernels.block import (
+    Pool4,
+    block_pre,
+    depthwise_masked,
+    evidence_norm,
+    glu_depthwise,
+    merge_conv,
+    merge_gate,
+    norm_silu,
+    pooled_attention,
+)
+from trifusion_amd.kernels.buffers import mask_buffer
+from trifusion_amd.kernels.native import add, mean_norm
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+BF = torch.bfloat16
+LENGTHS = torch.tensor([101, 57, 4])
+
+
+def gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def close_bf16(y, ref, steps=1):
+    y, ref = y.float().cpu(), ref.float().cpu()
+    tol = steps * 2 ** -7
+    torch.testing.assert_close(y, ref, rtol=tol, atol=tol * ref.abs().max().item())
+
+
+def norm(d, g):
+    n = RMSNorm(d)
+    with torch.no_grad():
+        n.weight.copy_(torch.rand(d, generator=g) + 0.5)
+    return n
+
+
+def test_block_pre():
+    g = gen(0)
+    x = torch.randn(3, 101, 1024, generator=g)
+    n = norm(1024, g)
+    xm, h, p = block_pre(x.to(DEV), LENGTHS.to(DEV), n.to(DEV))
+    rm, rh, rp = O.block_pre(x, LENGTHS, n.weight.detach().cpu())
+    assert torch.equal(xm.cpu(), rm)
+    close_bf16(h, rh)
+    close_bf16(p, rp)
+    # the unfused GPU ops: mask, fp32 norm, casts, fp32 pooling
+    mask = time_mask(LENGTHS, 101).to(DEV)
+    um = mask_buffer(x.to(DEV), mask)
+    uh = n(um)
+    assert torch.equal(h, uh.to(BF))
+    assert torch.equal(p, Pool4.apply(uh, LENGTHS.to(DEV)).to(BF))
+
+
+@pytest.mark.parametrize("k", [3, 7])
+def test_glu_depthwise_and_norm_silu(k):
+    g = gen(k)
+    up = torch.randn(3, 101, 2048, generator=g).to(BF)
+    layer = torch.nn.Conv1d(1024, 1024, k, padding=k // 2, groups=1024)
+    w, b = layer.weight.detach().clone(), layer.bias.detach().clone()
+    y = glu_depthwise(up.to(DEV), layer.to(DEV), LENGTHS.to(DEV))
+    ref = O.glu_depthwise(up, w, b, LENGTHS)
+    close_bf16(y, ref, steps=2)
+    assert not y[1, 57:].any() and not y[2, 4:].any()
+    with torch.autocast("cuda", dtype=BF):
+        unfused = depthwise_masked(F.glu(up.to(DEV), dim=-1), layer, LENGTHS.to(DEV))
+    assert torch.equal(y, unfused)
+    n = norm(1024, g)
+    s = norm_silu(ref.to(DEV), n.to(DEV))
+    close_bf16(s, O.norm_silu(ref, n.weight.detach().cpu()))
+    assert torch.equal(s, F.silu(n(ref.to(DEV))))
+
+
+@pytest.mark.parametrize("t,heads,hd", [(26, 16, 64), (101, 8, 32)])
+def test_pooled_attention(t, heads, hd):
+    g = gen(t)
+    qkv = torch.randn(3, t, 3 * heads * hd, generator=g).to(BF)
+    low = torch.tensor([t, (t + 1) // 2, 1])
+    phase = torch.arange(t).float()[:, None] * 10000.0 ** (-torch.arange(0, hd, 2).float() / hd)[None, :]
+    grids = SimpleNamespace(rope_cos=phase.cos().to(DEV), rope_sin=phase.sin().to(DEV), low_lengths=low.to(DEV))
+    y = pooled_attention(qkv.to(DEV), grids, heads)
+    ref = O.pooled_attention(qkv, phase.cos(), phase.sin(), low, heads)
+    assert y.shape == ref.shape
+    close_bf16(y, ref, steps=2)
+
+
+def test_merge_gate_and_conv():
+    g = gen(11)
+    d = 1024
+    cn, an = (torch.randn(3, 101, d, generator=g).to(BF) for _ in range(2))
+    mf, mb = (torch.randn(3, 101, d, generator=g).to(BF) for _ in range(2))
+    n = norm(d, g)
+    gate = torch.nn.Linear(3 * d, 3)
+    with torch.no_grad():
+        gate.weight.copy_(torch.randn(3, 3 * d, generator=g) * 0.02)
+        gate.bias.copy_(torch.randn(3, generator=g))
+    dev = [t.to(DEV) for t in (cn, mf, mb, an)]
+    mn, gg = merge_gate(*dev, n.to(DEV), gate.to(DEV))
+    rmn, rg = O.merge_gate(cn, mf, mb, an, n.weight.detach().cpu(), gate.weight.detach().cpu(),
+                           gate.bias.detach().cpu())
+    scale = rmn.abs().max().item()
+    assert ((mn.cpu() - rmn).abs().max().item()) <= 1e-5 * scale
+    assert torch.equal(mn, mean_norm(dev[1], dev[2], n.weight, n.eps))
+    close_bf16(gg, rg, steps=2)
+    layer = torch.nn.Conv1d(3 * d, 3 * d, 3, padding=1, groups=3 * d)
+    w, b = layer.weight.detach().clone(), layer.bias.detach().clone()
+    lengths = LENGTHS.to(DEV)
+    # zero-preserved inputs: rows past each length are 0 in the block
+    valid = time_mask(LENGTHS, 101)[..., None]
+    cn, an, rmn = cn * valid, an * valid, rmn * valid
+    y = merge_conv(cn.to(DEV), rmn.to(DEV), an.to(DEV), rg.to(DEV), layer.to(DEV), lengths)
+    close_bf16(y, O.merge_conv(cn, rmn, an, rg, w, b, LENGTHS))
+    s = torch.cat((cn.to(DEV).float(), rmn.to(DEV), an.to(DEV).float()), -1)
+    v = gated_concat(s, rg.to(DEV).float())
+    with torch.autocast("cuda", dtype=BF):
+        conv = depthwise_masked(v, layer, lengths)
+    assert torch.equal(y, add(v, conv, bf16=True))
+
+
+def test_evidence_norm_bf16_out():
+    g = gen(12)
+    x = torch.randn(2, 101, 1024, generator=g).to(DEV)
+    value = torch.randn(2, 101, 1024, generator=g).to(BF).to(DEV)
+    gate = torch.randn(2, 101, 1024, generator=g).to(BF).to(DEV)
+    w = (torch.rand(1024, generator=g) + 0.5).to(DEV)
+    mask = (torch.rand(2, 101, generator=g) > 0.2).to(DEV)
+    y32 = evidence_norm(x, value, gate, w, mask)
+    y16 = evidence_norm(x, value, gate, w, mask, bf16_out=True)
+    assert y16.dtype == BF and torch.equal(y16, y32.to(BF))

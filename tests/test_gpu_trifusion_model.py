@@ -7,7 +7,7 @@ import pytest
 import torch
 
 from oracle.trifusion_model import trifusion_forward
-from trifusion_amd import runtime
+from trifusion_amd import runtime, trifusion
 from trifusion_amd.trifusion import TriFusion, TriFusionConfig
 
 pytestmark = pytest.mark.gpu
@@ -39,11 +39,26 @@ def inputs(b=3, n=32000, seed=7):
     return audio, lengths, channels
 
 
-def test_trifusion_matches_oracle():
+def test_trifusion_matches_oracle(monkeypatch):
     model = make_model()
     audio, lengths, channels = inputs()
     eng = runtime.InferenceEngine(model)
+    # the fused block and front-stage kernels are the path under test
+    calls = {"block": 0, "stage": 0}
+    block_fused, stage = type(model.blocks[0]).forward_fused, trifusion.front_stage
+
+    def count_block(*a, **k):
+        calls["block"] += 1
+        return block_fused(*a, **k)
+
+    def count_stage(*a, **k):
+        calls["stage"] += 1
+        return stage(*a, **k)
+
+    monkeypatch.setattr(type(model.blocks[0]), "forward_fused", count_block)
+    monkeypatch.setattr(trifusion, "front_stage", count_stage)
     out = eng.eager(audio.to(DEV), lengths.to(DEV), channels.to(DEV)).cpu()
+    assert calls == {"block": SMALL["depth"], "stage": 3}
     ref = trifusion_forward(model.state_dict(), model.config, audio, lengths, channels)
     diff = (out.sigmoid() - ref.sigmoid()).abs().max().item()
     print(f"trifusion prob max diff {diff:.2e}", flush=True)

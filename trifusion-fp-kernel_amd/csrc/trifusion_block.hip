@@ -188,11 +188,11 @@ __global__ __launch_bounds__(256) void bands_kernel(const T* __restrict__ x, T* 
 // s = mask[row] ? x + a * (2 sigmoid(g)) : 0 (fp32), y = s rsqrt(mean(s^2) + eps) w
 // in fp32 (kernels/native.py:_norm MODE 1 via evidence_norm). One wave per row;
 // the second pass recomputes s from the (now cached) row.
-template <typename TA>
+template <typename TA, typename TY>
 __global__ __launch_bounds__(256) void evidence_norm_kernel(const float* __restrict__ x, const TA* __restrict__ a,
                                                             const TA* __restrict__ g,
                                                             const uint8_t* __restrict__ mask,
-                                                            const float* __restrict__ w, float* __restrict__ y,
+                                                            const float* __restrict__ w, TY* __restrict__ y,
                                                             int64_t rows, int D, float eps) {
   const int lane = threadIdx.x & 63;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
@@ -209,7 +209,7 @@ __global__ __launch_bounds__(256) void evidence_norm_kernel(const float* __restr
   }
   ss = wave_sum(ss);
   const float r = rsqrtf(ss / static_cast<float>(D) + eps);
-  for (int c = lane; c < D; c += 64) y[row * D + c] = value(c) * r * w[c];
+  for (int c = lane; c < D; c += 64) y[row * D + c] = from_f32<TY>(value(c) * r * w[c]);
 }
 
 // y[row, k d + j] = x[row, k d + j] * 2 sigmoid(gate[row, k]), k < 3
@@ -328,16 +328,24 @@ extern "C" int tf_bands(const void* x, int32_t dtype, const int64_t* strides, vo
 }
 
 extern "C" int tf_evidence_norm(const float* x, const void* a, const void* g, int32_t ag_dtype, const uint8_t* mask,
-                                const float* w, float* y, int64_t rows, int64_t d, float eps, void* stream) {
+                                const float* w, void* y, int32_t y_dtype, int64_t rows, int64_t d, float eps,
+                                void* stream) {
   if (!x || !a || !g || !w || !y) return TF_ERR_NULL;
   if (rows < 0 || d < 1) return TF_ERR_SHAPE;
+  if (y_dtype != TF_FLOAT32 && y_dtype != TF_BFLOAT16) return TF_ERR_DTYPE;
   if (rows == 0) return TF_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(tf::nblocks(rows, tf::kWaves));
   TF_DISPATCH(ag_dtype, TA,
-              hipLaunchKernelGGL(tf::evidence_norm_kernel<TA>, dim3(tf::nblocks(rows, tf::kWaves)), dim3(256), 0, s,
-                                 x, static_cast<const TA*>(a), static_cast<const TA*>(g), mask, w, y, rows,
-                                 static_cast<int>(d), eps);
-              return tf::launch_status());
+              if (y_dtype == TF_FLOAT32) {
+                hipLaunchKernelGGL((tf::evidence_norm_kernel<TA, float>), grid, dim3(256), 0, s, x,
+                                   static_cast<const TA*>(a), static_cast<const TA*>(g), mask, w,
+                                   static_cast<float*>(y), rows, static_cast<int>(d), eps);
+              } else {
+                hipLaunchKernelGGL((tf::evidence_norm_kernel<TA, tf::bf16_t>), grid, dim3(256), 0, s, x,
+                                   static_cast<const TA*>(a), static_cast<const TA*>(g), mask, w,
+                                   static_cast<tf::bf16_t*>(y), rows, static_cast<int>(d), eps);
+              } return tf::launch_status());
   return TF_ERR_DTYPE;
 }
 

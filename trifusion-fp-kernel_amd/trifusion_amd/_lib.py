@@ -106,7 +106,7 @@ _SIGNATURES = {
     ),
     "tf_interpolate": ([c_ptr, c_i32, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_ptr], c_i32),
     "tf_bands": ([c_ptr, c_i32, ctypes.POINTER(c_i64), c_ptr, c_i64, c_i64, c_i64, c_i64, c_ptr], c_i32),
-    "tf_evidence_norm": ([c_ptr, c_ptr, c_ptr, c_i32, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_f32, c_ptr], c_i32),
+    "tf_evidence_norm": ([c_ptr, c_ptr, c_ptr, c_i32, c_ptr, c_ptr, c_ptr, c_i32, c_i64, c_i64, c_f32, c_ptr], c_i32),
     "tf_gated_concat": ([c_ptr, c_ptr, c_i32, c_ptr, c_i64, c_i64, c_ptr], c_i32),
     "tf_front_conv1": (
         [c_ptr, c_i32, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_f32, c_ptr],
@@ -115,6 +115,18 @@ _SIGNATURES = {
     "tf_front_conv2": (
         [c_ptr, c_ptr, c_ptr, c_ptr, c_i32, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_f32,
          c_ptr],
+        c_i32,
+    ),
+    "tf_block_pre": ([c_ptr, c_ptr, c_ptr, c_f32, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_ptr], c_i32),
+    "tf_norm_silu": ([c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_f32, c_ptr], c_i32),
+    "tf_glu_depthwise": ([c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_ptr], c_i32),
+    "tf_pooled_attention": ([c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_ptr], c_i32),
+    "tf_merge_gate": (
+        [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_f32, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_ptr],
+        c_i32,
+    ),
+    "tf_merge_conv": (
+        [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_ptr],
         c_i32,
     ),
     "tf_version": ([], ctypes.c_char_p),

@@ -258,13 +258,14 @@ def launch_bands(x):
     return y
 
 
-def evidence_norm(x, value, gate, weight, mask, eps=1e-5):
-    """``rms(mask ? x + value * 2 sigmoid(gate) : 0) * weight`` in fp32
+def evidence_norm(x, value, gate, weight, mask, eps=1e-5, bf16_out=False):
+    """``rms(mask ? x + value * 2 sigmoid(gate) : 0) * weight`` in fp32, stored as
+    fp32 or, with ``bf16_out``, rounded to bf16 for a consumer that would cast it
     (``trifusion_amd::evidence_norm``)."""
-    return ops.evidence_norm(x, value, gate, weight, mask, float(eps))
+    return ops.evidence_norm(x, value, gate, weight, mask, float(eps), bool(bf16_out))
 
 
-def launch_evidence_norm(x, value, gate, weight, mask, eps=1e-5):
+def launch_evidence_norm(x, value, gate, weight, mask, eps=1e-5, bf16_out=False):
     lib = _lib.load()
     _lib.require_cuda(x, value, gate, weight, mask, what="evidence_norm")
     x = x.float().contiguous()
@@ -281,10 +282,11 @@ def launch_evidence_norm(x, value, gate, weight, mask, eps=1e-5):
         if mask.dtype != torch.bool or mask.numel() != rows:
             raise ValueError("evidence_norm: mask must be bool with one entry per row")
         m = mask.contiguous().data_ptr()
-    y = torch.empty(x.shape, device=x.device, dtype=torch.float32)
+    y = torch.empty(x.shape, device=x.device, dtype=torch.bfloat16 if bf16_out else torch.float32)
     status = lib.tf_evidence_norm(x.data_ptr(), value.data_ptr(), gate.data_ptr(),
                                   _lib.dtype_code(value, "evidence_norm"), m, weight.float().contiguous().data_ptr(),
-                                  y.data_ptr(), rows, d, float(eps), _lib.stream_of(x))
+                                  y.data_ptr(), _lib.dtype_code(y, "evidence_norm"), rows, d, float(eps),
+                                  _lib.stream_of(x))
     _lib.check(status, "evidence_norm")
     return y
 
@@ -307,4 +309,154 @@ def launch_gated_concat(x, gate):
     status = lib.tf_gated_concat(x.data_ptr(), gate.data_ptr(), _lib.dtype_code(x, "gated_concat"), y.data_ptr(),
                                  gate.numel() // 3, d, _lib.stream_of(x))
     _lib.check(status, "gated_concat")
+    return y
+
+
+# ---- fused block kernels (csrc/block_fused.hip) ----
+
+
+def _bf16(t, what, name):
+    if t.dtype != torch.bfloat16:
+        raise TypeError(f"{what}: {name} must be bf16, got {t.dtype}")
+    return _aligned16(t)
+
+
+def _lengths(lengths):
+    return lengths.to(torch.int64).contiguous()
+
+
+def block_pre(x, lengths, norm):
+    """Start of a block: ``(mask(x) fp32, bf16(pre(x)), bf16(pool4(pre(x))))``
+    (``trifusion_amd::block_pre``)."""
+    return ops.block_pre(x, lengths, norm.weight, float(norm.eps))
+
+
+def launch_block_pre(x, lengths, weight, eps):
+    lib = _lib.load()
+    _lib.require_cuda(x, lengths, weight, what="block_pre")
+    if x.dtype != torch.float32 or x.dim() != 3:
+        raise TypeError("block_pre: x must be fp32 [B, T, d]")
+    b, t, d = x.shape
+    xc, w = _aligned16(x), _aligned16(weight.float())
+    xm = torch.empty_like(xc)
+    h = torch.empty((b, t, d), device=x.device, dtype=torch.bfloat16)
+    p = torch.empty((b, (t + 3) // 4, d), device=x.device, dtype=torch.bfloat16)
+    status = lib.tf_block_pre(xc.data_ptr(), _lengths(lengths).data_ptr(), w.data_ptr(), float(eps), xm.data_ptr(),
+                              h.data_ptr(), p.data_ptr(), b, t, d, _lib.stream_of(x))
+    _lib.check(status, "block_pre")
+    return xm, h, p
+
+
+def norm_silu(x, norm):
+    """``silu(norm(x))`` of bf16 rows, both rounded to bf16 (``trifusion_amd::norm_silu``)."""
+    return ops.norm_silu(x, norm.weight, float(norm.eps))
+
+
+def launch_norm_silu(x, weight, eps):
+    lib = _lib.load()
+    _lib.require_cuda(x, weight, what="norm_silu")
+    xc, w = _bf16(x, "norm_silu", "x"), _aligned16(weight.float())
+    d = x.shape[-1]
+    y = torch.empty_like(xc)
+    status = lib.tf_norm_silu(xc.data_ptr(), w.data_ptr(), y.data_ptr(), x.numel() // d, d, float(eps),
+                              _lib.stream_of(x))
+    _lib.check(status, "norm_silu")
+    return y
+
+
+def glu_depthwise(up, layer, lengths):
+    """``depthwise_masked(F.glu(up), layer, lengths)`` in bf16 (``trifusion_amd::glu_depthwise``)."""
+    return ops.glu_depthwise(up, layer.weight, layer.bias, lengths)
+
+
+def launch_glu_depthwise(up, weight, bias, lengths):
+    lib = _lib.load()
+    _lib.require_cuda(up, weight, bias, lengths, what="glu_depthwise")
+    uc = _bf16(up, "glu_depthwise", "up")
+    b, t, d2 = uc.shape
+    d, k = d2 // 2, weight.shape[-1]
+    if weight.numel() != d * k or bias.shape != (d,):
+        raise ValueError("glu_depthwise: weight must be [d, 1, k] and bias [d]")
+    w = weight.to(torch.bfloat16).contiguous()
+    bb = bias.to(torch.bfloat16).contiguous()
+    y = torch.empty((b, t, d), device=up.device, dtype=torch.bfloat16)
+    status = lib.tf_glu_depthwise(uc.data_ptr(), w.data_ptr(), bb.data_ptr(), _lengths(lengths).data_ptr(),
+                                  y.data_ptr(), b, t, d, k, _lib.stream_of(up))
+    _lib.check(status, "glu_depthwise")
+    return y
+
+
+def pooled_attention(qkv, grids, heads):
+    """Rotary + masked attention on the pooled grid: ``qkv [B, T, 3 H D]`` bf16 ->
+    ``[B, T, H D]`` bf16 (``trifusion_amd::pooled_attention``)."""
+    return ops.pooled_attention(qkv, grids.rope_cos, grids.rope_sin, grids.low_lengths, int(heads))
+
+
+def launch_pooled_attention(qkv, cos, sin, low_lengths, heads):
+    lib = _lib.load()
+    _lib.require_cuda(qkv, cos, sin, low_lengths, what="pooled_attention")
+    qc = _bf16(qkv, "pooled_attention", "qkv")
+    b, t, width = qc.shape
+    hd = width // (3 * heads)
+    if width != 3 * heads * hd or cos.shape != (t, hd // 2) or sin.shape != (t, hd // 2):
+        raise ValueError("pooled_attention: qkv must be [B, T, 3 H D] with cos/sin [T, D/2]")
+    y = torch.empty((b, t, heads * hd), device=qkv.device, dtype=torch.bfloat16)
+    status = lib.tf_pooled_attention(qc.data_ptr(), cos.float().contiguous().data_ptr(),
+                                     sin.float().contiguous().data_ptr(), _lengths(low_lengths).data_ptr(),
+                                     y.data_ptr(), b, t, heads, hd, _lib.stream_of(qkv))
+    _lib.check(status, "pooled_attention")
+    return y
+
+
+def merge_gate(cn, mf, mb, an, norm, gate):
+    """``(mean_norm(mf, mb) fp32, gate(cat(cn, mn, an)) bf16 [.., 3])``
+    (``trifusion_amd::merge_gate``)."""
+    return ops.merge_gate(cn, mf, mb, an, norm.weight, float(norm.eps), gate.weight, gate.bias)
+
+
+def launch_merge_gate(cn, mf, mb, an, norm_weight, eps, gate_weight, gate_bias):
+    lib = _lib.load()
+    _lib.require_cuda(cn, mf, mb, an, norm_weight, gate_weight, gate_bias, what="merge_gate")
+    cc, fc, bc, ac = (_bf16(t, "merge_gate", n) for t, n in ((cn, "cn"), (mf, "mf"), (mb, "mb"), (an, "an")))
+    d = cc.shape[-1]
+    rows = cc.numel() // d
+    if any(t.shape != cc.shape for t in (fc, bc, ac)) or gate_weight.shape != (3, 3 * d) or gate_bias.shape != (3,):
+        raise ValueError("merge_gate: cn, mf, mb, an must match and the gate be Linear(3 d, 3)")
+    gw = _aligned16(gate_weight.to(torch.bfloat16))
+    gb = gate_bias.to(torch.bfloat16).contiguous()
+    w = _aligned16(norm_weight.float())
+    mn = torch.empty(cc.shape, device=cn.device, dtype=torch.float32)
+    g = torch.empty((*cc.shape[:-1], 3), device=cn.device, dtype=torch.bfloat16)
+    status = lib.tf_merge_gate(cc.data_ptr(), fc.data_ptr(), bc.data_ptr(), ac.data_ptr(), w.data_ptr(), float(eps),
+                               gw.data_ptr(), gb.data_ptr(), mn.data_ptr(), g.data_ptr(), rows, d, _lib.stream_of(cn))
+    _lib.check(status, "merge_gate")
+    return mn, g
+
+
+def merge_conv(cn, mn, an, g, layer, lengths):
+    """``add(v, depthwise_masked(v, layer), bf16=True)`` with ``v = gated_concat(cat(cn,
+    mn, an), g)`` (``trifusion_amd::merge_conv``)."""
+    return ops.merge_conv(cn, mn, an, g, layer.weight, layer.bias, lengths)
+
+
+def launch_merge_conv(cn, mn, an, g, weight, bias, lengths):
+    lib = _lib.load()
+    _lib.require_cuda(cn, mn, an, g, weight, bias, lengths, what="merge_conv")
+    cc, ac, gc = _bf16(cn, "merge_conv", "cn"), _bf16(an, "merge_conv", "an"), _bf16(g, "merge_conv", "g")
+    if mn.dtype != torch.float32:
+        raise TypeError("merge_conv: mn must be fp32")
+    mc = _aligned16(mn)
+    b, t, d = cc.shape
+    k = weight.shape[-1]
+    if mc.shape != cc.shape or ac.shape != cc.shape or gc.shape != (b, t, 3):
+        raise ValueError("merge_conv: cn, mn, an must be [B, T, d] and g [B, T, 3]")
+    if weight.numel() != 3 * d * k or bias.shape != (3 * d,):
+        raise ValueError("merge_conv: weight must be [3 d, 1, k] and bias [3 d]")
+    w = weight.to(torch.bfloat16).contiguous()
+    bb = bias.to(torch.bfloat16).contiguous()
+    y = torch.empty((b, t, 3 * d), device=cn.device, dtype=torch.bfloat16)
+    status = lib.tf_merge_conv(cc.data_ptr(), mc.data_ptr(), ac.data_ptr(), gc.data_ptr(), w.data_ptr(),
+                               bb.data_ptr(), _lengths(lengths).data_ptr(), y.data_ptr(), b, t, d, k,
+                               _lib.stream_of(cn))
+    _lib.check(status, "merge_conv")
     return y

@@ -52,9 +52,25 @@ _SCHEMAS = {
     "front_norm": "front_norm(Tensor x, Tensor lengths, Tensor weight, float eps, bool silu) -> Tensor",
     "interpolate": "interpolate(Tensor low, Tensor left, Tensor right, Tensor alpha, Tensor lengths) -> Tensor",
     "bands": "bands(Tensor x) -> Tensor",
-    "evidence_norm": "evidence_norm(Tensor x, Tensor value, Tensor gate, Tensor weight, Tensor? mask, float eps) -> Tensor",
+    "evidence_norm": (
+        "evidence_norm(Tensor x, Tensor value, Tensor gate, Tensor weight, Tensor? mask, float eps, "
+        "bool bf16_out=False) -> Tensor"
+    ),
     "gated_concat": "gated_concat(Tensor x, Tensor gate) -> Tensor",
     "front_conv1": "front_conv1(Tensor x, Tensor weight, Tensor norm_weight, Tensor lengths, int stride, float eps) -> Tensor",
+    "block_pre": "block_pre(Tensor x, Tensor lengths, Tensor weight, float eps) -> (Tensor, Tensor, Tensor)",
+    "norm_silu": "norm_silu(Tensor x, Tensor weight, float eps) -> Tensor",
+    "glu_depthwise": "glu_depthwise(Tensor up, Tensor weight, Tensor bias, Tensor lengths) -> Tensor",
+    "pooled_attention": (
+        "pooled_attention(Tensor qkv, Tensor cos, Tensor sin, Tensor low_lengths, int heads) -> Tensor"
+    ),
+    "merge_gate": (
+        "merge_gate(Tensor cn, Tensor mf, Tensor mb, Tensor an, Tensor norm_weight, float eps, Tensor gate_weight, "
+        "Tensor gate_bias) -> (Tensor, Tensor)"
+    ),
+    "merge_conv": (
+        "merge_conv(Tensor cn, Tensor mn, Tensor an, Tensor g, Tensor weight, Tensor bias, Tensor lengths) -> Tensor"
+    ),
     "front_conv2": (
         "front_conv2(Tensor h, Tensor weight, Tensor norm_weight, Tensor x, Tensor skip_weight, Tensor lengths, "
         "int stride, float eps) -> Tensor"
@@ -285,8 +301,34 @@ def _meta_bands(x):
     return x.new_empty((b, t, 8, c))
 
 
-def _meta_evidence_norm(x, value, gate, weight, mask, eps):
-    return x.new_empty(x.shape, dtype=torch.float32)
+def _meta_evidence_norm(x, value, gate, weight, mask, eps, bf16_out=False):
+    return x.new_empty(x.shape, dtype=torch.bfloat16 if bf16_out else torch.float32)
+
+
+def _meta_block_pre(x, lengths, weight, eps):
+    b, t, d = x.shape
+    return (torch.empty_like(x, memory_format=torch.contiguous_format), x.new_empty((b, t, d), dtype=torch.bfloat16),
+            x.new_empty((b, (t + 3) // 4, d), dtype=torch.bfloat16))
+
+
+def _meta_norm_silu(x, weight, eps):
+    return torch.empty_like(x, memory_format=torch.contiguous_format)
+
+
+def _meta_glu_depthwise(up, weight, bias, lengths):
+    return up.new_empty((*up.shape[:-1], up.shape[-1] // 2), dtype=torch.bfloat16)
+
+
+def _meta_pooled_attention(qkv, cos, sin, low_lengths, heads):
+    return qkv.new_empty((*qkv.shape[:-1], qkv.shape[-1] // 3), dtype=torch.bfloat16)
+
+
+def _meta_merge_gate(cn, mf, mb, an, norm_weight, eps, gate_weight, gate_bias):
+    return cn.new_empty(cn.shape, dtype=torch.float32), cn.new_empty((*cn.shape[:-1], 3), dtype=torch.bfloat16)
+
+
+def _meta_merge_conv(cn, mn, an, g, weight, bias, lengths):
+    return cn.new_empty((*cn.shape[:-1], 3 * cn.shape[-1]), dtype=torch.bfloat16)
 
 
 def _meta_gated_concat(x, gate):
@@ -336,7 +378,8 @@ _KERNELS = {
     **{
         name: (_block(name), globals()["_meta_" + name])
         for name in ("depthwise_masked", "pool4", "rotary_qkv", "front_norm", "interpolate", "bands",
-                     "evidence_norm", "gated_concat", "front_conv1", "front_conv2")
+                     "evidence_norm", "gated_concat", "front_conv1", "front_conv2", "block_pre", "norm_silu",
+                     "glu_depthwise", "pooled_attention", "merge_gate", "merge_conv")
     },
 }
 

@@ -37,15 +37,21 @@ from .kernels.block import (
     Pool4,
     RotaryQKV,
     bands,
+    block_pre,
     depthwise_masked,
     evidence_norm,
     front_norm,
     front_stage,
+    glu_depthwise,
     interpolate,
+    merge_conv,
+    merge_gate,
+    norm_silu,
     pack_conv3x3,
+    pooled_attention,
 )
 from .kernels.buffers import mask_buffer
-from .kernels.native import add, mean_norm
+from .kernels.native import add, add_rms, mean_norm
 from .mamba import Mamba3Inference
 from .masking import time_mask
 
@@ -74,6 +80,10 @@ class TriFusionConfig:
     mamba_parallel_bwd: bool = True
     mamba_fast_launch: bool = True
     paired_mamba_grid_limit: int = 64
+
+
+def _bf16_autocast():
+    return torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16
 
 
 class _MambaShape:
@@ -149,7 +159,7 @@ class CNNStage(nn.Module):
 
     def forward(self, x, lengths):
         lengths = (lengths + self.stride - 1) // self.stride
-        if x.is_cuda and torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16:
+        if x.is_cuda and _bf16_autocast():
             return front_stage(self, x, lengths)
         h = front_norm(self.conv1(x), lengths, self.norm1, silu=True)
         h = front_norm(self.conv2(h), lengths, self.norm2)
@@ -267,7 +277,17 @@ class TriFusionBlock(nn.Module):
             self.merge.weight.mul_(1 / math.sqrt(2 * c.depth))
             self.down.weight.mul_(1 / math.sqrt(2 * c.depth))
 
+    def fusable(self, x):
+        """The fused forward applies: a CUDA fp32 residual stream under bf16
+        autocast, widths the fused kernels take, the reference's kernel sizes."""
+        d = x.shape[-1]
+        return (x.is_cuda and x.dtype == torch.float32 and _bf16_autocast() and d % 8 == 0 and d <= 4096
+                and self.attention.head_dim in (32, 64) and self.merge_dw.kernel_size[0] == 3
+                and self.local.dw.kernel_size[0] in (3, 7))
+
     def forward(self, x, grids):
+        if self.fusable(x):
+            return self.forward_fused(x, grids)
         mask, lengths = grids.mask, grids.lengths
         x = mask_buffer(x, mask)
         h = self.pre(x)
@@ -285,6 +305,27 @@ class TriFusionBlock(nn.Module):
         bf16 = torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16
         r = x + self.merge(add(v, conv, bf16=bf16))
         f = swiglu(self.gate_up(self.ff_norm(r)))
+        return add(r, self.down(f), mask), mf, mb
+
+    def forward_fused(self, x, grids):
+        """``forward`` with the elementwise runs between the GEMMs fused: the same
+        tensors in the same dtypes as the autocast forward, the casts the GEMMs
+        would make done by the producing kernels."""
+        mask, lengths = grids.mask, grids.lengths
+        x, h, p = block_pre(x, lengths, self.pre)
+        local = self.local
+        cn = self.cn(local.out(norm_silu(glu_depthwise(local.up(h), local.dw, lengths), local.norm)))
+        att = self.attention
+        an = self.an(grids.interpolate(att.out(pooled_attention(att.qkv(p), grids, att.heads))))
+        z = F.silu(self.e_down(torch.cat((cn, an), -1)))
+        u = evidence_norm(x, self.e_value(z), self.e_gate(z), self.u_norm.weight, mask, self.u_norm.eps,
+                          bf16_out=True)
+        mf = self.forward_mamba(u, lengths)
+        mb = self.backward_mamba(u, lengths, reverse=True)
+        mn, g = merge_gate(cn, mf, mb, an, self.mn, self.gate)
+        merged = self.merge(merge_conv(cn, mn, an, g, self.merge_dw, lengths))
+        r, f = add_rms(x, merged, self.ff_norm.weight, None, self.ff_norm.eps, torch.bfloat16)
+        f = swiglu(self.gate_up(f))
         return add(r, self.down(f), mask), mf, mb
 
 
