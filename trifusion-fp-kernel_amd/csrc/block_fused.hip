@@ -180,19 +180,39 @@ __global__ __launch_bounds__(256) void norm_silu_kernel(const uint16_t* __restri
   }
 }
 
+// Depthwise taps of 8 consecutive channels ([channel][K] bf16, 16-byte aligned:
+// 8 K elements are K 16-byte vectors) and their biases (one 16-byte vector).
+template <int K>
+__device__ __forceinline__ void load_taps(const uint16_t* w, const uint16_t* bias, float (&wk)[8][K], float (&bb)[8]) {
+  float flat[8 * K];
+#pragma unroll
+  for (int v = 0; v < K; ++v) {
+    float part[8];
+    ld8(w + 8 * v, part);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) flat[8 * v + e] = part[e];
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+#pragma unroll
+    for (int q = 0; q < K; ++q) wk[e][q] = flat[e * K + q];
+  ld8(bias, bb);
+}
+
 // ---- GLU + masked depthwise conv ----------------------------------------------
-// Block (tile, b) takes TT time steps; each thread 8 channels at a time. The GLU
+// One wave per (512 channels, TT time steps, batch row); each lane 8 channels. The GLU
 // rows t0 - K/2 .. t0 + TT - 1 + K/2 (bf16, a * 1 / (1 + e^-b)) are formed once
 // and slid over; sources outside [0, T) are 0, outputs at t >= L are 0.
 template <int K, int TT>
-__global__ __launch_bounds__(128) void glu_depthwise_kernel(const uint16_t* __restrict__ up,
-                                                            const uint16_t* __restrict__ w,
-                                                            const uint16_t* __restrict__ bias,
-                                                            const int64_t* __restrict__ lengths,
-                                                            uint16_t* __restrict__ y, int T, int d) {
-  const int t0 = blockIdx.x * TT, b = blockIdx.y;
+__global__ __launch_bounds__(64) void glu_depthwise_kernel(const uint16_t* __restrict__ up,
+                                                           const uint16_t* __restrict__ w,
+                                                           const uint16_t* __restrict__ bias,
+                                                           const int64_t* __restrict__ lengths,
+                                                           uint16_t* __restrict__ y, int T, int d) {
+  const int t0 = blockIdx.y * TT, b = blockIdx.z;
   const int L = clamp_len(lengths, b, T);
-  for (int c8 = threadIdx.x; c8 < d / 8; c8 += blockDim.x) {
+  const int c8 = blockIdx.x * 64 + threadIdx.x;
+  if (c8 < d / 8) {
     const int c = 8 * c8;
     float win[TT + K - 1][8];
 #pragma unroll
@@ -211,12 +231,7 @@ __global__ __launch_bounds__(128) void glu_depthwise_kernel(const uint16_t* __re
       }
     }
     float wk[8][K], bb[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      bb[e] = bf16_to_f32(bias[c + e]);
-#pragma unroll
-      for (int q = 0; q < K; ++q) wk[e][q] = bf16_to_f32(w[(c + e) * K + q]);
-    }
+    load_taps<K>(w + static_cast<int64_t>(c) * K, bias + c, wk, bb);
 #pragma unroll
     for (int i = 0; i < TT; ++i) {
       const int t = t0 + i;
@@ -239,10 +254,11 @@ __global__ __launch_bounds__(128) void glu_depthwise_kernel(const uint16_t* __re
 }
 
 // ---- rotary + masked attention on the pooled grid -------------------------------
-// One wave per (query tile of 64, head, batch row); lane = query row. Keys and
-// values of 64 positions at a time sit in LDS as fp32 after the rotary (rounded
-// to bf16 like the rotary kernel's output); an online softmax runs over the
-// valid keys j < low_length.
+// One wave per (tile of 16 queries, head, batch row). Each query belongs to four
+// lanes, each holding a quarter of its head dims; together they walk the valid
+// keys j < low_length with one online softmax, G keys at a time (independent
+// dot products). Keys (rotated and rounded to bf16 like the rotary kernel's
+// output) and values of 64 positions at a time sit in LDS as bf16.
 template <int D>
 __device__ __forceinline__ void rotate_row(const uint16_t* src, const float* cs, const float* sn, bool rot,
                                           float (&o)[D]) {
@@ -267,29 +283,46 @@ __device__ __forceinline__ void rotate_row(const uint16_t* src, const float* cs,
   }
 }
 
+constexpr int kAttSplit = 4;                  // lanes per query
+constexpr int kAttQueries = 64 / kAttSplit;   // queries per wave
+constexpr int kAttGroup = 4;                  // keys scored together
+
+// Lane (qi, part) = (lane % 16, lane / 16) holds dims [part D/4, (part+1) D/4) of
+// query qi's rotated q and of its output; a score is the sum of the four lanes'
+// partial dots (two xor shuffles), so all four keep the same softmax state.
 template <int D>
 __global__ __launch_bounds__(64) void attention_kernel(const uint16_t* __restrict__ qkv, const float* __restrict__ cs,
                                                        const float* __restrict__ sn,
                                                        const int64_t* __restrict__ low_lengths,
                                                        uint16_t* __restrict__ y, int LT, int H, float scale) {
-  constexpr int RS = D + 4;  // LDS row stride (floats)
-  __shared__ __align__(16) float ks[64 * RS];
-  __shared__ __align__(16) float vs[64 * RS];
+  constexpr int RS = D + 8;  // LDS row stride (bf16 elements; rows stay 16-byte aligned)
+  constexpr int DP = D / kAttSplit;  // dims per lane
+  // the rotated keys and the values are bf16 numbers, so bf16 storage is exact
+  __shared__ __align__(16) uint16_t ks[64 * RS];
+  __shared__ __align__(16) uint16_t vs[64 * RS];
   const int lane = threadIdx.x;
-  const int t = blockIdx.x * 64 + lane, h = blockIdx.y, b = blockIdx.z;
+  const int qi = lane % kAttQueries, part = lane / kAttQueries;
+  const int t = blockIdx.x * kAttQueries + qi, h = blockIdx.y, b = blockIdx.z;
   const int LL = clamp_len(low_lengths, b, LT);
   const int64_t width = static_cast<int64_t>(3) * H * D;
-  float q[D];
-  if (t < LT) {
-    rotate_row<D>(qkv + (static_cast<int64_t>(b) * LT + t) * width + static_cast<int64_t>(h) * D,
-                  cs + static_cast<int64_t>(t) * (D / 2), sn + static_cast<int64_t>(t) * (D / 2), true, q);
-  } else {
+  float q[DP];
+  {
+    const int tq = t < LT ? t : 0;
+    float full[D];
+    rotate_row<D>(qkv + (static_cast<int64_t>(b) * LT + tq) * width + static_cast<int64_t>(h) * D,
+                  cs + static_cast<int64_t>(tq) * (D / 2), sn + static_cast<int64_t>(tq) * (D / 2), true, full);
 #pragma unroll
-    for (int i = 0; i < D; ++i) q[i] = 0.f;
+    for (int i = 0; i < DP; ++i) {
+      float v = 0.f;
+#pragma unroll
+      for (int pp = 0; pp < kAttSplit; ++pp)
+        if (pp == part) v = full[pp * DP + i];
+      q[i] = v;
+    }
   }
-  float acc[D];
+  float acc[DP];
 #pragma unroll
-  for (int i = 0; i < D; ++i) acc[i] = 0.f;
+  for (int i = 0; i < DP; ++i) acc[i] = 0.f;
   float m = -INFINITY, l = 0.f;
   for (int j0 = 0; j0 < LL; j0 += 64) {
     const int j = j0 + lane;
@@ -299,43 +332,78 @@ __global__ __launch_bounds__(64) void attention_kernel(const uint16_t* __restric
       rotate_row<D>(row + static_cast<int64_t>(H) * D, cs + static_cast<int64_t>(j) * (D / 2),
                     sn + static_cast<int64_t>(j) * (D / 2), true, kr);
 #pragma unroll
-      for (int i = 0; i < D; i += 4)
-        *reinterpret_cast<float4*>(ks + lane * RS + i) = make_float4(kr[i], kr[i + 1], kr[i + 2], kr[i + 3]);
-      rotate_row<D>(row + static_cast<int64_t>(2) * H * D, cs, sn, false, kr);
+      for (int i = 0; i < D; i += 8) {
+        float o[8];
 #pragma unroll
-      for (int i = 0; i < D; i += 4)
-        *reinterpret_cast<float4*>(vs + lane * RS + i) = make_float4(kr[i], kr[i + 1], kr[i + 2], kr[i + 3]);
+        for (int e = 0; e < 8; ++e) o[e] = kr[i + e];
+        st8_bf16(ks + lane * RS + i, o);
+      }
+      const uint16_t* vrow = row + static_cast<int64_t>(2) * H * D;
+#pragma unroll
+      for (int i = 0; i < D; i += 8)
+        *reinterpret_cast<uint4*>(vs + lane * RS + i) = *reinterpret_cast<const uint4*>(vrow + i);
     }
     __syncthreads();
     const int nk = min(64, LL - j0);
-    for (int jj = 0; jj < nk; ++jj) {
-      float s = 0.f;
+    const uint16_t* kp = ks + part * DP;
+    const uint16_t* vp = vs + part * DP;
+    for (int jb = 0; jb < nk; jb += kAttGroup) {
+      float sc[kAttGroup];
 #pragma unroll
-      for (int i = 0; i < D; i += 4) {
-        const float4 kv = *reinterpret_cast<const float4*>(ks + jj * RS + i);
-        s += q[i] * kv.x + q[i + 1] * kv.y + q[i + 2] * kv.z + q[i + 3] * kv.w;
-      }
-      s *= scale;
-      const float mn = fmaxf(m, s);
-      const float corr = expf(m - mn), p = expf(s - mn);
-      l = l * corr + p;
+      for (int g = 0; g < kAttGroup; ++g) {
+        const int jj = jb + g < nk ? jb + g : 0;
+        float part_dot = 0.f;
 #pragma unroll
-      for (int i = 0; i < D; i += 4) {
-        const float4 vv = *reinterpret_cast<const float4*>(vs + jj * RS + i);
-        acc[i] = acc[i] * corr + p * vv.x;
-        acc[i + 1] = acc[i + 1] * corr + p * vv.y;
-        acc[i + 2] = acc[i + 2] * corr + p * vv.z;
-        acc[i + 3] = acc[i + 3] * corr + p * vv.w;
+        for (int i = 0; i < DP; i += 8) {
+          float kv[8];
+          ld8(kp + jj * RS + i, kv);
+#pragma unroll
+          for (int e = 0; e < 8; e += 2) part_dot += q[i + e] * kv[e] + q[i + e + 1] * kv[e + 1];
+        }
+        sc[g] = part_dot;
       }
-      m = mn;
+#pragma unroll
+      for (int g = 0; g < kAttGroup; ++g) {
+        sc[g] += __shfl_xor(sc[g], kAttQueries, 64);
+        sc[g] += __shfl_xor(sc[g], 2 * kAttQueries, 64);
+      }
+      float mx = m;
+#pragma unroll
+      for (int g = 0; g < kAttGroup; ++g) {
+        sc[g] = jb + g < nk ? sc[g] * scale : -INFINITY;
+        mx = fmaxf(mx, sc[g]);
+      }
+      const float corr = expf(m - mx);
+      float pr[kAttGroup];
+      float psum = 0.f;
+#pragma unroll
+      for (int g = 0; g < kAttGroup; ++g) {
+        pr[g] = expf(sc[g] - mx);
+        psum += pr[g];
+      }
+      l = l * corr + psum;
+#pragma unroll
+      for (int i = 0; i < DP; ++i) acc[i] *= corr;
+#pragma unroll
+      for (int g = 0; g < kAttGroup; ++g) {
+        const int jj = jb + g < nk ? jb + g : 0;
+#pragma unroll
+        for (int i = 0; i < DP; i += 8) {
+          float vv[8];
+          ld8(vp + jj * RS + i, vv);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[i + e] += pr[g] * vv[e];
+        }
+      }
+      m = mx;
     }
     __syncthreads();
   }
   if (t < LT) {
     const float inv = l > 0.f ? 1.0f / l : 0.f;
-    uint16_t* dst = y + (static_cast<int64_t>(b) * LT + t) * H * D + static_cast<int64_t>(h) * D;
+    uint16_t* dst = y + (static_cast<int64_t>(b) * LT + t) * H * D + static_cast<int64_t>(h) * D + part * DP;
 #pragma unroll
-    for (int i = 0; i < D; i += 8) {
+    for (int i = 0; i < DP; i += 8) {
       float o[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = acc[i + e] * inv;
@@ -412,15 +480,15 @@ __global__ __launch_bounds__(256) void merge_gate_kernel(const uint16_t* __restr
 }
 
 // ---- gated concatenation -> masked depthwise conv -> residual add ---------------
-// Block (third, tile, b): one third of the 3 d channels (cn, mn or an), TT time
-// steps. v = s * (2 sigmoid(g)) in fp32, the conv reads bf16(v); the output is
+// One wave per (512 channels of one third of the 3 d channels -- cn, mn or an --,
+// TT time steps, batch row); each lane 8 channels. v = s * (2 sigmoid(g)) in fp32, the conv reads bf16(v); the output is
 // bf16(v + bf16(conv)) with conv = 0 at t >= L.
 template <int K, int TT, typename TS>
 __device__ __forceinline__ void merge_conv_third(const TS* __restrict__ src, const uint16_t* __restrict__ g,
                                                  const uint16_t* __restrict__ w, const uint16_t* __restrict__ bias,
-                                                 uint16_t* __restrict__ y, int third, int t0, int b, int T, int L,
-                                                 int d) {
-  for (int c8 = threadIdx.x; c8 < d / 8; c8 += blockDim.x) {
+                                                 uint16_t* __restrict__ y, int third, int c8, int t0, int b, int T,
+                                                 int L, int d) {
+  if (c8 < d / 8) {
     const int c = 8 * c8, gc = third * d + c;
     float vb[TT + K - 1][8], vc[TT][8];
 #pragma unroll
@@ -446,12 +514,7 @@ __device__ __forceinline__ void merge_conv_third(const TS* __restrict__ src, con
       }
     }
     float wk[8][K], bb[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      bb[e] = bf16_to_f32(bias[gc + e]);
-#pragma unroll
-      for (int q = 0; q < K; ++q) wk[e][q] = bf16_to_f32(w[static_cast<int64_t>(gc + e) * K + q]);
-    }
+    load_taps<K>(w + static_cast<int64_t>(gc) * K, bias + gc, wk, bb);
 #pragma unroll
     for (int i = 0; i < TT; ++i) {
       const int t = t0 + i;
@@ -474,19 +537,20 @@ __device__ __forceinline__ void merge_conv_third(const TS* __restrict__ src, con
 }
 
 template <int K, int TT>
-__global__ __launch_bounds__(128) void merge_conv_kernel(const uint16_t* __restrict__ cn, const float* __restrict__ mn,
-                                                         const uint16_t* __restrict__ an,
-                                                         const uint16_t* __restrict__ g,
-                                                         const uint16_t* __restrict__ w,
-                                                         const uint16_t* __restrict__ bias,
-                                                         const int64_t* __restrict__ lengths, uint16_t* __restrict__ y,
-                                                         int T, int d) {
-  const int third = blockIdx.x, t0 = blockIdx.y * TT, b = blockIdx.z;
+__global__ __launch_bounds__(64) void merge_conv_kernel(const uint16_t* __restrict__ cn, const float* __restrict__ mn,
+                                                        const uint16_t* __restrict__ an,
+                                                        const uint16_t* __restrict__ g,
+                                                        const uint16_t* __restrict__ w,
+                                                        const uint16_t* __restrict__ bias,
+                                                        const int64_t* __restrict__ lengths, uint16_t* __restrict__ y,
+                                                        int T, int d, int chunks) {
+  const int third = blockIdx.x / chunks, c8 = (blockIdx.x % chunks) * 64 + threadIdx.x;
+  const int t0 = blockIdx.y * TT, b = blockIdx.z;
   const int L = clamp_len(lengths, b, T);
   if (third == 1) {
-    merge_conv_third<K, TT, float>(mn, g, w, bias, y, third, t0, b, T, L, d);
+    merge_conv_third<K, TT, float>(mn, g, w, bias, y, third, c8, t0, b, T, L, d);
   } else {
-    merge_conv_third<K, TT, uint16_t>(third == 0 ? cn : an, g, w, bias, y, third, t0, b, T, L, d);
+    merge_conv_third<K, TT, uint16_t>(third == 0 ? cn : an, g, w, bias, y, third, c8, t0, b, T, L, d);
   }
 }
 
@@ -498,7 +562,7 @@ int per8_of(int64_t d) {
   return per8;
 }
 
-constexpr int kTT = 8;
+constexpr int kTT = 4;  // time steps per depthwise tile
 
 }  // namespace
 }  // namespace tf
@@ -553,14 +617,17 @@ extern "C" int tf_norm_silu(const void* x, const float* w, void* y, int64_t rows
 extern "C" int tf_glu_depthwise(const void* up, const void* w, const void* bias, const int64_t* lengths, void* y,
                                 int64_t batch, int64_t time, int64_t d, int64_t k, void* stream) {
   if (!up || !w || !bias || !lengths || !y) return TF_ERR_NULL;
-  if (batch < 0 || time < 0 || d < 8 || d % 8 || batch > 65535 || batch * time > 0x7fffffff) return TF_ERR_SHAPE;
-  if (!tf::a16(up) || !tf::a16(y)) return TF_ERR_SHAPE;
+  if (batch < 0 || time < 0 || d < 8 || d % 8 || batch > 65535 || batch * time > 0x7fffffff ||
+      (time + tf::kTT - 1) / tf::kTT > 65535)
+    return TF_ERR_SHAPE;
+  if (!tf::a16(up) || !tf::a16(y) || !tf::a16(w) || !tf::a16(bias)) return TF_ERR_SHAPE;
   if (batch * time == 0) return TF_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid(static_cast<uint32_t>((time + tf::kTT - 1) / tf::kTT), static_cast<uint32_t>(batch));
+  const dim3 grid(static_cast<uint32_t>((d / 8 + 63) / 64), static_cast<uint32_t>((time + tf::kTT - 1) / tf::kTT),
+                  static_cast<uint32_t>(batch));
 #define TF_GLU(KV)                                                                                               \
   if (k == KV) {                                                                                                  \
-    hipLaunchKernelGGL((tf::glu_depthwise_kernel<KV, tf::kTT>), grid, dim3(128), 0, s,                           \
+    hipLaunchKernelGGL((tf::glu_depthwise_kernel<KV, tf::kTT>), grid, dim3(64), 0, s,                            \
                        static_cast<const uint16_t*>(up), static_cast<const uint16_t*>(w),                        \
                        static_cast<const uint16_t*>(bias), lengths, static_cast<uint16_t*>(y),                   \
                        static_cast<int>(time), static_cast<int>(d));                                             \
@@ -580,8 +647,8 @@ extern "C" int tf_pooled_attention(const void* qkv, const float* cos_t, const fl
   if (!tf::a16(qkv) || !tf::a16(y)) return TF_ERR_SHAPE;
   if (batch * low_time == 0) return TF_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid(static_cast<uint32_t>((low_time + 63) / 64), static_cast<uint32_t>(heads),
-                  static_cast<uint32_t>(batch));
+  const dim3 grid(static_cast<uint32_t>((low_time + tf::kAttQueries - 1) / tf::kAttQueries),
+                  static_cast<uint32_t>(heads), static_cast<uint32_t>(batch));
   const float scale = 1.0f / sqrtf(static_cast<float>(head_dim));
 #define TF_ATT(DV)                                                                                                \
   if (head_dim == DV) {                                                                                            \
@@ -625,19 +692,23 @@ extern "C" int tf_merge_conv(const void* cn, const float* mn, const void* an, co
                              const void* bias, const int64_t* lengths, void* y, int64_t batch, int64_t time,
                              int64_t d, int64_t k, void* stream) {
   if (!cn || !mn || !an || !g || !w || !bias || !lengths || !y) return TF_ERR_NULL;
-  if (batch < 0 || time < 0 || d < 8 || d % 8 || batch > 65535 || batch * time > 0x7fffffff) return TF_ERR_SHAPE;
-  for (const void* p : {cn, static_cast<const void*>(mn), an, static_cast<const void*>(y)})
+  if (batch < 0 || time < 0 || d < 8 || d % 8 || batch > 65535 || batch * time > 0x7fffffff ||
+      (time + tf::kTT - 1) / tf::kTT > 65535)
+    return TF_ERR_SHAPE;
+  for (const void* p : {cn, static_cast<const void*>(mn), an, static_cast<const void*>(y), w, bias})
     if (!tf::a16(p)) return TF_ERR_SHAPE;
   if (batch * time == 0) return TF_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid(3, static_cast<uint32_t>((time + tf::kTT - 1) / tf::kTT), static_cast<uint32_t>(batch));
+  const int chunks = static_cast<int>((d / 8 + 63) / 64);
+  const dim3 grid(static_cast<uint32_t>(3 * chunks), static_cast<uint32_t>((time + tf::kTT - 1) / tf::kTT),
+                  static_cast<uint32_t>(batch));
 #define TF_MC(KV)                                                                                                 \
   if (k == KV) {                                                                                                   \
-    hipLaunchKernelGGL((tf::merge_conv_kernel<KV, tf::kTT>), grid, dim3(128), 0, s,                               \
+    hipLaunchKernelGGL((tf::merge_conv_kernel<KV, tf::kTT>), grid, dim3(64), 0, s,                                \
                        static_cast<const uint16_t*>(cn), mn, static_cast<const uint16_t*>(an),                    \
                        static_cast<const uint16_t*>(g), static_cast<const uint16_t*>(w),                          \
                        static_cast<const uint16_t*>(bias), lengths, static_cast<uint16_t*>(y),                    \
-                       static_cast<int>(time), static_cast<int>(d));                                              \
+                       static_cast<int>(time), static_cast<int>(d), chunks);                                      \
     return tf::launch_status();                                                                                   \
   }
   TF_MC(3)

@@ -212,6 +212,83 @@ __global__ __launch_bounds__(256) void evidence_norm_kernel(const float* __restr
   for (int c = lane; c < D; c += 64) y[row * D + c] = from_f32<TY>(value(c) * r * w[c]);
 }
 
+// evidence_norm_kernel through 8-element vectors: one wave per row, lane holds
+// elements 8 (lane + 64 i) .. +7, i < PER8.
+template <typename T>
+__device__ __forceinline__ void load8v(const T* p, float (&v)[8]) {
+  if constexpr (sizeof(T) == 4) {
+    const float4 a = reinterpret_cast<const float4*>(p)[0];
+    const float4 b = reinterpret_cast<const float4*>(p)[1];
+    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+  } else {
+    const uint4 u = *reinterpret_cast<const uint4*>(p);
+    const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[2 * e] = to_f32(__builtin_bit_cast(T, static_cast<uint16_t>(wd[e] & 0xffffu)));
+      v[2 * e + 1] = to_f32(__builtin_bit_cast(T, static_cast<uint16_t>(wd[e] >> 16)));
+    }
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void store8v(T* p, const float (&v)[8]) {
+  if constexpr (sizeof(T) == 4) {
+    reinterpret_cast<float4*>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
+    reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
+  } else {
+    uint32_t wd[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      wd[e] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, from_f32<T>(v[2 * e]))) |
+              (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, from_f32<T>(v[2 * e + 1]))) << 16);
+    *reinterpret_cast<uint4*>(p) = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+  }
+}
+
+template <typename TA, typename TY, int PER8>
+__global__ __launch_bounds__(256) void evidence_norm_vec_kernel(const float* __restrict__ x,
+                                                                const TA* __restrict__ a, const TA* __restrict__ g,
+                                                                const uint8_t* __restrict__ mask,
+                                                                const float* __restrict__ w, TY* __restrict__ y,
+                                                                int64_t rows, int D, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const bool valid = mask == nullptr || mask[row] != 0;
+  float v[PER8][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < PER8; ++i) {
+    const int i0 = 8 * (lane + 64 * i);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[i][e] = 0.f;
+    if (i0 < D && valid) {
+      float xv[8], av[8], gv[8];
+      load8v(x + row * D + i0, xv);
+      load8v(a + row * D + i0, av);
+      load8v(g + row * D + i0, gv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[i][e] = xv[e] + av[e] * (2.f * sigmoid_acc(gv[e]));
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += v[i][e] * v[i][e];
+  }
+  ss = wave_sum(ss);
+  const float r = rsqrtf(ss / static_cast<float>(D) + eps);
+#pragma unroll
+  for (int i = 0; i < PER8; ++i) {
+    const int i0 = 8 * (lane + 64 * i);
+    if (i0 < D) {
+      float wv[8], o[8];
+      load8v(w + i0, wv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = v[i][e] * r * wv[e];
+      store8v(y + row * D + i0, o);
+    }
+  }
+}
+
 // y[row, k d + j] = x[row, k d + j] * 2 sigmoid(gate[row, k]), k < 3
 // (primitives.py:_gate forward through gated_concat).
 template <typename T>
@@ -223,6 +300,8 @@ __global__ __launch_bounds__(256) void gated_concat_kernel(const T* __restrict__
   const float s = sigmoid_acc(to_f32(gate[gi]));
   y[i] = from_f32<T>(to_f32(x[i]) * (2.f * s));
 }
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 uint32_t nblocks(int64_t n, int per) { return static_cast<uint32_t>((n + per - 1) / per); }
 
@@ -336,6 +415,25 @@ extern "C" int tf_evidence_norm(const float* x, const void* a, const void* g, in
   if (rows == 0) return TF_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid(tf::nblocks(rows, tf::kWaves));
+  const bool vec = d % 8 == 0 && d <= 2048 && tf::aligned16(x) && tf::aligned16(a) && tf::aligned16(g) &&
+                   tf::aligned16(w) && tf::aligned16(y);
+  if (vec) {
+    const int per8 = d <= 512 ? 1 : (d <= 1024 ? 2 : 4);
+#define TF_EVN(TAV, TYV, P)                                                                                   \
+  hipLaunchKernelGGL((tf::evidence_norm_vec_kernel<TAV, TYV, P>), grid, dim3(256), 0, s, x,                   \
+                     static_cast<const TAV*>(a), static_cast<const TAV*>(g), mask, w, static_cast<TYV*>(y),   \
+                     rows, static_cast<int>(d), eps)
+#define TF_EVN_P(TAV, TYV)          \
+  if (per8 == 1) TF_EVN(TAV, TYV, 1); \
+  else if (per8 == 2) TF_EVN(TAV, TYV, 2); \
+  else TF_EVN(TAV, TYV, 4);
+    TF_DISPATCH(ag_dtype, TA,
+                if (y_dtype == TF_FLOAT32) { TF_EVN_P(TA, float) } else { TF_EVN_P(TA, tf::bf16_t) } return
+                tf::launch_status());
+#undef TF_EVN_P
+#undef TF_EVN
+    return TF_ERR_DTYPE;
+  }
   TF_DISPATCH(ag_dtype, TA,
               if (y_dtype == TF_FLOAT32) {
                 hipLaunchKernelGGL((tf::evidence_norm_kernel<TA, float>), grid, dim3(256), 0, s, x,

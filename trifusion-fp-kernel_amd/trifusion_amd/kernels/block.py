@@ -377,8 +377,8 @@ def launch_glu_depthwise(up, weight, bias, lengths):
     d, k = d2 // 2, weight.shape[-1]
     if weight.numel() != d * k or bias.shape != (d,):
         raise ValueError("glu_depthwise: weight must be [d, 1, k] and bias [d]")
-    w = weight.to(torch.bfloat16).contiguous()
-    bb = bias.to(torch.bfloat16).contiguous()
+    w = _aligned16(weight.to(torch.bfloat16))
+    bb = _aligned16(bias.to(torch.bfloat16))
     y = torch.empty((b, t, d), device=up.device, dtype=torch.bfloat16)
     status = lib.tf_glu_depthwise(uc.data_ptr(), w.data_ptr(), bb.data_ptr(), _lengths(lengths).data_ptr(),
                                   y.data_ptr(), b, t, d, k, _lib.stream_of(up))
@@ -452,8 +452,8 @@ def launch_merge_conv(cn, mn, an, g, weight, bias, lengths):
         raise ValueError("merge_conv: cn, mn, an must be [B, T, d] and g [B, T, 3]")
     if weight.numel() != 3 * d * k or bias.shape != (3 * d,):
         raise ValueError("merge_conv: weight must be [3 d, 1, k] and bias [3 d]")
-    w = weight.to(torch.bfloat16).contiguous()
-    bb = bias.to(torch.bfloat16).contiguous()
+    w = _aligned16(weight.to(torch.bfloat16))
+    bb = _aligned16(bias.to(torch.bfloat16))
     y = torch.empty((b, t, 3 * d), device=cn.device, dtype=torch.bfloat16)
     status = lib.tf_merge_conv(cc.data_ptr(), mc.data_ptr(), ac.data_ptr(), gc.data_ptr(), w.data_ptr(),
                                bb.data_ptr(), _lengths(lengths).data_ptr(), y.data_ptr(), b, t, d, k,
