@@ -63,6 +63,8 @@ REVERSE_CASES = {
     "b2_l90_h4_wide_rotary": (2, 90, 4, 64, 64, 24, 1, (90, 3)),
     "b2_l90_no_lengths": (2, 90, 4, 64, 64, 16, 1, None),
     "b16_l400_h16_varlen": (16, 400, 16, 64, 64, 16, 1, "random"),
+    # the TriFusion block's shape: 512 units, more than one workgroup round
+    "b16_l101_h32_p64_n128_varlen": (16, 101, 32, 64, 128, 32, 1, "random"),
 }
 
 
@@ -163,6 +165,7 @@ RAW_CASES = {
     "b3_l150_h4_p32_n32_ragged": (3, 150, 4, 32, 32, 8, 1, (150, 90, 5)),
     "b2_l130_h2_p64_n128": (2, 130, 2, 64, 128, 32, 1, None),
     "b2_l100_h4_p32_n16": (2, 100, 4, 32, 16, 4, 1, None),
+    "b16_l101_h32_p64_n128": (16, 101, 32, 64, 128, 32, 1, None),
 }
 
 

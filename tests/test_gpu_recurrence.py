@@ -82,6 +82,7 @@ CLIP_CASES = {
     "long_b1_l7200_h16_p64_n64": (1, 7200, 16, 64, 64, 16, 1, torch.bfloat16),
     "hq_equals_h": (2, 200, 8, 64, 64, 16, 8, torch.bfloat16),
     "n128_p64": (2, 150, 4, 64, 128, 32, 1, torch.bfloat16),
+    "model_b16_l101_h32_p64_n128": (16, 101, 32, 64, 128, 32, 1, torch.bfloat16),
     "n32_p32": (3, 130, 4, 32, 32, 8, 2, torch.bfloat16),
     "n16_p32_bf16": (2, 100, 4, 32, 16, 4, 1, torch.bfloat16),
 }
