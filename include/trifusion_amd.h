@@ -337,12 +337,14 @@ int tf_bands(const void *x, int32_t dtype, const int64_t *strides, void *y, int6
 /*
  * Evidence-gated RMSNorm: s = mask[r] ? x + a * 2 sigmoid(g) : 0 (fp32),
  * y = s rsqrt(mean(s^2) + eps) w, computed in fp32 and stored as y_dtype (fp32, or
- * bf16 for a consumer that casts it); x fp32, a and g of ag_dtype, all contiguous
- * [rows, d]; mask uint8 [rows] or NULL. Replaces evidence_norm (`_norm` MODE 1,
- * src/trifusion_l4/kernels/native.py:9-39,73-74).
+ * bf16 for a consumer that casts it); x and y contiguous [rows, d] (x fp32); a and g
+ * of ag_dtype, rows of d elements ag_stride apart (both halves of one [rows, 2d]
+ * projection, or contiguous with ag_stride = d); mask uint8 [rows] or NULL.
+ * Replaces evidence_norm (`_norm` MODE 1, src/trifusion_l4/kernels/native.py:9-39,73-74).
  */
-int tf_evidence_norm(const float *x, const void *a, const void *g, int32_t ag_dtype, const uint8_t *mask,
-                     const float *w, void *y, int32_t y_dtype, int64_t rows, int64_t d, float eps, void *stream);
+int tf_evidence_norm(const float *x, const void *a, const void *g, int32_t ag_dtype, int64_t ag_stride,
+                     const uint8_t *mask, const float *w, void *y, int32_t y_dtype, int64_t rows, int64_t d,
+                     float eps, void *stream);
 
 /*
  * Sigmoid-gated concatenation: y[r, k d + j] = x[r, k d + j] * 2 sigmoid(gate[r, k])

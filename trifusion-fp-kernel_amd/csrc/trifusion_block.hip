@@ -190,7 +190,7 @@ __global__ __launch_bounds__(256) void bands_kernel(const T* __restrict__ x, T* 
 // the second pass recomputes s from the (now cached) row.
 template <typename TA, typename TY>
 __global__ __launch_bounds__(256) void evidence_norm_kernel(const float* __restrict__ x, const TA* __restrict__ a,
-                                                            const TA* __restrict__ g,
+                                                            const TA* __restrict__ g, int64_t ag_stride,
                                                             const uint8_t* __restrict__ mask,
                                                             const float* __restrict__ w, TY* __restrict__ y,
                                                             int64_t rows, int D, float eps) {
@@ -199,8 +199,8 @@ __global__ __launch_bounds__(256) void evidence_norm_kernel(const float* __restr
   if (row >= rows) return;
   const bool valid = mask == nullptr || mask[row] != 0;
   auto value = [&](int c) {
-    const int64_t o = row * D + c;
-    return valid ? x[o] + to_f32(a[o]) * (2.f * sigmoid_acc(to_f32(g[o]))) : 0.f;
+    const int64_t o = row * D + c, oa = row * ag_stride + c;
+    return valid ? x[o] + to_f32(a[oa]) * (2.f * sigmoid_acc(to_f32(g[oa]))) : 0.f;
   };
   float ss = 0.f;
   for (int c = lane; c < D; c += 64) {
@@ -249,7 +249,7 @@ __device__ __forceinline__ void store8v(T* p, const float (&v)[8]) {
 template <typename TA, typename TY, int PER8>
 __global__ __launch_bounds__(256) void evidence_norm_vec_kernel(const float* __restrict__ x,
                                                                 const TA* __restrict__ a, const TA* __restrict__ g,
-                                                                const uint8_t* __restrict__ mask,
+                                                                int64_t ag_stride, const uint8_t* __restrict__ mask,
                                                                 const float* __restrict__ w, TY* __restrict__ y,
                                                                 int64_t rows, int D, float eps) {
   const int lane = threadIdx.x & 63;
@@ -266,8 +266,8 @@ __global__ __launch_bounds__(256) void evidence_norm_vec_kernel(const float* __r
     if (i0 < D && valid) {
       float xv[8], av[8], gv[8];
       load8v(x + row * D + i0, xv);
-      load8v(a + row * D + i0, av);
-      load8v(g + row * D + i0, gv);
+      load8v(a + row * ag_stride + i0, av);
+      load8v(g + row * ag_stride + i0, gv);
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[i][e] = xv[e] + av[e] * (2.f * sigmoid_acc(gv[e]));
     }
@@ -406,22 +406,23 @@ extern "C" int tf_bands(const void* x, int32_t dtype, const int64_t* strides, vo
   return TF_ERR_DTYPE;
 }
 
-extern "C" int tf_evidence_norm(const float* x, const void* a, const void* g, int32_t ag_dtype, const uint8_t* mask,
-                                const float* w, void* y, int32_t y_dtype, int64_t rows, int64_t d, float eps,
-                                void* stream) {
+extern "C" int tf_evidence_norm(const float* x, const void* a, const void* g, int32_t ag_dtype, int64_t ag_stride,
+                                const uint8_t* mask, const float* w, void* y, int32_t y_dtype, int64_t rows, int64_t d,
+                                float eps, void* stream) {
   if (!x || !a || !g || !w || !y) return TF_ERR_NULL;
-  if (rows < 0 || d < 1) return TF_ERR_SHAPE;
+  if (rows < 0 || d < 1 || ag_stride < d) return TF_ERR_SHAPE;
   if (y_dtype != TF_FLOAT32 && y_dtype != TF_BFLOAT16) return TF_ERR_DTYPE;
   if (rows == 0) return TF_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid(tf::nblocks(rows, tf::kWaves));
-  const bool vec = d % 8 == 0 && d <= 2048 && tf::aligned16(x) && tf::aligned16(a) && tf::aligned16(g) &&
-                   tf::aligned16(w) && tf::aligned16(y);
+  const bool vec = d % 8 == 0 && ag_stride % 8 == 0 && d <= 2048 && tf::aligned16(x) && tf::aligned16(a) &&
+                   tf::aligned16(g) && tf::aligned16(w) && tf::aligned16(y);
   if (vec) {
     const int per8 = d <= 512 ? 1 : (d <= 1024 ? 2 : 4);
 #define TF_EVN(TAV, TYV, P)                                                                                   \
   hipLaunchKernelGGL((tf::evidence_norm_vec_kernel<TAV, TYV, P>), grid, dim3(256), 0, s, x,                   \
-                     static_cast<const TAV*>(a), static_cast<const TAV*>(g), mask, w, static_cast<TYV*>(y),   \
+                     static_cast<const TAV*>(a), static_cast<const TAV*>(g), ag_stride, mask, w,              \
+                     static_cast<TYV*>(y),                                                                      \
                      rows, static_cast<int>(d), eps)
 #define TF_EVN_P(TAV, TYV)          \
   if (per8 == 1) TF_EVN(TAV, TYV, 1); \
@@ -437,11 +438,11 @@ extern "C" int tf_evidence_norm(const float* x, const void* a, const void* g, in
   TF_DISPATCH(ag_dtype, TA,
               if (y_dtype == TF_FLOAT32) {
                 hipLaunchKernelGGL((tf::evidence_norm_kernel<TA, float>), grid, dim3(256), 0, s, x,
-                                   static_cast<const TA*>(a), static_cast<const TA*>(g), mask, w,
+                                   static_cast<const TA*>(a), static_cast<const TA*>(g), ag_stride, mask, w,
                                    static_cast<float*>(y), rows, static_cast<int>(d), eps);
               } else {
                 hipLaunchKernelGGL((tf::evidence_norm_kernel<TA, tf::bf16_t>), grid, dim3(256), 0, s, x,
-                                   static_cast<const TA*>(a), static_cast<const TA*>(g), mask, w,
+                                   static_cast<const TA*>(a), static_cast<const TA*>(g), ag_stride, mask, w,
                                    static_cast<tf::bf16_t*>(y), rows, static_cast<int>(d), eps);
               } return tf::launch_status());
   return TF_ERR_DTYPE;

@@ -106,7 +106,10 @@ _SIGNATURES = {
     ),
     "tf_interpolate": ([c_ptr, c_i32, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_ptr], c_i32),
     "tf_bands": ([c_ptr, c_i32, ctypes.POINTER(c_i64), c_ptr, c_i64, c_i64, c_i64, c_i64, c_ptr], c_i32),
-    "tf_evidence_norm": ([c_ptr, c_ptr, c_ptr, c_i32, c_ptr, c_ptr, c_ptr, c_i32, c_i64, c_i64, c_f32, c_ptr], c_i32),
+    "tf_evidence_norm": (
+        [c_ptr, c_ptr, c_ptr, c_i32, c_i64, c_ptr, c_ptr, c_ptr, c_i32, c_i64, c_i64, c_f32, c_ptr],
+        c_i32,
+    ),
     "tf_gated_concat": ([c_ptr, c_ptr, c_i32, c_ptr, c_i64, c_i64, c_ptr], c_i32),
     "tf_front_conv1": (
         [c_ptr, c_i32, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_f32, c_ptr],

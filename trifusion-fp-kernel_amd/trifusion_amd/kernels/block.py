@@ -36,6 +36,20 @@ def _strides(x):
     return (ctypes.c_int64 * 4)(*x.stride())
 
 
+def _row_stride(t):
+    """Common stride of the rows of ``t`` (last dim contiguous, leading dims
+    collapsible to one row index), or None."""
+    if t.dim() == 0 or t.stride(-1) != 1 and t.shape[-1] > 1:
+        return None
+    stride = t.stride(-2) if t.dim() > 1 else t.shape[-1]
+    expect = stride
+    for i in range(t.dim() - 2, -1, -1):
+        if t.shape[i] > 1 and t.stride(i) != expect:
+            return None
+        expect *= t.shape[i]
+    return stride
+
+
 def depthwise_masked(x, layer, lengths):
     """Masked depthwise Conv1d over time (``layer``: ``Conv1d(D, D, K,
     padding=K//2, groups=D)``) on ``[B, T, D]``; rows past each length are 0.
@@ -271,12 +285,15 @@ def launch_evidence_norm(x, value, gate, weight, mask, eps=1e-5, bf16_out=False)
     x = x.float().contiguous()
     if value.dtype != gate.dtype:
         gate = gate.to(value.dtype)
-    value = value.contiguous()
-    gate = gate.contiguous()
     d = x.shape[-1]
     rows = x.numel() // d
-    if value.numel() != x.numel() or gate.numel() != x.numel():
+    if value.shape != x.shape or gate.shape != x.shape:
         raise ValueError("evidence_norm: value and gate must match x")
+    # value and gate may be column halves of one projection: rows a common stride apart
+    stride = _row_stride(value)
+    if stride is None or _row_stride(gate) != stride:
+        value, gate = value.contiguous(), gate.contiguous()
+        stride = d
     m = None
     if mask is not None:
         if mask.dtype != torch.bool or mask.numel() != rows:
@@ -284,7 +301,8 @@ def launch_evidence_norm(x, value, gate, weight, mask, eps=1e-5, bf16_out=False)
         m = mask.contiguous().data_ptr()
     y = torch.empty(x.shape, device=x.device, dtype=torch.bfloat16 if bf16_out else torch.float32)
     status = lib.tf_evidence_norm(x.data_ptr(), value.data_ptr(), gate.data_ptr(),
-                                  _lib.dtype_code(value, "evidence_norm"), m, weight.float().contiguous().data_ptr(),
+                                  _lib.dtype_code(value, "evidence_norm"), stride, m,
+                                  weight.float().contiguous().data_ptr(),
                                   y.data_ptr(), _lib.dtype_code(y, "evidence_norm"), rows, d, float(eps),
                                   _lib.stream_of(x))
     _lib.check(status, "evidence_norm")

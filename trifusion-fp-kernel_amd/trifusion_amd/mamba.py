@@ -96,9 +96,17 @@ class Mamba3Inference(nn.Module):
         )
 
     def forward(self, u, lengths=None, reverse=False):
-        b, t, _ = u.shape
-        width = self.in_proj.out_features
-        p = F.linear(u, self._padded_in_proj())[..., :width]
+        return self.out_proj(self.mix(self.project(u), lengths, reverse))
+
+    def project(self, u):
+        """The in-projection ``[B, T, width]`` (a view of the padded GEMM output)."""
+        return F.linear(u, self._padded_in_proj())[..., : self.in_proj.out_features]
+
+    def mix(self, p, lengths=None, reverse=False, out=None):
+        """Norms, controls and the fused recurrence from the projection ``p``:
+        ``[B, T, d_inner]`` before the out-projection (written into ``out``, a
+        ``[B, T, H, P]`` buffer, when given)."""
+        b, t, _ = p.shape
         z, v, k, q, ddt, a, trap, angles = self.split(p)
         if self.B_norm.eps == self.C_norm.eps:
             # B and C sit side by side in the projection: both norms, one launch
@@ -131,6 +139,7 @@ class Mamba3Inference(nn.Module):
             lengths=lengths,
             variant=self.variant,
             reverse=reverse,
+            out=out,
             **raw,
         )
-        return self.out_proj(y.reshape(b, t, self.d_inner))
+        return y.reshape(b, t, self.d_inner)

@@ -267,6 +267,7 @@ class TriFusionBlock(nn.Module):
         self.ff_norm = RMSNorm(d)
         self.gate_up = nn.Linear(d, 2 * c.ffn_dim, bias=False)
         self.down = nn.Linear(c.ffn_dim, d, bias=False)
+        self._fused_weights = {}
         nn.init.zeros_(self.e_gate.weight)
         nn.init.zeros_(self.e_gate.bias)
         nn.init.normal_(self.e_value.weight, std=1e-3)
@@ -307,21 +308,49 @@ class TriFusionBlock(nn.Module):
         f = swiglu(self.gate_up(self.ff_norm(r)))
         return add(r, self.down(f), mask), mf, mb
 
+    def _joined(self, name, parts, build):
+        """Weights of two layers that read the same input, joined for one GEMM;
+        rebuilt when any part changes."""
+        # inference tensors (caches built under inference mode) have no version
+        # counter; they are rebuilt, at a new address, when their source changes
+        key = tuple((t.data_ptr(), -1 if t.is_inference() else t._version, t.dtype, t.device) for t in parts)
+        hit = self._fused_weights.get(name)
+        if hit is None or hit[0] != key:
+            with torch.no_grad():
+                hit = (key, build())
+            self._fused_weights[name] = hit
+        return hit[1]
+
     def forward_fused(self, x, grids):
         """``forward`` with the elementwise runs between the GEMMs fused: the same
         tensors in the same dtypes as the autocast forward, the casts the GEMMs
-        would make done by the producing kernels."""
+        would make done by the producing kernels. Layers that read one input run
+        as one GEMM: e_value with e_gate, and the in-projections of the two
+        Mamba directions; the two out-projections run as one batched GEMM."""
         mask, lengths = grids.mask, grids.lengths
+        b, t, d = x.shape
         x, h, p = block_pre(x, lengths, self.pre)
         local = self.local
         cn = self.cn(local.out(norm_silu(glu_depthwise(local.up(h), local.dw, lengths), local.norm)))
         att = self.attention
         an = self.an(grids.interpolate(att.out(pooled_attention(att.qkv(p), grids, att.heads))))
         z = F.silu(self.e_down(torch.cat((cn, an), -1)))
-        u = evidence_norm(x, self.e_value(z), self.e_gate(z), self.u_norm.weight, mask, self.u_norm.eps,
-                          bf16_out=True)
-        mf = self.forward_mamba(u, lengths)
-        mb = self.backward_mamba(u, lengths, reverse=True)
+        ev, eg = self.e_value, self.e_gate
+        wv = self._joined("evidence", (ev.weight, ev.bias, eg.weight, eg.bias),
+                          lambda: (torch.cat((ev.weight, eg.weight)), torch.cat((ev.bias, eg.bias))))
+        ve = F.linear(z, *wv)
+        u = evidence_norm(x, ve[..., :d], ve[..., d:], self.u_norm.weight, mask, self.u_norm.eps, bf16_out=True)
+        fw, bw = self.forward_mamba, self.backward_mamba
+        pf, pb = fw._padded_in_proj(), bw._padded_in_proj()
+        proj = F.linear(u, self._joined("in_proj", (pf, pb), lambda: torch.cat((pf, pb))))
+        width, half = fw.in_proj.out_features, pf.shape[0]
+        ys = torch.empty((2, b, t, fw.nheads, fw.headdim), device=x.device, dtype=torch.bfloat16)
+        fw.mix(proj[..., :width], lengths, out=ys[0])
+        bw.mix(proj[..., half : half + width], lengths, reverse=True, out=ys[1])
+        wo = (fw.out_proj.weight, bw.out_proj.weight)
+        wo = self._joined("out_proj", wo, lambda: torch.stack((wo[0].t(), wo[1].t())).contiguous())
+        m = torch.bmm(ys.view(2, b * t, fw.d_inner), wo)
+        mf, mb = m[0].view(b, t, d), m[1].view(b, t, d)
         mn, g = merge_gate(cn, mf, mb, an, self.mn, self.gate)
         merged = self.merge(merge_conv(cn, mn, an, g, self.merge_dw, lengths))
         r, f = add_rms(x, merged, self.ff_norm.weight, None, self.ff_norm.eps, torch.bfloat16)
