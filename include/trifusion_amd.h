@@ -441,6 +441,22 @@ int tf_merge_conv(const void *cn, const float *mn, const void *an, const void *g
                   const int64_t *lengths, void *y, int64_t batch, int64_t time, int64_t d, int64_t k,
                   void *stream);
 
+/*
+ * Query read of the decoder: y[b, i, h D + d] = softmax_j(q_i,h . k_j,h / sqrt(D)) v_j,h
+ * in fp32 over keys j < key_lengths[b], rounded to bf16; q bf16 [queries, heads, D]
+ * (the same for every batch row), kv bf16 [B, T, 2, heads, D] (keys, then values; 16-byte
+ * aligned), y bf16 [B, queries, heads D]. queries = 10 and D = 32 (the decoder's shape).
+ * A query row with no valid key is 0. workspace: caller-allocated fp32 scratch of at least
+ * tf_query_read_workspace_size(...) bytes (per 64-key tile partial softmax records).
+ * Replaces QueryRead's masked_attention call (src/trifusion_l4/decoder.py:24-32,
+ * attention.py:8-18).
+ */
+int64_t tf_query_read_workspace_size(int64_t batch, int64_t time, int64_t heads, int64_t queries,
+                                     int64_t head_dim);
+int tf_query_read(const void *q, const void *kv, const int64_t *key_lengths, void *y, void *workspace,
+                  int64_t workspace_bytes, int64_t batch, int64_t time, int64_t heads, int64_t queries,
+                  int64_t head_dim, void *stream);
+
 /* Library version string (static storage). */
 const char *tf_version(void);
 

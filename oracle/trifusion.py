@@ -26,7 +26,9 @@ replace:
   autocast makes: ``block_pre`` (mask, pre norm, 4:1 pool), ``glu_depthwise``,
   ``norm_silu``, ``pooled_attention`` (rotary, fp32 SDPA, head merge),
   ``merge_gate`` (mean norm, gate linear) and ``merge_conv`` (gated concat,
-  depthwise merge, bf16 add).
+  depthwise merge, bf16 add);
+* ``query_read``: the decoder's ``QueryRead`` attention (``decoder.py:24-30``,
+  ``attention.py:8-18``): fp32 SDPA of the shared queries over a key prefix.
 
 Pinning (tests/test_oracle_trifusion.py): each against an explicit loop or
 closed form on small inputs.
@@ -179,3 +181,16 @@ def merge_conv(cn, mn, an, g, weight, bias, lengths):
     v = gated_concat(torch.cat((cn.float(), mn.float(), an.float()), -1), g)
     conv = depthwise_masked(v.to(BF16), weight.to(BF16), bias.to(BF16), lengths).float()
     return (v + conv).to(BF16)
+
+
+def query_read(q, kv, key_lengths, heads=8):
+    """``q [Q, heads D]``, ``kv [B, T, 2 heads D]`` -> ``[B, Q, heads D]`` bf16: fp32
+    SDPA with keys ``j < key_lengths[b]``."""
+    b, t, width = kv.shape
+    nq, qw = q.shape
+    d = qw // heads
+    k, v = kv.float().view(b, t, 2, heads, d).permute(2, 0, 3, 1, 4).unbind(0)
+    qq = q.float().view(nq, heads, d).transpose(0, 1).unsqueeze(0).expand(b, -1, -1, -1)
+    mask = time_mask(key_lengths, t)[:, None, None, :]
+    y = F.scaled_dot_product_attention(qq, k, v, attn_mask=mask)
+    return y.transpose(1, 2).reshape(b, nq, qw).to(BF16)

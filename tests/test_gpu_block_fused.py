@@ -27,6 +27,7 @@ from trifusion_amd.kernels.block import (
     merge_gate,
     norm_silu,
     pooled_attention,
+    query_read,
 )
 from trifusion_amd.kernels.buffers import mask_buffer
 from trifusion_amd.kernels.native import add, mean_norm
@@ -146,3 +147,15 @@ def test_evidence_norm_bf16_out():
     y32 = evidence_norm(x, value, gate, w, mask)
     y16 = evidence_norm(x, value, gate, w, mask, bf16_out=True)
     assert y16.dtype == BF and torch.equal(y16, y32.to(BF))
+
+
+@pytest.mark.parametrize("t,lengths", [(101, [101, 57, 4]), (1608, [1608, 800, 8]), (70, [0, 1])])
+def test_query_read(t, lengths):
+    g = gen(t)
+    lengths = torch.tensor(lengths)
+    q = (torch.randn(10, 256, generator=g) * 0.5).to(BF)
+    kv = torch.randn(len(lengths), t, 512, generator=g).to(BF)
+    y = query_read(q.to(DEV), kv.to(DEV), lengths.to(DEV)).cpu()
+    some = lengths > 0
+    close_bf16(y[some], O.query_read(q, kv, lengths)[some], steps=2)
+    assert not y[~some].any()

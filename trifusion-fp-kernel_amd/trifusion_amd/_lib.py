@@ -132,6 +132,8 @@ _SIGNATURES = {
         [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_ptr],
         c_i32,
     ),
+    "tf_query_read_workspace_size": ([c_i64, c_i64, c_i64, c_i64, c_i64], c_i64),
+    "tf_query_read": ([c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_ptr], c_i32),
     "tf_version": ([], ctypes.c_char_p),
 }
 

@@ -478,3 +478,28 @@ def launch_merge_conv(cn, mn, an, g, weight, bias, lengths):
                                _lib.stream_of(cn))
     _lib.check(status, "merge_conv")
     return y
+
+
+def query_read(q, kv, key_lengths, heads=8):
+    """Decoder query read: ``q [Q, heads D]`` (bf16, shared by the batch), ``kv
+    [B, T, 2 heads D]`` -> ``[B, Q, heads D]`` bf16, fp32 softmax over keys
+    ``j < key_lengths`` (``trifusion_amd::query_read``)."""
+    return ops.query_read(q, kv, key_lengths, int(heads))
+
+
+def launch_query_read(q, kv, key_lengths, heads):
+    lib = _lib.load()
+    _lib.require_cuda(q, kv, key_lengths, what="query_read")
+    qc, kc = _bf16(q, "query_read", "q"), _bf16(kv, "query_read", "kv")
+    b, t, width = kc.shape
+    nq, qw = qc.shape
+    d = qw // heads
+    if width != 2 * qw or qw != heads * d:
+        raise ValueError("query_read: kv must be [B, T, 2 heads D] and q [Q, heads D]")
+    y = torch.empty((b, nq, qw), device=kv.device, dtype=torch.bfloat16)
+    size = lib.tf_query_read_workspace_size(b, t, heads, nq, d)
+    ws = torch.empty((max(size, 4),), device=kv.device, dtype=torch.uint8)
+    status = lib.tf_query_read(qc.data_ptr(), kc.data_ptr(), _lengths(key_lengths).data_ptr(), y.data_ptr(),
+                               ws.data_ptr(), ws.numel(), b, t, heads, nq, d, _lib.stream_of(kv))
+    _lib.check(status, "query_read")
+    return y

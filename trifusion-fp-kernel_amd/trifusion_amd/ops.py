@@ -71,6 +71,7 @@ _SCHEMAS = {
     "merge_conv": (
         "merge_conv(Tensor cn, Tensor mn, Tensor an, Tensor g, Tensor weight, Tensor bias, Tensor lengths) -> Tensor"
     ),
+    "query_read": "query_read(Tensor q, Tensor kv, Tensor key_lengths, int heads) -> Tensor",
     "front_conv2": (
         "front_conv2(Tensor h, Tensor weight, Tensor norm_weight, Tensor x, Tensor skip_weight, Tensor lengths, "
         "int stride, float eps) -> Tensor"
@@ -344,6 +345,10 @@ def _meta_front_conv2(h, weight, norm_weight, x, skip_weight, lengths, stride, e
     return torch.empty_like(h, memory_format=torch.contiguous_format)
 
 
+def _meta_query_read(q, kv, key_lengths, heads):
+    return kv.new_empty((kv.shape[0], q.shape[0], q.shape[1]), dtype=torch.bfloat16)
+
+
 # ---- CPU kernels: loud failure, no fallback ----
 
 
@@ -379,7 +384,7 @@ _KERNELS = {
         name: (_block(name), globals()["_meta_" + name])
         for name in ("depthwise_masked", "pool4", "rotary_qkv", "front_norm", "interpolate", "bands",
                      "evidence_norm", "gated_concat", "front_conv1", "front_conv2", "block_pre", "norm_silu",
-                     "glu_depthwise", "pooled_attention", "merge_gate", "merge_conv")
+                     "glu_depthwise", "pooled_attention", "merge_gate", "merge_conv", "query_read")
     },
 }
 

@@ -49,11 +49,12 @@ from .kernels.block import (
     norm_silu,
     pack_conv3x3,
     pooled_attention,
+    query_read,
 )
 from .kernels.buffers import mask_buffer
 from .kernels.native import add, add_rms, mean_norm
 from .mamba import Mamba3Inference
-from .masking import time_mask
+from .masking import masked_mean, time_mask
 
 
 @dataclass
@@ -376,8 +377,13 @@ class QueryRead(nn.Module):
         self.q = nn.Linear(256, 256, bias=False)
         self.out = nn.Linear(256, 256, bias=False)
 
-    def forward(self, query, x, mask):
+    def forward(self, query, x, mask, key_lengths=None):
+        """``mask`` marks the valid keys; ``key_lengths`` (valid keys form a prefix
+        of that length) selects the fused query-read kernel under bf16 autocast."""
         b, t, _ = x.shape
+        if key_lengths is not None and x.is_cuda and _bf16_autocast():
+            h = self.out(query_read(self.q(query), self.kv(x), key_lengths, 8))
+            return h[:, :4].mean(1), h[:, 4:8].mean(1), h[:, 8:].mean(1)
         k, v = self.kv(x).view(b, t, 2, 8, 32).permute(2, 0, 3, 1, 4).unbind(0)
         q = self.q(query).view(10, 8, 32).transpose(0, 1).unsqueeze(0).expand(b, -1, -1, -1)
         h = self.out(masked_attention(q, k, v, mask[:, None, None, :]).transpose(1, 2).reshape(b, 10, 256))
@@ -405,10 +411,16 @@ class Decoder(nn.Module):
         b, tf, _, _ = fine.shape
         dev = x.device
         fm = time_mask(fine_lengths, tf)
-        deep = self.deep_read(self.query, x, grids.mask)
+        deep = self.deep_read(self.query, x, grids.mask, grids.lengths)
         fp = fine + sin_position(tf, 64, dev)[None, :, None, :].to(fine.dtype) + self.band.to(fine.dtype)[None, None]
-        fine_q = self.fine_read(self.query, fp.flatten(1, 2), fm[:, :, None].expand(b, tf, 8).reshape(b, -1))
-        global_feature = self.global_proj((x.float() * grids.mask[..., None]).sum(1) / grids.lengths[:, None])
+        # the fine keys are (frame, band) pairs: valid exactly below 8 * fine_lengths
+        fine_q = self.fine_read(self.query, fp.flatten(1, 2), fm[:, :, None].expand(b, tf, 8).reshape(b, -1),
+                                8 * fine_lengths)
+        if x.is_cuda:
+            pooled = masked_mean(x.float(), grids.lengths)
+        else:
+            pooled = (x.float() * grids.mask[..., None]).sum(1) / grids.lengths[:, None]
+        global_feature = self.global_proj(pooled)
         end = mf[torch.arange(b, device=dev), grids.lengths - 1]
         memory = self.memory_proj(torch.cat((end, mb[:, 0]), -1))
         flat = fine.flatten(2)
