@@ -457,6 +457,30 @@ int tf_query_read(const void *q, const void *kv, const int64_t *key_lengths, voi
                   int64_t workspace_bytes, int64_t batch, int64_t time, int64_t heads, int64_t queries,
                   int64_t head_dim, void *stream);
 
+/*
+ * Front-end preparations (src/trifusion_l4/front.py:62-90, masking.py:14-57), one launch each:
+ *  - tf_mask_audio: y[b, c, n] = n < lengths[b] && c < channels[b] ? audio[b, c, n] : 0 (fp32,
+ *    contiguous [B, C, N]);
+ *  - tf_log_power: y[b, f, k] = f < lengths[b] / hop + 1 ? log(1e-6 + sum_c |spec[b C + c, k, f]|^2
+ *    / channels[b]) : 0, spec complex64 (interleaved) with element strides[3] (complex units),
+ *    y fp32 contiguous [B, frames, bins];
+ *  - tf_front_lengths: out[0] = n / hop + 1 (frames), out[i + 1] = ceil(out[i] / strides[i]), int64
+ *    [4, B];
+ *  - tf_grids: mask[b, t] = t < L_b, low_lengths = ceil(L / 4), low_mask[b, j] = j < low_b, and the
+ *    interpolation grid pos = min(max((t + 0.5) low / L - 0.5, 0), low - 1) (fp32, op by op),
+ *    left = trunc(pos), right = min(left + 1, low - 1), alpha = pos - left; masks are bytes.
+ * Replace the elementwise torch runs of Frontend.spectrogram, the stage length updates and
+ * Grids.make (src/trifusion_l4/front.py:62-90,105-110, masking.py:29-57).
+ */
+int tf_mask_audio(const float *audio, const int64_t *lengths, const int64_t *channels, float *y, int64_t batch,
+                  int64_t chans, int64_t samples, void *stream);
+int tf_log_power(const void *spec, const int64_t *strides, const int64_t *channels, const int64_t *sample_lengths,
+                 float *y, int64_t batch, int64_t chans, int64_t bins, int64_t frames, int64_t hop, void *stream);
+int tf_front_lengths(const int64_t *sample_lengths, int64_t *out, int64_t batch, int64_t hop,
+                     const int64_t *strides, void *stream);
+int tf_grids(const int64_t *lengths, void *mask, int64_t *low_lengths, void *low_mask, int64_t *left,
+             int64_t *right, float *alpha, int64_t batch, int64_t time, void *stream);
+
 /* Library version string (static storage). */
 const char *tf_version(void);
 

@@ -134,6 +134,13 @@ _SIGNATURES = {
     ),
     "tf_query_read_workspace_size": ([c_i64, c_i64, c_i64, c_i64, c_i64], c_i64),
     "tf_query_read": ([c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_i64, c_i64, c_ptr], c_i32),
+    "tf_mask_audio": ([c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_ptr], c_i32),
+    "tf_log_power": (
+        [c_ptr, ctypes.POINTER(c_i64), c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_i64, c_i64, c_ptr],
+        c_i32,
+    ),
+    "tf_front_lengths": ([c_ptr, c_ptr, c_i64, c_i64, ctypes.POINTER(c_i64), c_ptr], c_i32),
+    "tf_grids": ([c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_ptr], c_i32),
     "tf_version": ([], ctypes.c_char_p),
 }
 

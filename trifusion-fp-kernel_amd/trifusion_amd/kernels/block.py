@@ -503,3 +503,88 @@ def launch_query_read(q, kv, key_lengths, heads):
                                ws.data_ptr(), ws.numel(), b, t, heads, nq, d, _lib.stream_of(kv))
     _lib.check(status, "query_read")
     return y
+
+
+# ---- front-end preparations (csrc/front_prep.hip) ----
+
+
+def mask_audio(audio, lengths, channels):
+    """``[B, C, N]`` waveform -> fp32 ``[B C, N]`` with samples past each length and
+    channels past each channel count cleared (``trifusion_amd::mask_audio``)."""
+    return ops.mask_audio(audio, lengths, channels)
+
+
+def launch_mask_audio(audio, lengths, channels):
+    lib = _lib.load()
+    _lib.require_cuda(audio, lengths, channels, what="mask_audio")
+    x = audio.float().contiguous()
+    b, c, n = x.shape
+    y = torch.empty((b * c, n), device=x.device, dtype=torch.float32)
+    status = lib.tf_mask_audio(x.data_ptr(), _lengths(lengths).data_ptr(), _lengths(channels).data_ptr(),
+                               y.data_ptr(), b, c, n, _lib.stream_of(x))
+    _lib.check(status, "mask_audio")
+    return y
+
+
+def log_power(spec, channels, sample_lengths, hop=160):
+    """complex ``[B C, bins, frames]`` STFT -> fp32 ``[B, frames, bins]`` log power
+    averaged over channels, frames past each clip's count 0 (``trifusion_amd::log_power``)."""
+    return ops.log_power(spec, channels, sample_lengths, int(hop))
+
+
+def launch_log_power(spec, channels, sample_lengths, hop):
+    lib = _lib.load()
+    _lib.require_cuda(spec, channels, sample_lengths, what="log_power")
+    if spec.dtype != torch.complex64:
+        raise TypeError("log_power: spectrum must be complex64")
+    bc, bins, frames = spec.shape
+    b = channels.shape[0]
+    if bc % b:
+        raise ValueError("log_power: spectrum rows must be batch x channels")
+    y = torch.empty((b, frames, bins), device=spec.device, dtype=torch.float32)
+    status = lib.tf_log_power(spec.data_ptr(), (ctypes.c_int64 * 3)(*spec.stride()), _lengths(channels).data_ptr(),
+                              _lengths(sample_lengths).data_ptr(), y.data_ptr(), b, bc // b, bins, frames, hop,
+                              _lib.stream_of(spec))
+    _lib.check(status, "log_power")
+    return y
+
+
+def front_lengths(sample_lengths, hop=160, strides=(1, 2, 2)):
+    """int64 ``[4, B]``: frames ``n // hop + 1`` and the counts after each CNN stage
+    (``trifusion_amd::front_lengths``)."""
+    return ops.front_lengths(sample_lengths, int(hop), [int(s) for s in strides])
+
+
+def launch_front_lengths(sample_lengths, hop, strides):
+    lib = _lib.load()
+    _lib.require_cuda(sample_lengths, what="front_lengths")
+    n = _lengths(sample_lengths)
+    out = torch.empty((4, n.shape[0]), device=n.device, dtype=torch.int64)
+    status = lib.tf_front_lengths(n.data_ptr(), out.data_ptr(), n.shape[0], hop, (ctypes.c_int64 * 3)(*strides),
+                                  _lib.stream_of(n))
+    _lib.check(status, "front_lengths")
+    return out
+
+
+def grids(lengths, time):
+    """``(mask, low_lengths, low_mask, left, right, alpha)`` of the frame grid and its
+    4:1 pooled grid (``trifusion_amd::grids``)."""
+    return ops.grids(lengths, int(time))
+
+
+def launch_grids(lengths, time):
+    lib = _lib.load()
+    _lib.require_cuda(lengths, what="grids")
+    n = _lengths(lengths)
+    b, dev = n.shape[0], n.device
+    lt = (time + 3) // 4
+    mask = torch.empty((b, time), device=dev, dtype=torch.bool)
+    low = torch.empty((b,), device=dev, dtype=torch.int64)
+    low_mask = torch.empty((b, lt), device=dev, dtype=torch.bool)
+    left = torch.empty((b, time), device=dev, dtype=torch.int64)
+    right = torch.empty((b, time), device=dev, dtype=torch.int64)
+    alpha = torch.empty((b, time), device=dev, dtype=torch.float32)
+    status = lib.tf_grids(n.data_ptr(), mask.data_ptr(), low.data_ptr(), low_mask.data_ptr(), left.data_ptr(),
+                          right.data_ptr(), alpha.data_ptr(), b, time, _lib.stream_of(n))
+    _lib.check(status, "grids")
+    return mask, low, low_mask, left, right, alpha

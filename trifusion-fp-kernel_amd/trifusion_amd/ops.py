@@ -72,6 +72,10 @@ _SCHEMAS = {
         "merge_conv(Tensor cn, Tensor mn, Tensor an, Tensor g, Tensor weight, Tensor bias, Tensor lengths) -> Tensor"
     ),
     "query_read": "query_read(Tensor q, Tensor kv, Tensor key_lengths, int heads) -> Tensor",
+    "mask_audio": "mask_audio(Tensor audio, Tensor lengths, Tensor channels) -> Tensor",
+    "log_power": "log_power(Tensor spec, Tensor channels, Tensor sample_lengths, int hop) -> Tensor",
+    "front_lengths": "front_lengths(Tensor sample_lengths, int hop, int[] strides) -> Tensor",
+    "grids": "grids(Tensor lengths, int time) -> (Tensor, Tensor, Tensor, Tensor, Tensor, Tensor)",
     "front_conv2": (
         "front_conv2(Tensor h, Tensor weight, Tensor norm_weight, Tensor x, Tensor skip_weight, Tensor lengths, "
         "int stride, float eps) -> Tensor"
@@ -349,6 +353,26 @@ def _meta_query_read(q, kv, key_lengths, heads):
     return kv.new_empty((kv.shape[0], q.shape[0], q.shape[1]), dtype=torch.bfloat16)
 
 
+def _meta_mask_audio(audio, lengths, channels):
+    b, c, n = audio.shape
+    return audio.new_empty((b * c, n), dtype=torch.float32)
+
+
+def _meta_log_power(spec, channels, sample_lengths, hop):
+    return spec.new_empty((channels.shape[0], spec.shape[2], spec.shape[1]), dtype=torch.float32)
+
+
+def _meta_front_lengths(sample_lengths, hop, strides):
+    return sample_lengths.new_empty((4, sample_lengths.shape[0]), dtype=torch.int64)
+
+
+def _meta_grids(lengths, time):
+    b, lt = lengths.shape[0], (time + 3) // 4
+    e = lengths.new_empty
+    return (e((b, time), dtype=torch.bool), e((b,), dtype=torch.int64), e((b, lt), dtype=torch.bool),
+            e((b, time), dtype=torch.int64), e((b, time), dtype=torch.int64), e((b, time), dtype=torch.float32))
+
+
 # ---- CPU kernels: loud failure, no fallback ----
 
 
@@ -384,7 +408,8 @@ _KERNELS = {
         name: (_block(name), globals()["_meta_" + name])
         for name in ("depthwise_masked", "pool4", "rotary_qkv", "front_norm", "interpolate", "bands",
                      "evidence_norm", "gated_concat", "front_conv1", "front_conv2", "block_pre", "norm_silu",
-                     "glu_depthwise", "pooled_attention", "merge_gate", "merge_conv", "query_read")
+                     "glu_depthwise", "pooled_attention", "merge_gate", "merge_conv", "query_read", "mask_audio",
+                     "log_power", "front_lengths", "grids")
     },
 }
 

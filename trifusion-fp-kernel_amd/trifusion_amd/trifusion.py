@@ -48,6 +48,10 @@ from .kernels.block import (
     merge_gate,
     norm_silu,
     pack_conv3x3,
+    front_lengths,
+    grids,
+    log_power,
+    mask_audio,
     pooled_attention,
     query_read,
 )
@@ -103,6 +107,20 @@ def masked_attention(q, k, v, mask):
     return y.to(dtype)
 
 
+_ROPE = {}
+
+
+def rope_tables(time, head_dim, device):
+    """cos/sin ``[time, head_dim / 2]`` of the rotary phases t 10000^(-2i/D), kept per
+    (time, head_dim, device): they depend on the shape only."""
+    key = (time, head_dim, str(device))
+    if key not in _ROPE:
+        freq = 10000.0 ** (-torch.arange(0, head_dim, 2, device=device).float() / head_dim)
+        phase = torch.arange(time, device=device).float()[:, None] * freq[None, :]
+        _ROPE[key] = (phase.cos(), phase.sin())
+    return _ROPE[key]
+
+
 class Grids:
     """Frame grid, its 4:1 pooled grid and the interpolation back
     (``masking.py:14-57``): per clip the frame and pooled lengths and masks,
@@ -112,19 +130,20 @@ class Grids:
     def __init__(self, lengths, time, head_dim):
         dev = lengths.device
         self.lengths = lengths
-        self.mask = time_mask(lengths, time)
-        self.low_lengths = (lengths + 3) // 4
         low_t = (time + 3) // 4
-        self.low_mask = time_mask(self.low_lengths, low_t)
-        centre = torch.arange(time, device=dev)[None, :].float() + 0.5
-        pos = (centre * self.low_lengths[:, None] / lengths[:, None] - 0.5).clamp_min(0)
-        pos = torch.minimum(pos, (self.low_lengths - 1)[:, None])
-        self.left = pos.long()
-        self.right = torch.minimum(self.left + 1, (self.low_lengths - 1)[:, None])
-        self.alpha = pos - self.left
-        freq = 10000.0 ** (-torch.arange(0, head_dim, 2, device=dev).float() / head_dim)
-        phase = torch.arange(low_t, device=dev).float()[:, None] * freq[None, :]
-        self.rope_cos, self.rope_sin = phase.cos(), phase.sin()
+        if lengths.is_cuda:
+            self.mask, self.low_lengths, self.low_mask, self.left, self.right, self.alpha = grids(lengths, time)
+        else:
+            self.mask = time_mask(lengths, time)
+            self.low_lengths = (lengths + 3) // 4
+            self.low_mask = time_mask(self.low_lengths, low_t)
+            centre = torch.arange(time, device=dev)[None, :].float() + 0.5
+            pos = (centre * self.low_lengths[:, None] / lengths[:, None] - 0.5).clamp_min(0)
+            pos = torch.minimum(pos, (self.low_lengths - 1)[:, None])
+            self.left = pos.long()
+            self.right = torch.minimum(self.left + 1, (self.low_lengths - 1)[:, None])
+            self.alpha = pos - self.left
+        self.rope_cos, self.rope_sin = rope_tables(low_t, head_dim, dev)
 
     def pool(self, x):
         return Pool4.apply(x.contiguous(), self.lengths)
@@ -158,8 +177,10 @@ class CNNStage(nn.Module):
             self._packed_key = key
         return self._packed
 
-    def forward(self, x, lengths):
-        lengths = (lengths + self.stride - 1) // self.stride
+    def forward(self, x, lengths, out_lengths=None):
+        """``lengths`` are the input's valid time steps; ``out_lengths``, when the
+        caller has them, the output's (ceil(lengths / stride))."""
+        lengths = (lengths + self.stride - 1) // self.stride if out_lengths is None else out_lengths
         if x.is_cuda and _bf16_autocast():
             return front_stage(self, x, lengths)
         h = front_norm(self.conv1(x), lengths, self.norm1, silu=True)
@@ -180,8 +201,19 @@ class Frontend(nn.Module):
         if channels_last:
             self.to(memory_format=torch.channels_last)
 
-    def spectrogram(self, audio, sample_lengths, channels):
+    def spectrogram(self, audio, sample_lengths, channels, frames=None):
+        """Masked log power ``[B, 1, frames, 257]`` and the frame counts (``frames``
+        when the caller has them)."""
         b, c, n = audio.shape
+        if audio.is_cuda:
+            # masking and the log-power post-processing as one launch each around rocFFT
+            wave = mask_audio(audio, sample_lengths, channels)
+            with torch.autocast("cuda", enabled=False):
+                spec = torch.stft(wave, n_fft=512, hop_length=160, win_length=400, window=self.window.float(),
+                                  center=True, pad_mode="constant", return_complex=True)
+            if frames is None:
+                frames = sample_lengths // 160 + 1
+            return log_power(spec, channels, sample_lengths, 160).unsqueeze(1), frames
         with torch.autocast("cuda", enabled=False):
             keep = time_mask(sample_lengths, n)[:, None, :] & (torch.arange(c, device=audio.device)[None, :]
                                                                < channels[:, None])[..., None]
@@ -196,7 +228,9 @@ class Frontend(nn.Module):
         return log, lengths
 
     def forward(self, audio, sample_lengths, channels):
-        x, lengths = self.spectrogram(audio, sample_lengths, channels)
+        # on the GPU, the frame counts before and after every stage in one launch
+        counts = front_lengths(sample_lengths, 160, [st.stride for st in self.stages]) if audio.is_cuda else None
+        x, lengths = self.spectrogram(audio, sample_lengths, channels, None if counts is None else counts[0])
         if self.channels_last:
             x = x.contiguous(memory_format=torch.channels_last)
         fine = fine_lengths = None
@@ -207,8 +241,12 @@ class Frontend(nn.Module):
         with torch.backends.cudnn.flags(enabled=torch.backends.cudnn.enabled, benchmark=False, deterministic=True,
                                         allow_tf32=False):
             for i, stage in enumerate(self.stages):
-                x = stage(x, lengths)
-                lengths = (lengths + stage.stride - 1) // stage.stride
+                if counts is None:
+                    x = stage(x, lengths)
+                    lengths = (lengths + stage.stride - 1) // stage.stride
+                else:
+                    x = stage(x, lengths, counts[i + 1])
+                    lengths = counts[i + 1]
                 if i == 1:
                     fine, fine_lengths = bands(x), lengths
         return bands(x).flatten(2), fine, lengths, fine_lengths
