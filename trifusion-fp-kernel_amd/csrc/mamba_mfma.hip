@@ -670,6 +670,14 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
     }
     lds_barrier();  // barrier 2: exchange tiles visible, phase staging no longer read
 
+    // gate operand of this half, loaded while the products and the state scan run
+    u32x4 zrow[PS] = {};
+    if (MODE == 0 && active) {
+      const uint16_t* z_row = zbase + (t < L ? t : t0) * P.z_st;
+#pragma unroll
+      for (int s = 0; s < PS; ++s) zrow[s] = load_row8(z_row, kidx(s, hh, 0));
+    }
+
     f32x16 yacc[PT] = {};  // y^T tiles: lane = t, elements = p
     if (active) {
       u32x4 scy_o[2];
@@ -718,13 +726,6 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
     }
     lds_barrier();  // barrier 3: every dS share in LDS
 
-    // gate operand of this half, loaded while the state scan runs
-    u32x4 zrow[PS] = {};
-    if (MODE == 0 && active) {
-      const uint16_t* z_row = zbase + (t < L ? t : t0) * P.z_st;
-#pragma unroll
-      for (int s = 0; s < PS; ++s) zrow[s] = load_row8(z_row, kidx(s, hh, 0));
-    }
     // controls and angles of the same half of the next super-chunk
     Ctl nxt = {};
     if (g0 + CW + cw < c_stop) {
