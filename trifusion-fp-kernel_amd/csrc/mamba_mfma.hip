@@ -434,10 +434,11 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
 
   lds_barrier();
 
-  // Half 0's q/k/v rows of the next super-chunk, issued before the output phase
-  // of this one (the output phase covers their latency; the live range is short
-  // enough to cost two registers). Half 1 keeps loading its rows after phase
-  // pass 1, which staggers the two halves' bursts.
+  // Half 0's q/k/v rows of the next super-chunk, issued before the state scan of
+  // this one (the scan and the output phase cover their latency). Half 1 keeps
+  // loading its rows after phase pass 1, which staggers the two halves' bursts;
+  // prefetching both halves, or issuing the next controls before the scan, was
+  // slower.
   HalfRows<KS, PS> pre = {};
   for (int g0 = c_begin; g0 < c_stop; g0 += CW) {
     // Lane-derived indices are rebuilt from an index the compiler cannot see
@@ -725,6 +726,11 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
       }
     }
     lds_barrier();  // barrier 3: every dS share in LDS
+    pre = {};
+    if (hf == 0 && g0 + CW + cw < c_stop) {
+      const int t0n = (g0 + CW + cw) * kChunk;
+      load_rows<MODE == 0>(P, pre, qbase, kbase, vbase, t0n, t0n + c32, L, hh);
+    }
 
     // controls and angles of the same half of the next super-chunk
     Ctl nxt = {};
@@ -767,11 +773,6 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
       }
     }
     lds_barrier();  // barrier 4: exclusive states in LDS
-    pre = {};
-    if (hf == 0 && g0 + CW + cw < c_stop) {
-      const int t0n = (g0 + CW + cw) * kChunk;
-      load_rows<MODE == 0>(P, pre, qbase, kbase, vbase, t0n, t0n + c32, L, hh);
-    }
 
     // ---------------- inter-chunk term, gate, store ----------------
     if (MODE == 0 && active) {
