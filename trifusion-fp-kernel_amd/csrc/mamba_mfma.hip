@@ -373,7 +373,12 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
   const int c_begin = tseg * P.SC;
   const int c_end = min(c_begin + P.SC, (T + kChunk - 1) / kChunk);
   const int c_stop = min(c_end, nvalid);
-  const int rs = (R + 1) & ~1;  // row stride of the staged phases (even: 8-byte pair reads)
+  // Row stride of the staged phases: even (8-byte pair reads) and, where the
+  // slot has room, 2 more than a multiple of 4 floats, so that the rows of one
+  // read (lane = row) fall on distinct LDS banks; a multiple of 16 floats would
+  // put 16 rows on the same bank.
+  const int rs0 = (R + 1) & ~1;
+  const int rs = (rs0 % 4 == 0 && 64 * (rs0 + 2) <= 4 * kF4) ? rs0 + 2 : rs0;
   const float skip = P.d[h];
   const int tlim = P.rev ? L : T;  // steps that have a row (halo bound)
 
