@@ -84,7 +84,10 @@ __global__ __launch_bounds__(256) void block_pre_kernel(const float* __restrict_
                                                         const float* __restrict__ w, float* __restrict__ xm,
                                                         uint16_t* __restrict__ h16, uint16_t* __restrict__ p16,
                                                         int T, int LT, int d, float eps) {
-  extern __shared__ float hs[];  // [4][d]
+  // fp32 norm rows as float4 [4 rows][2 halves][d / 8]: half e of 8-element group
+  // c8 holds elements 8 c8 + 4 e .. + 3, so consecutive lanes touch consecutive
+  // 16-byte slots (conflict-free LDS access)
+  extern __shared__ float4 hs4[];
   const int lane = threadIdx.x & 63, k = threadIdx.x >> 6;
   const int j = blockIdx.x, b = blockIdx.y;
   const int t = 4 * j + k;
@@ -120,8 +123,9 @@ __global__ __launch_bounds__(256) void block_pre_kernel(const float* __restrict_
 #pragma unroll
         for (int e = 0; e < 8; ++e) o[e] = v[i][e] * r * wv[e];
         st8_bf16(h16 + row * d + i0, o);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) hs[k * d + i0 + e] = o[e];
+        const int c8 = lane + 64 * i;
+        hs4[(2 * k) * (d / 8) + c8] = make_float4(o[0], o[1], o[2], o[3]);
+        hs4[(2 * k + 1) * (d / 8) + c8] = make_float4(o[4], o[5], o[6], o[7]);
       }
     }
   }
@@ -129,12 +133,20 @@ __global__ __launch_bounds__(256) void block_pre_kernel(const float* __restrict_
   const int count = max(min(L - 4 * j, 4), 1);
   const int64_t prow = static_cast<int64_t>(b) * LT + j;
   for (int c8 = threadIdx.x; c8 < d / 8; c8 += blockDim.x) {
+    float hv[4][8];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4 lo = hs4[(2 * q) * (d / 8) + c8], hi = hs4[(2 * q + 1) * (d / 8) + c8];
+      const float e8[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) hv[q][e] = 4 * j + q < L ? e8[e] : 0.f;
+    }
     float o[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       float acc = 0.f;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) acc = add_nc(acc, 4 * j + q < L ? hs[q * d + 8 * c8 + e] : 0.f);
+      for (int q = 0; q < 4; ++q) acc = add_nc(acc, hv[q][e]);
       o[e] = acc / static_cast<float>(count);
     }
     st8_bf16(p16 + prow * d + 8 * c8, o);
