@@ -212,55 +212,75 @@ __device__ __forceinline__ void load_taps(const uint16_t* w, const uint16_t* bia
 }
 
 // ---- GLU + masked depthwise conv ----------------------------------------------
-// One wave per (512 channels, TT time steps, batch row); each lane 8 channels. The GLU
-// rows t0 - K/2 .. t0 + TT - 1 + K/2 (bf16, a * 1 / (1 + e^-b)) are formed once
-// and slid over; sources outside [0, T) are 0, outputs at t >= L are 0.
-template <int K, int TT>
-__global__ __launch_bounds__(64) void glu_depthwise_kernel(const uint16_t* __restrict__ up,
-                                                           const uint16_t* __restrict__ w,
-                                                           const uint16_t* __restrict__ bias,
-                                                           const int64_t* __restrict__ lengths,
-                                                           uint16_t* __restrict__ y, int T, int d) {
-  const int t0 = blockIdx.y * TT, b = blockIdx.z;
+// One workgroup per (512 channels, TW time steps, batch row), lane = 8 channels.
+// Its four waves form the GLU rows t0 - K/2 .. t0 + TW - 1 + K/2 once (row r by
+// wave r % 4, a * 1 / (1 + e^-b) rounded to bf16, kept as bf16 in LDS), then
+// each wave convolves TW / 4 consecutive time steps from LDS. Sources outside
+// [0, T) are 0, outputs at t >= L are 0.
+template <int K, int TW>
+__global__ __launch_bounds__(256) void glu_depthwise_kernel(const uint16_t* __restrict__ up,
+                                                            const uint16_t* __restrict__ w,
+                                                            const uint16_t* __restrict__ bias,
+                                                            const int64_t* __restrict__ lengths,
+                                                            uint16_t* __restrict__ y, int T, int d) {
+  constexpr int R = TW + K - 1;  // GLU rows of the tile
+  constexpr int TO = TW / 4;     // outputs per wave
+  static_assert(TW % 4 == 0, "four waves share the tile's time steps");
+  __shared__ uint4 glu[R][64];   // [row][lane]: 8 bf16 channels per 16 bytes
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t0 = blockIdx.y * TW, b = blockIdx.z;
   const int L = clamp_len(lengths, b, T);
-  const int c8 = blockIdx.x * 64 + threadIdx.x;
-  if (c8 < d / 8) {
-    const int c = 8 * c8;
-    float win[TT + K - 1][8];
+  const int c8 = blockIdx.x * 64 + lane;
+  const bool on = c8 < d / 8;
+  const int c = 8 * c8;
+  for (int r = wave; r < R; r += 4) {
+    const int t = t0 - K / 2 + r;
+    float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (on && t >= 0 && t < T) {
+      float a[8], g[8];
+      const uint16_t* src = up + (static_cast<int64_t>(b) * T + t) * 2 * d;
+      ld8(src + c, a);
+      ld8(src + d + c, g);
 #pragma unroll
-    for (int r = 0; r < TT + K - 1; ++r) {
-      const int t = t0 - K / 2 + r;
-      if (t >= 0 && t < T) {
-        float a[8], g[8];
-        const uint16_t* src = up + (static_cast<int64_t>(b) * T + t) * 2 * d;
-        ld8(src + c, a);
-        ld8(src + d + c, g);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) win[r][e] = round_bf16(a[e] * (1.0f / (1.0f + expf(-g[e]))));
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) win[r][e] = 0.f;
-      }
+      for (int e = 0; e < 8; ++e) o[e] = a[e] * (1.0f / (1.0f + expf(-g[e])));
     }
-    float wk[8][K], bb[8];
-    load_taps<K>(w + static_cast<int64_t>(c) * K, bias + c, wk, bb);
+    uint32_t wd[4];
 #pragma unroll
-    for (int i = 0; i < TT; ++i) {
-      const int t = t0 + i;
-      if (t < T) {
-        float o[8];
+    for (int e = 0; e < 4; ++e)
+      wd[e] = static_cast<uint32_t>(f32_to_bf16(o[2 * e])) | (static_cast<uint32_t>(f32_to_bf16(o[2 * e + 1])) << 16);
+    glu[r][lane] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+  }
+  __syncthreads();
+  if (!on) return;
+  float wk[8][K], bb[8];
+  load_taps<K>(w + static_cast<int64_t>(c) * K, bias + c, wk, bb);
+  float win[TO + K - 1][8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          float acc = 0.f;
-          if (t < L) {
+  for (int r = 0; r < TO + K - 1; ++r) {
+    const uint4 q = glu[wave * TO + r][lane];
+    const uint32_t wd[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-            for (int q = 0; q < K; ++q) acc = add_nc(acc, mul_nc(win[i + q][e], wk[e][q]));
-            acc = add_nc(acc, bb[e]);
-          }
-          o[e] = acc;
+    for (int e = 0; e < 4; ++e) {
+      win[r][2 * e] = __uint_as_float(wd[e] << 16);
+      win[r][2 * e + 1] = __uint_as_float(wd[e] & 0xffff0000u);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < TO; ++i) {
+    const int t = t0 + wave * TO + i;
+    if (t < T) {
+      float o[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float acc = 0.f;
+        if (t < L) {
+#pragma unroll
+          for (int q = 0; q < K; ++q) acc = add_nc(acc, mul_nc(win[i + q][e], wk[e][q]));
+          acc = add_nc(acc, bb[e]);
         }
-        st8_bf16(y + (static_cast<int64_t>(b) * T + t) * d + c, o);
+        o[e] = acc;
       }
+      st8_bf16(y + (static_cast<int64_t>(b) * T + t) * d + c, o);
     }
   }
 }
@@ -574,7 +594,8 @@ int per8_of(int64_t d) {
   return per8;
 }
 
-constexpr int kTT = 4;  // time steps per depthwise tile
+constexpr int kTT = 4;     // time steps per depthwise tile (merge_conv)
+constexpr int kGluTW = 8;  // time steps per GLU + depthwise workgroup
 
 }  // namespace
 }  // namespace tf
@@ -630,16 +651,16 @@ extern "C" int tf_glu_depthwise(const void* up, const void* w, const void* bias,
                                 int64_t batch, int64_t time, int64_t d, int64_t k, void* stream) {
   if (!up || !w || !bias || !lengths || !y) return TF_ERR_NULL;
   if (batch < 0 || time < 0 || d < 8 || d % 8 || batch > 65535 || batch * time > 0x7fffffff ||
-      (time + tf::kTT - 1) / tf::kTT > 65535)
+      (time + tf::kGluTW - 1) / tf::kGluTW > 65535)
     return TF_ERR_SHAPE;
   if (!tf::a16(up) || !tf::a16(y) || !tf::a16(w) || !tf::a16(bias)) return TF_ERR_SHAPE;
   if (batch * time == 0) return TF_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid(static_cast<uint32_t>((d / 8 + 63) / 64), static_cast<uint32_t>((time + tf::kTT - 1) / tf::kTT),
-                  static_cast<uint32_t>(batch));
+  const dim3 grid(static_cast<uint32_t>((d / 8 + 63) / 64),
+                  static_cast<uint32_t>((time + tf::kGluTW - 1) / tf::kGluTW), static_cast<uint32_t>(batch));
 #define TF_GLU(KV)                                                                                               \
   if (k == KV) {                                                                                                  \
-    hipLaunchKernelGGL((tf::glu_depthwise_kernel<KV, tf::kTT>), grid, dim3(64), 0, s,                            \
+    hipLaunchKernelGGL((tf::glu_depthwise_kernel<KV, tf::kGluTW>), grid, dim3(256), 0, s,                        \
                        static_cast<const uint16_t*>(up), static_cast<const uint16_t*>(w),                        \
                        static_cast<const uint16_t*>(bias), lengths, static_cast<uint16_t*>(y),                   \
                        static_cast<int>(time), static_cast<int>(d));                                             \
