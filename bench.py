@@ -44,6 +44,7 @@ WORKLOADS = {
 }
 METRIC = "fused_mamba GB/s & %HBM peak; ms/forward 4s mono×16 encoder, 1 MI355X"
 TRAFFIC_FILE = ROOT / "profiles" / "fused_mamba_clip_b16_l400_pmc.txt"
+COUNTERS_FILE = ROOT / "profiles" / "fused_mamba_clip_b16_l400_counters.txt"
 
 
 def parse_args():
@@ -99,6 +100,23 @@ def traffic_bytes():
         if line.startswith("traffic_bytes_per_call:"):
             return int(line.split(":", 1)[1].strip())
     return None
+
+
+def utilisation_counters():
+    """MfmaUtil / VALUBusy (percent) of the clip kernel from the committed
+    rocprofv3 --pmc summary, if any."""
+    if not COUNTERS_FILE.exists():
+        return None
+    out = {}
+    for line in COUNTERS_FILE.read_text().splitlines():
+        parts = line.split()
+        if len(parts) >= 3 and parts[0] in ("MfmaUtil", "VALUBusy") and parts[-1] == "%":
+            out[parts[0]] = float(parts[-2])
+    if not out:
+        return None
+    out["unit"] = "percent"
+    out["source"] = "profiles/" + COUNTERS_FILE.name
+    return out
 
 
 def time_fused_mamba(args, torch, fused_mamba, sets, steps, warmup, variant, eager, lengths=None):
@@ -376,6 +394,8 @@ def main():
             "traffic": traffic_bytes() if args.workload == "clip" else None,
         },
     }
+    if args.workload == "clip":
+        line["counters"] = utilisation_counters()
     if not args.no_kernels and args.workload == "clip":
         line["bandwidth_kernels"] = bandwidth_kernels(torch)
     if not args.no_encoder:
