@@ -397,12 +397,20 @@ class TriFusionBlock(nn.Module):
         return add(r, self.down(f), mask), mf, mb
 
 
-def sin_position(time, dim, device):
-    """Interleaved sin/cos positions ``[time, dim]`` (``decoder.py:9-14``)."""
-    phase = torch.arange(time, device=device).float()[:, None] * (
-        10000.0 ** (-torch.arange(0, dim, 2, device=device).float() / dim)
-    )[None, :]
-    return torch.stack((phase.sin(), phase.cos()), -1).flatten(-2)
+_SINPOS = {}
+
+
+def sin_position(time, dim, device, dtype=torch.float32):
+    """Interleaved sin/cos positions ``[time, dim]`` (``decoder.py:9-14``), formed
+    in fp32 and cast to ``dtype``; kept per (time, dim, device, dtype), since they
+    depend on the shape only (one table instead of eight launches per forward)."""
+    key = (time, dim, str(device), dtype)
+    if key not in _SINPOS:
+        phase = torch.arange(time, device=device).float()[:, None] * (
+            10000.0 ** (-torch.arange(0, dim, 2, device=device).float() / dim)
+        )[None, :]
+        _SINPOS[key] = torch.stack((phase.sin(), phase.cos()), -1).flatten(-2).to(dtype)
+    return _SINPOS[key]
 
 
 class QueryRead(nn.Module):
@@ -450,7 +458,7 @@ class Decoder(nn.Module):
         dev = x.device
         fm = time_mask(fine_lengths, tf)
         deep = self.deep_read(self.query, x, grids.mask, grids.lengths)
-        fp = fine + sin_position(tf, 64, dev)[None, :, None, :].to(fine.dtype) + self.band.to(fine.dtype)[None, None]
+        fp = fine + sin_position(tf, 64, dev, fine.dtype)[None, :, None, :] + self.band.to(fine.dtype)[None, None]
         # the fine keys are (frame, band) pairs: valid exactly below 8 * fine_lengths
         fine_q = self.fine_read(self.query, fp.flatten(1, 2), fm[:, :, None].expand(b, tf, 8).reshape(b, -1),
                                 8 * fine_lengths)
