@@ -854,9 +854,9 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
 // entering segment g,
 //   S_0 = 0,  S_{g+1} = S_g 2^{T_g} + dS_g,
 // the composition the serial walk applies chunk by chunk. Workgroup
-// (unit, slice) takes 256 float4 of the unit's state, so the few units of a
+// (unit, slice) takes kScanSlice float4 of the unit's state, so the few units of a
 // long sequence still spread over many CUs.
-constexpr int kScanSlice = 256;
+constexpr int kScanSlice = 64;  // one wave per slice (256 float4 per slice: 1 us slower at B1 L7200)
 
 __global__ __launch_bounds__(kScanSlice) void segment_scan_kernel(float4* state, const float* decay, int kf4, int G) {
   constexpr int kBatch = 16;  // records loaded ahead of the serial chain
