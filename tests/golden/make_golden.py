@@ -13,6 +13,33 @@ special cases its maths fixes (mamba_fused.py:72-152):
   y_t = silu(z_t) * (sum_{u<t} (q~_t . k~_u) dt_u v_u + (D + dt_t q~_t . k~_t) v_t),
   with q~ = q + qb, k~ = k + kb.
 
+The remaining cases pin the trapezoid step s_u that scales key u
+(mamba_fused.py:96-101), which the cases above cannot see: with trap = 30 the
+next-step term dt_{u+1} (1 - sigmoid(trap_{u+1})) is exactly 0. Each uses
+trap = +-40, whose sigmoid is 1 or 0 in float32 and float64 alike, no rotation
+(theta = 0), and writes s_u from a table of the neighbours' sigmoids instead of
+the formula, so a sigmoid written where 1 - sigmoid belongs, or step t read
+where t + 1 belongs, changes the answer:
+
+  sig_u  sig_{u+1} | s_u                 (u < T - 1)
+    1       1      | dt_u
+    1       0      | dt_u + dt_{u+1}
+    0       1      | 0
+    0       0      | dt_{u+1}
+  and s_{T-1} = dt_{T-1} sig_{T-1} (the step past the sequence loads 0).
+
+  y_t = silu(z_t) * (sum_{u<t} exp(sum_{m=u+1..t} adt_m) (q~_t . k~_u) s_u v_u
+                     + (D + dt_t sig_t q~_t . k~_t) v_t).
+
+* ``shift`` (T = 96): trap = -40 everywhere, no decay: s_u = dt_{u+1}, no skip
+  term from the keys' own step.
+* ``mixed_trap`` (T = 96): trap = +-40 at random, no decay: all four rows of
+  the table occur.
+* ``segmented`` (B = 1, H = 1, T = 300): mixed trap and a constant decay
+  adt = -0.02. With a single (batch, head) unit the MFMA kernel cuts the
+  sequence into segments (a boundary at t = 256), so the step at the end of a
+  segment reads its halo from the next segment.
+
 q, k, v and z are rounded to bf16 values (stored as float32), so bf16 kernels
 read them exactly. Shapes use N = P = 32, R = 8, Hq = 1, which every kernel
 variant takes. Run from the repository root: ``python tests/golden/make_golden.py``.
@@ -85,9 +112,64 @@ def linear_attention(rng):
     return c
 
 
+def trapezoid_steps(dt, sig):
+    """s_u by the table in the module docstring. ``dt``, ``sig``: [B, H, T]
+    (sig in {0, 1})."""
+    s = np.zeros_like(dt, dtype=np.float64)
+    t = dt.shape[-1]
+    for u in range(t):
+        if u == t - 1:
+            s[..., u] = dt[..., u] * sig[..., u]
+            continue
+        here, nxt = sig[..., u], sig[..., u + 1]
+        table = {
+            (1, 1): dt[..., u],
+            (1, 0): dt[..., u] + dt[..., u + 1],
+            (0, 1): np.zeros_like(dt[..., u]),
+            (0, 0): dt[..., u + 1],
+        }
+        for (a, b), val in table.items():
+            pick = (here == a) & (nxt == b)
+            s[..., u] = np.where(pick, val, s[..., u])
+    return s
+
+
+def halo_case(rng, b, t, h, trap_sign, decay):
+    """A trapezoid-step case (see the module docstring): ``trap_sign`` "neg"
+    (all -40) or "mixed" (+-40 at random), ``decay`` a constant adt."""
+    c = inputs(rng, b, t, h, 32, 32, 8)
+    decay = float(np.float32(decay))  # the float32 value the kernels read
+    c["angles"][:] = 0.0
+    c["adt"][:] = decay
+    if trap_sign == "neg":
+        sig = np.zeros((b, h, t))
+    else:
+        sig = (rng.random((b, h, t)) < 0.5).astype(np.float64)
+    c["trap"] = np.where(sig == 1, 40.0, -40.0).astype(np.float32)
+    dt = c["dt"].astype(np.float64)
+    s = trapezoid_steps(dt, sig)
+    q = c["q"].astype(np.float64)[:, :, 0]
+    k = c["k"].astype(np.float64)[:, :, 0]
+    qt = q[:, :, None] + c["qb"].astype(np.float64)[None, None]  # [B, T, H, N]
+    kt = k[:, :, None] + c["kb"].astype(np.float64)[None, None]
+    scores = np.einsum("bthn,buhn->bhtu", qt, kt)
+    steps = np.arange(t)
+    gap = (steps[:, None] - steps[None, :]).astype(np.float64)  # t - u
+    weight = np.where(gap > 0, np.exp(decay * gap), 0.0)  # sum_{m=u+1..t} adt_m = decay (t - u)
+    w = scores * weight[None, None] * s[:, :, None, :]
+    acc = np.einsum("bhtu,buhp->bthp", w, c["v"].astype(np.float64))
+    skip = np.einsum("bhtt->bht", scores) * dt * sig
+    acc += (c["d"].astype(np.float64)[None, :, None] + skip).transpose(0, 2, 1)[..., None] * c["v"].astype(np.float64)
+    c["expected"] = silu(c["z"].astype(np.float64)) * acc
+    return c
+
+
 def main():
     rng = np.random.default_rng(20240611)
     cases = {"single_step": single_step(rng), "linear_attention": linear_attention(rng)}
+    cases["shift"] = halo_case(rng, 1, 96, 2, "neg", 0.0)
+    cases["mixed_trap"] = halo_case(rng, 1, 96, 2, "mixed", 0.0)
+    cases["segmented"] = halo_case(rng, 1, 300, 1, "mixed", -0.02)
     flat = {f"{name}/{key}": val for name, c in cases.items() for key, val in c.items()}
     np.savez_compressed(OUT, **flat)
     print(f"wrote {OUT} ({OUT.stat().st_size} bytes)")

@@ -193,6 +193,13 @@ def test_empty_inputs():
         assert y.shape == args[2].shape
 
 
-def test_auto_selects_mfma_for_clip_shape():
-    args = to_dev(clip_inputs(2, 64, seed=1))
-    assert selected_variant(*args) in ("mfma", "generic")
+@pytest.mark.parametrize(
+    "b,t,h,n,r",
+    [(16, 400, 16, 64, 16), (16, 101, 32, 128, 32), (1, 7200, 16, 64, 16), (2, 64, 16, 64, 16)],
+)
+def test_auto_selects_mfma(b, t, h, n, r):
+    """The clip workload, the model's bidirectional shape (N = 128) and the long
+    clip must take the matrix-core kernel: the generic one is ~70x slower."""
+    args = to_dev(clip_inputs(b, t, heads=h, head_dim=64, state=n, rotary=r, seed=1))
+    assert selected_variant(*args) == "mfma"
+    assert selected_variant(*args, reverse=True) == "mfma"

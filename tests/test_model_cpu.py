@@ -72,3 +72,26 @@ def test_padded_stem_weight():
     assert w.shape[1] % STEM_ALIGN == 0 and w.shape[1] >= c.stem_kernel
     assert torch.equal(w[:, : c.stem_kernel], enc.stem.weight.reshape(c.dim, c.stem_kernel))
     assert not w[:, c.stem_kernel :].any() and enc._stem_weight() is w
+
+
+def test_weight_caches_under_inference_mode():
+    """A model built and cast inside torch.inference_mode() holds inference
+    tensors, which have no version counter; the derived-weight caches (padded
+    projection, padded FFN, stem GEMM weight, packed convolutions) still build
+    and hit."""
+    from trifusion_amd.trifusion import CNNStage
+
+    with torch.inference_mode():
+        torch.manual_seed(2)
+        enc = Encoder(ModelConfig(depth=1)).eval().to(torch.bfloat16)
+        blk = enc.blocks[0]
+        assert blk.mamba.in_proj.weight.is_inference()
+        wp = blk.mamba._padded_in_proj()
+        assert wp.shape[0] % PROJ_ALIGN == 0 and blk.mamba._padded_in_proj() is wp
+        ffn = blk._padded_ffn()
+        assert blk._padded_ffn() is ffn
+        stem = enc._stem_weight()
+        assert enc._stem_weight() is stem
+        stage = CNNStage(8, 16, 2).to(torch.bfloat16)
+        packed = stage.packed()
+        assert stage.packed() is packed

@@ -28,6 +28,15 @@ from .kernels.native import rms_pair
 from .kernels.buffers import mamba_controls
 from .mamba_fused import fused_mamba
 
+
+def weight_key(t):
+    """Identity of a weight's current contents for the derived-weight caches:
+    its address, version counter, dtype and device. Inference tensors (a model
+    loaded or cast under ``torch.inference_mode()``) have no version counter;
+    they take -1, and a changed inference tensor is a new tensor at a new
+    address."""
+    return (t.data_ptr(), -1 if t.is_inference() else t._version, t.dtype, t.device)
+
 # Output width the in-projection GEMM runs at: rows of zeros pad the weight to
 # a multiple of this (2240 -> 2304 at dim 512); the extra columns of the
 # projection are never read, the splits are views of its first 2240 columns.
@@ -72,7 +81,7 @@ class Mamba3Inference(nn.Module):
         padded = -(-rows // PROJ_ALIGN) * PROJ_ALIGN
         if padded == rows:
             return w
-        key = (w.data_ptr(), w._version, w.dtype, w.device)
+        key = weight_key(w)
         if self._padded_key != key:
             with torch.no_grad():
                 wp = w.new_zeros(padded, w.shape[1])

@@ -30,7 +30,7 @@ from torch import nn
 
 from .kernels import RMSNorm, swiglu
 from .kernels.native import add, add_rms, mask_rms, mean_norm
-from .mamba import Mamba3Inference
+from .mamba import Mamba3Inference, weight_key
 from .masking import masked_mean
 from .stem import frame_audio, frames_mask, small_linear
 
@@ -80,7 +80,7 @@ class EncoderBlock(nn.Module):
         of down, so the result is the same up to the GEMMs' summation order.
         Rebuilt when either weight changes."""
         w1, w2 = self.gate_up.weight, self.down.weight
-        key = (w1.data_ptr(), w1._version, w2.data_ptr(), w2._version, w1.dtype, w1.device)
+        key = (weight_key(w1), weight_key(w2))
         if self._padded_key != key:
             f, d = self.down.in_features, self.down.out_features
             fp = -(-f // FFN_ALIGN) * FFN_ALIGN
@@ -132,7 +132,7 @@ class Encoder(nn.Module):
         runs K = 448 faster than K = 400); rebuilt when the weight changes."""
         cfg = self.config
         w = self.stem.weight
-        key = (w.data_ptr(), w._version, w.dtype, w.device)
+        key = weight_key(w)
         if self._stem_key != key:
             width = -(-cfg.stem_kernel // STEM_ALIGN) * STEM_ALIGN
             with torch.no_grad():

@@ -88,6 +88,19 @@ def clip_lengths(batch, time, low, seed=2, device="cpu"):
     return torch.randint(low, time + 1, (batch,), generator=g).to(device)
 
 
+def channel_fold_lengths(clips, time, low, seed=2, device="cpu"):
+    """Valid lengths of a batch that folds each clip's channels into the batch:
+    rows ``2i`` and ``2i + 1`` are clip ``i``'s two channel slots. Clip lengths
+    ~ U{low..time} and channel counts ~ U{1, 2}; a mono clip's second slot has
+    length 0 (fully masked, as the model masks it). Returns ``(lengths [2*clips],
+    channels [clips])``."""
+    g = _gen(seed)
+    clip_len = torch.randint(low, time + 1, (clips,), generator=g)
+    channels = torch.randint(1, 3, (clips,), generator=g)
+    lengths = torch.stack((clip_len, torch.where(channels == 2, clip_len, torch.zeros_like(clip_len))), 1)
+    return lengths.reshape(-1).to(device), channels.to(device)
+
+
 def algorithmic_bytes(args, out_dtype=None, lengths=None):
     """Unique input bytes plus output bytes of one ``fused_mamba`` call.
 

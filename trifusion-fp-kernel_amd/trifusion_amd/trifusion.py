@@ -57,7 +57,7 @@ from .kernels.block import (
 )
 from .kernels.buffers import mask_buffer
 from .kernels.native import add, add_rms, mean_norm
-from .mamba import Mamba3Inference
+from .mamba import Mamba3Inference, weight_key
 from .masking import masked_mean, time_mask
 
 
@@ -169,7 +169,7 @@ class CNNStage(nn.Module):
         """bf16 weights in the fused kernels' layout: conv1 and conv2 tap-major
         ``[9, cout, cin]``, the skip ``[cout, cin]``; rebuilt when a weight changes."""
         ws = (self.conv1.weight, self.conv2.weight, self.skip.weight)
-        key = tuple((w.data_ptr(), w._version, w.device) for w in ws)
+        key = tuple(weight_key(w) for w in ws)
         if self._packed_key != key:
             with torch.no_grad():
                 skip = ws[2].detach().flatten(1).to(torch.bfloat16).contiguous()
@@ -350,9 +350,7 @@ class TriFusionBlock(nn.Module):
     def _joined(self, name, parts, build):
         """Weights of two layers that read the same input, joined for one GEMM;
         rebuilt when any part changes."""
-        # inference tensors (caches built under inference mode) have no version
-        # counter; they are rebuilt, at a new address, when their source changes
-        key = tuple((t.data_ptr(), -1 if t.is_inference() else t._version, t.dtype, t.device) for t in parts)
+        key = tuple(weight_key(t) for t in parts)
         hit = self._fused_weights.get(name)
         if hit is None or hit[0] != key:
             with torch.no_grad():
