@@ -35,6 +35,7 @@ typedef enum tf_status {
   TF_ERR_STRIDE = 4,      /* layout the selected kernel cannot read */
   TF_ERR_VARIANT = 5,     /* requested kernel variant cannot run these arguments */
   TF_ERR_LAUNCH = 6,      /* the HIP runtime rejected the launch */
+  TF_ERR_WORKSPACE = 7,   /* needs more scratch than tf_fused_mamba_static holds */
 } tf_status;
 
 /* Kernel selection for tf_fused_mamba. */
@@ -120,6 +121,25 @@ int64_t tf_fused_mamba_workspace_size(const tf_mamba_args *args);
 /* Which kernel TF_MAMBA_AUTO would run for these arguments (1 or 2), or a
  * negative tf_status if no kernel can run them. */
 int tf_fused_mamba_variant(const tf_mamba_args *args);
+
+/*
+ * tf_fused_mamba without a caller workspace, for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). No counterpart in the reference. args->workspace is ignored: the
+ * chunk-parallel form takes its scratch from a library-owned device array of
+ * tf_fused_mamba_static_scratch_bytes() (16 MiB) that every device holds until
+ * the process ends. Arguments whose tf_fused_mamba_workspace_size exceeds it
+ * return TF_ERR_WORKSPACE and launch nothing. Calls allocate nothing; the
+ * first call on a device looks up that device's copy of the array. Every call
+ * on one device shares that device's array, and the kernels rewrite all of the
+ * scratch they read within the call (nothing needs to start at zero), so calls
+ * that overlap on one device (different streams, no ordering) race: serialise
+ * them. Outputs equal tf_fused_mamba's for the same arguments.
+ */
+int tf_fused_mamba_static(const tf_mamba_args *args, void *stream);
+
+/* Size in bytes of the scratch array tf_fused_mamba_static uses. */
+int64_t tf_fused_mamba_static_scratch_bytes(void);
 
 /*
  * Row RMSNorm: y[r,:] = x[r,:] * rsqrt(mean(x[r,:]^2) + eps) * w, fp32

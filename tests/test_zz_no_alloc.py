@@ -1,0 +1,88 @@
+"""tf_fused_mamba_static (the entry point that allocates nothing) against
+tf_fused_mamba with a caller workspace, through the C ABI (MI355X).
+
+Two calls in a row on the library's static scratch, the second smaller, each
+compared bit for bit with tf_fused_mamba on a torch-allocated workspace (both
+run the same kernels with the same segment plan). Also a shape that needs no
+scratch, and one whose scratch exceeds the static array, which must be
+rejected with TF_ERR_WORKSPACE before anything is launched.
+"""
+
+import ctypes
+
+import pytest
+import torch
+
+from trifusion_amd import _lib
+from trifusion_amd.mamba_fused import build_args
+from trifusion_amd.synthetic import clip_inputs
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+TF_ERR_WORKSPACE = 7
+
+
+def call(entry, dargs, lengths=None, reverse=False):
+    lib = _lib.load()
+    v = dargs[2]
+    out = torch.full(v.shape, float("nan"), device=DEV, dtype=torch.float32)
+    args = build_args(*dargs, out, lengths, "auto", reverse, None, 1e-4)
+    workspace = None
+    if entry == "tf_fused_mamba":
+        need = lib.tf_fused_mamba_workspace_size(ctypes.byref(args))
+        assert need >= 0
+        if need:
+            workspace = torch.empty(need, dtype=torch.uint8, device=DEV)
+            args.workspace, args.workspace_bytes = workspace.data_ptr(), need
+    rc = getattr(lib, entry)(ctypes.byref(args), _lib.stream_of(v))
+    torch.cuda.synchronize()
+    return rc, out
+
+
+def test_static_scratch_matches_workspace_entry():
+    lib = _lib.load()
+    limit = lib.tf_fused_mamba_static_scratch_bytes()
+    assert limit == 16 << 20
+    cases = [
+        ("long_b1_l7200_h16", clip_inputs(1, 7200, seed=21), None, False),
+        ("smaller_b1_l3000_h8_reverse", clip_inputs(1, 3000, heads=8, seed=22), torch.tensor([2900]), True),
+        ("serial_b4_l200_h16", clip_inputs(4, 200, seed=23), None, False),
+    ]
+    for name, args, lengths, reverse in cases:
+        print(f"case {name}", flush=True)
+        dargs = tuple(a.to(DEV) for a in args)
+        dl = None if lengths is None else lengths.to(DEV)
+        probe = build_args(*dargs, torch.empty(dargs[2].shape, device=DEV), dl, "auto", reverse, None, 1e-4)
+        need = lib.tf_fused_mamba_workspace_size(ctypes.byref(probe))
+        assert 0 <= need <= limit
+        assert (need > 0) == (name != "serial_b4_l200_h16")
+        rc_ref, ref = call("tf_fused_mamba", dargs, dl, reverse)
+        rc, got = call("tf_fused_mamba_static", dargs, dl, reverse)
+        assert rc_ref == 0 and rc == 0
+        assert torch.isfinite(got).all()
+        assert torch.equal(got, ref), f"{name}: max diff {(got - ref).abs().max().item():.3e}"
+
+
+def test_static_scratch_rejects_oversized_plans():
+    lib = _lib.load()
+    b, t, h, n, p, r = 1, 16384, 128, 64, 64, 16
+    bf = dict(device=DEV, dtype=torch.bfloat16)
+    f32 = dict(device=DEV, dtype=torch.float32)
+    q = torch.zeros(b, t, 1, n, **bf)
+    k = torch.zeros(b, t, 1, n, **bf)
+    v = torch.zeros(b, t, h, p, **bf)
+    z = torch.zeros(b, t, h, p, **bf)
+    ctl = [torch.zeros(b, h, t, **f32) for _ in range(3)]
+    angles = torch.zeros(b, t, h, r, **f32)
+    qb, kb, d = torch.zeros(h, n, **f32), torch.zeros(h, n, **f32), torch.ones(h, **f32)
+    out = torch.full((b, t, h, p), -1.0, **f32)
+    args = build_args(q, k, v, *ctl, qb, kb, angles, d, z, out, None, "auto", False, None, 1e-4)
+    need = lib.tf_fused_mamba_workspace_size(ctypes.byref(args))
+    assert need > lib.tf_fused_mamba_static_scratch_bytes()
+    rc = lib.tf_fused_mamba_static(ctypes.byref(args), _lib.stream_of(v))
+    torch.cuda.synchronize()
+    assert rc == TF_ERR_WORKSPACE
+    assert torch.all(out == -1.0), "a rejected call must launch nothing"
+    with pytest.raises(ValueError, match="static area"):
+        _lib.check(rc, "fused_mamba")

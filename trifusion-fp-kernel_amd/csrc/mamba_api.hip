@@ -3,10 +3,40 @@
 // (src/trifusion_l4/mamba_fused.py:155-161), generalised to the shapes the
 // kernels here support; the Python wrapper maps the status codes to
 // ValueError/TypeError/RuntimeError before anything is launched.
+#include <mutex>
+
 #include "mamba_internal.h"
 
 namespace tf {
 namespace {
+
+// Library-owned scratch of tf_fused_mamba_static: the chunk-parallel form's
+// segment states, chunk phase sums and segment decays, for callers that cannot
+// allocate. Each device holds its own copy for the life of the process. In
+// host code `scratch` names a host-side stand-in, never the device memory:
+// host code uses only the per-device address that hipGetSymbolAddress returns.
+constexpr int64_t kStaticScratchBytes = int64_t(16) << 20;
+__device__ __align__(256) char scratch[kStaticScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::once_flag g_scratch_once[kMaxDevices];
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// Device address of `scratch` on `device`, looked up once per device with that
+// device current (the previous current device is restored). NULL on failure.
+void* static_scratch(int device) {
+  if (device < 0 || device >= kMaxDevices) return nullptr;
+  std::call_once(g_scratch_once[device], [device] {
+    int prev = -1;
+    hipError_t rc = hipGetDevice(&prev);
+    if (rc == hipSuccess && prev != device) rc = hipSetDevice(device);
+    void* ptr = nullptr;
+    if (rc == hipSuccess) rc = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (prev >= 0 && prev != device) (void)hipSetDevice(prev);
+    g_scratch_ptr[device] = rc == hipSuccess ? ptr : nullptr;
+  });
+  return g_scratch_ptr[device];
+}
 
 bool empty(const tf_mamba_args* a) { return a->batch == 0 || a->time == 0; }
 
@@ -59,5 +89,30 @@ extern "C" int64_t tf_fused_mamba_workspace_size(const tf_mamba_args* a) {
   if (tf::empty(a) || which != TF_MAMBA_MFMA) return 0;
   return tf::mfma_workspace_bytes(*a);
 }
+
+extern "C" int tf_fused_mamba_static(const tf_mamba_args* a, void* stream) {
+  const int which = tf::select(a);
+  if (which < 0) return -which;
+  if (tf::empty(a)) return TF_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (which != TF_MAMBA_MFMA) return tf::launch_generic(*a, s);
+  const int64_t need = tf::mfma_workspace_bytes(*a);
+  tf_mamba_args local = *a;
+  local.workspace = nullptr;
+  local.workspace_bytes = 0;
+  if (need > 0) {
+    if (need > tf::kStaticScratchBytes) return TF_ERR_WORKSPACE;
+    int device = -1;
+    hipError_t rc = s != nullptr ? hipStreamGetDevice(s, &device) : hipGetDevice(&device);
+    if (rc != hipSuccess) return TF_ERR_LAUNCH;
+    void* ptr = tf::static_scratch(device);
+    if (ptr == nullptr) return TF_ERR_LAUNCH;
+    local.workspace = ptr;
+    local.workspace_bytes = tf::kStaticScratchBytes;
+  }
+  return tf::launch_mfma(local, s);
+}
+
+extern "C" int64_t tf_fused_mamba_static_scratch_bytes(void) { return tf::kStaticScratchBytes; }
 
 extern "C" const char* tf_version(void) { return "trifusion_amd 0.1.0 (gfx950)"; }

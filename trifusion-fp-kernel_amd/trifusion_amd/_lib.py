@@ -28,6 +28,7 @@ STATUS = {
     4: "unsupported layout (strides)",
     5: "requested kernel variant cannot run these arguments",
     6: "the HIP runtime rejected the kernel launch",
+    7: "needs more scratch than the library's static area holds",
 }
 
 VARIANTS = {"auto": 0, "generic": 1, "mfma": 2}
@@ -76,6 +77,8 @@ _SIGNATURES = {
     "tf_fused_mamba": ([ctypes.POINTER(MambaArgs), c_ptr], c_i32),
     "tf_fused_mamba_variant": ([ctypes.POINTER(MambaArgs)], c_i32),
     "tf_fused_mamba_workspace_size": ([ctypes.POINTER(MambaArgs)], c_i64),
+    "tf_fused_mamba_static": ([ctypes.POINTER(MambaArgs), c_ptr], c_i32),
+    "tf_fused_mamba_static_scratch_bytes": ([], c_i64),
     "tf_rmsnorm": ([c_ptr, c_i32, c_i64, c_ptr, c_ptr, c_i32, c_i64, c_i64, c_f32, c_ptr], c_i32),
     "tf_add_rmsnorm": (
         [c_ptr, c_i32, c_ptr, c_i32, c_ptr, c_ptr, c_ptr, c_i32, c_ptr, c_i32, c_i64, c_i64, c_f32, c_ptr],
@@ -175,7 +178,7 @@ def check(status, what):
     if status == 0:
         return
     message = STATUS.get(status, f"status {status}")
-    if status in (2, 4, 5):
+    if status in (2, 4, 5, 7):
         raise ValueError(f"{what}: {message}")
     if status == 3:
         raise TypeError(f"{what}: {message}")
