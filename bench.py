@@ -62,7 +62,7 @@ def parse_args():
     p.add_argument("--trifusion-only", action="store_true",
                    help="only time the full TriFusion-FP model forward at 4 s mono x 16 (profiling aid)")
     p.add_argument("--no-trifusion", action="store_true", help="skip the full TriFusion-FP model timing")
-    p.add_argument("--variant", default="auto", choices=["auto", "mfma", "generic"])
+    p.add_argument("--variant", default="auto", choices=["auto", "pipe", "mfma", "generic"])
     p.add_argument("--workload", default="clip", choices=sorted(WORKLOADS),
                    help="shape to time (clip: the headline B16 L400 workload)")
     p.add_argument("--eager", action="store_true", help="time Python-dispatched calls instead of graph replay")

@@ -40,9 +40,12 @@ typedef enum tf_status {
 
 /* Kernel selection for tf_fused_mamba. */
 typedef enum tf_mamba_variant {
-  TF_MAMBA_AUTO = 0,      /* chunked MFMA kernel when supported, else generic */
+  TF_MAMBA_AUTO = 0,      /* pipelined kernel when supported and the chunked kernel
+                             would not cut the sequence into time segments, else
+                             the chunked kernel when supported, else generic */
   TF_MAMBA_GENERIC = 1,   /* fp32-FMA kernel: any dtype, N <= 128, P <= 64 */
   TF_MAMBA_MFMA = 2,      /* bf16 MFMA chunked-scan kernel (gfx950) */
+  TF_MAMBA_PIPE = 3,      /* bf16 MFMA pipelined serial walk, N = P = 64 (gfx950) */
 } tf_mamba_variant;
 
 /*
@@ -118,7 +121,7 @@ int tf_fused_mamba(const tf_mamba_args *args, void *stream);
  */
 int64_t tf_fused_mamba_workspace_size(const tf_mamba_args *args);
 
-/* Which kernel TF_MAMBA_AUTO would run for these arguments (1 or 2), or a
+/* Which kernel TF_MAMBA_AUTO would run for these arguments (1, 2 or 3), or a
  * negative tf_status if no kernel can run them. */
 int tf_fused_mamba_variant(const tf_mamba_args *args);
 

@@ -39,10 +39,12 @@ where t + 1 belongs, changes the answer:
   adt = -0.02. With a single (batch, head) unit the MFMA kernel cuts the
   sequence into segments (a boundary at t = 256), so the step at the end of a
   segment reads its halo from the next segment.
+* ``mixed_trap_n64`` (T = 100, N = P = 64, R = 16): mixed trap and a constant
+  decay adt = -0.05 at the state and head dims the pipelined kernel takes.
 
 q, k, v and z are rounded to bf16 values (stored as float32), so bf16 kernels
-read them exactly. Shapes use N = P = 32, R = 8, Hq = 1, which every kernel
-variant takes. Run from the repository root: ``python tests/golden/make_golden.py``.
+read them exactly. Shapes use N = P = 32, R = 8, Hq = 1 (the generic and chunked
+kernels), and N = P = 64, R = 16 for the last case (every kernel). Run from the repository root: ``python tests/golden/make_golden.py``.
 """
 
 from pathlib import Path
@@ -134,10 +136,11 @@ def trapezoid_steps(dt, sig):
     return s
 
 
-def halo_case(rng, b, t, h, trap_sign, decay):
+def halo_case(rng, b, t, h, trap_sign, decay, n=32, r=8):
     """A trapezoid-step case (see the module docstring): ``trap_sign`` "neg"
-    (all -40) or "mixed" (+-40 at random), ``decay`` a constant adt."""
-    c = inputs(rng, b, t, h, 32, 32, 8)
+    (all -40) or "mixed" (+-40 at random), ``decay`` a constant adt; state and
+    head dim ``n``."""
+    c = inputs(rng, b, t, h, n, n, r)
     decay = float(np.float32(decay))  # the float32 value the kernels read
     c["angles"][:] = 0.0
     c["adt"][:] = decay
@@ -170,6 +173,7 @@ def main():
     cases["shift"] = halo_case(rng, 1, 96, 2, "neg", 0.0)
     cases["mixed_trap"] = halo_case(rng, 1, 96, 2, "mixed", 0.0)
     cases["segmented"] = halo_case(rng, 1, 300, 1, "mixed", -0.02)
+    cases["mixed_trap_n64"] = halo_case(rng, 1, 100, 1, "mixed", -0.05, n=64, r=16)
     flat = {f"{name}/{key}": val for name, c in cases.items() for key, val in c.items()}
     np.savez_compressed(OUT, **flat)
     print(f"wrote {OUT} ({OUT.stat().st_size} bytes)")

@@ -12,7 +12,7 @@ from oracle import recurrence as R
 
 KAT = Path(__file__).parent / "golden" / "recurrence_kat.npz"
 ORDER = ("q", "k", "v", "adt", "dt", "trap", "qb", "kb", "angles", "d", "z")
-CASES = ["single_step", "linear_attention", "shift", "mixed_trap", "segmented"]
+CASES = ["single_step", "linear_attention", "shift", "mixed_trap", "segmented", "mixed_trap_n64"]
 
 
 def load_case(name):
@@ -41,7 +41,7 @@ def test_oracle_matches_known_answers(name):
     assert R.rel_fro(R.fused_mamba_chunked(*bf, out_dtype=torch.float32), expected) < 0.012
 
 
-HALO_CASES = ["shift", "mixed_trap", "segmented"]
+HALO_CASES = ["shift", "mixed_trap", "segmented", "mixed_trap_n64"]
 
 
 def _sig(trap):

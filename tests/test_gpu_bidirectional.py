@@ -32,7 +32,7 @@ pytestmark = pytest.mark.gpu
 
 DEV = "cuda"
 MAX_REL = 1e-3
-VARIANTS = ["generic", "mfma"]
+VARIANTS = ["generic", "mfma", "pipe"]
 
 
 def to_dev(args):

@@ -54,7 +54,7 @@ def check(y, ref, lengths):
 
 
 @pytest.mark.parametrize("reverse", [False, True])
-@pytest.mark.parametrize("variant", ["generic", "mfma"])
+@pytest.mark.parametrize("variant", ["generic", "mfma", "pipe"])
 def test_channel_fold_batch(variant, reverse):
     lengths, channels = channel_fold_lengths(16, 400, 50, seed=12)
     assert (lengths == 0).any() and (channels == 2).any()
@@ -69,7 +69,7 @@ def test_channel_fold_batch(variant, reverse):
 
 
 @pytest.mark.parametrize("reverse", [False, True])
-@pytest.mark.parametrize("variant", ["generic", "mfma"])
+@pytest.mark.parametrize("variant", ["generic", "mfma", "pipe"])
 def test_lengths_zero_and_one(variant, reverse):
     lengths = torch.tensor([0, 1, 130, 0, 1, 64, 65, 130])
     args = clip_inputs(8, 130, heads=4, head_dim=64, state=64, seed=14)

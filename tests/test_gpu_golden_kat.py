@@ -29,8 +29,8 @@ TIME_AXIS = {0: 1, 1: 1, 2: 1, 3: 2, 4: 2, 5: 2, 8: 1, 10: 1}  # operand index -
 
 
 @pytest.mark.parametrize("reverse", [False, True])
-@pytest.mark.parametrize("variant", ["generic", "mfma"])
-@pytest.mark.parametrize("name", ["single_step", "linear_attention", "shift", "mixed_trap", "segmented"])
+@pytest.mark.parametrize("variant", ["generic", "mfma", "pipe"])
+@pytest.mark.parametrize("name", ["single_step", "linear_attention", "shift", "mixed_trap", "segmented", "mixed_trap_n64"])
 def test_known_answers(name, variant, reverse):
     args, expected = load_case(name)
     if reverse:

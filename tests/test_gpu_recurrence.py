@@ -19,7 +19,7 @@ from trifusion_amd.synthetic import clip_inputs, clip_lengths, reference_test_in
 pytestmark = pytest.mark.gpu
 
 DEV = "cuda"
-VARIANTS = ["generic", "mfma"]
+VARIANTS = ["generic", "mfma", "pipe"]
 MAX_REL = 1e-3
 
 
@@ -194,12 +194,18 @@ def test_empty_inputs():
 
 
 @pytest.mark.parametrize(
-    "b,t,h,n,r",
-    [(16, 400, 16, 64, 16), (16, 101, 32, 128, 32), (1, 7200, 16, 64, 16), (2, 64, 16, 64, 16)],
+    "b,t,h,n,r,kernel",
+    [
+        (16, 400, 16, 64, 16, "pipe"),  # clip workload: pipelined walk
+        (16, 101, 32, 128, 32, "mfma"),  # the model's bidirectional shape (N = 128)
+        (1, 7200, 16, 64, 16, "mfma"),  # long clip: chunked kernel, cut into time segments
+        (2, 64, 16, 64, 16, "pipe"),
+    ],
 )
-def test_auto_selects_mfma(b, t, h, n, r):
-    """The clip workload, the model's bidirectional shape (N = 128) and the long
-    clip must take the matrix-core kernel: the generic one is ~70x slower."""
+def test_auto_selects_matrix_core_kernel(b, t, h, n, r, kernel):
+    """The clip workload, the model's bidirectional shape and the long clip must
+    take a matrix-core kernel (the generic one is ~70x slower), and the one
+    meant for the shape."""
     args = to_dev(clip_inputs(b, t, heads=h, head_dim=64, state=n, rotary=r, seed=1))
-    assert selected_variant(*args) == "mfma"
-    assert selected_variant(*args, reverse=True) == "mfma"
+    assert selected_variant(*args) == kernel
+    assert selected_variant(*args, reverse=True) == kernel

@@ -51,7 +51,7 @@ int validate(const tf_mamba_args* a) {
   if (a->state < 2 || a->state % 2 || a->head_dim < 1) return TF_ERR_SHAPE;
   if (a->rotary < 0 || a->rotary > a->state / 2) return TF_ERR_SHAPE;
   if (a->batch > 65535 || a->heads > 65535 || a->time > (int64_t(1) << 30)) return TF_ERR_SHAPE;
-  if (a->variant < TF_MAMBA_AUTO || a->variant > TF_MAMBA_MFMA) return TF_ERR_VARIANT;
+  if (a->variant < TF_MAMBA_AUTO || a->variant > TF_MAMBA_PIPE) return TF_ERR_VARIANT;
   if (a->reverse != 0 && a->reverse != 1) return TF_ERR_SHAPE;
   // empty tensors may carry NULL data pointers
   if (!empty(a) && (!a->q || !a->k || !a->v || !a->adt || !a->dt || !a->trap || !a->angles ||
@@ -63,8 +63,12 @@ int validate(const tf_mamba_args* a) {
 int select(const tf_mamba_args* a) {
   const int rc = validate(a);
   if (rc != TF_OK) return -rc;
+  if (a->variant == TF_MAMBA_PIPE) return pipe_supported(*a) ? TF_MAMBA_PIPE : -TF_ERR_VARIANT;
   if (a->variant == TF_MAMBA_MFMA) return mfma_supported(*a) ? TF_MAMBA_MFMA : -TF_ERR_VARIANT;
   if (a->variant == TF_MAMBA_GENERIC) return generic_supported(*a) ? TF_MAMBA_GENERIC : -TF_ERR_SHAPE;
+  // the pipelined walk, unless the chunked kernel would cut few long units
+  // into time segments (its chunk-parallel form)
+  if (pipe_supported(*a) && mfma_workspace_bytes(*a) == 0) return TF_MAMBA_PIPE;
   if (mfma_supported(*a)) return TF_MAMBA_MFMA;
   if (generic_supported(*a)) return TF_MAMBA_GENERIC;
   return -TF_ERR_SHAPE;
@@ -80,6 +84,7 @@ extern "C" int tf_fused_mamba(const tf_mamba_args* a, void* stream) {
   if (which < 0) return -which;
   if (tf::empty(a)) return TF_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (which == TF_MAMBA_PIPE) return tf::launch_pipe(*a, s);
   return which == TF_MAMBA_MFMA ? tf::launch_mfma(*a, s) : tf::launch_generic(*a, s);
 }
 
@@ -95,6 +100,7 @@ extern "C" int tf_fused_mamba_static(const tf_mamba_args* a, void* stream) {
   if (which < 0) return -which;
   if (tf::empty(a)) return TF_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (which == TF_MAMBA_PIPE) return tf::launch_pipe(*a, s);
   if (which != TF_MAMBA_MFMA) return tf::launch_generic(*a, s);
   const int64_t need = tf::mfma_workspace_bytes(*a);
   tf_mamba_args local = *a;

@@ -24,4 +24,8 @@ int launch_mfma(const tf_mamba_args& a, hipStream_t stream);
 // (0: one workgroup per unit).
 int64_t mfma_workspace_bytes(const tf_mamba_args& a);
 
+// Pipelined serial-walk MFMA kernel (N = P = 64).
+bool pipe_supported(const tf_mamba_args& a);
+int launch_pipe(const tf_mamba_args& a, hipStream_t stream);
+
 }  // namespace tf

@@ -36,182 +36,11 @@
 // D values index X's rows i = drow(e, hh). Contraction indices are permuted the
 // same way on both sides, slot j of k-step s holding k = kidx(s, hh, j), which
 // makes the D values of one product directly usable as the K slots of the next
-// product's operand.
-#include "mamba_internal.h"
+// product's operand (mfma_tile.h).
+#include "mfma_tile.h"
 
 namespace tf {
 namespace {
-
-typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
-typedef __attribute__((ext_vector_type(16))) float f32x16;
-typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
-typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
-
-__device__ __forceinline__ f32x16 mfma(const u32x4& x, const u32x4& y, const f32x16& acc) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, x), __builtin_bit_cast(bf16x8, y),
-                                                 acc, 0, 0, 0);
-}
-
-__device__ __forceinline__ f32x16 zero16() {
-  f32x16 z;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) z[i] = 0.f;
-  return z;
-}
-
-// Row (within a 32-row tile) held in D element e by lane half hh.
-__device__ __forceinline__ int drow(int e, int hh) { return 8 * (e >> 2) + 4 * hh + (e & 3); }
-
-// Contraction index held in slot j of k-step s (16 indices per step) by lane half hh.
-__device__ __forceinline__ int kidx(int s, int hh, int j) {
-  return 32 * (s >> 1) + 16 * (s & 1) + 8 * (j >> 2) + 4 * hh + (j & 3);
-}
-
-typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
-
-// Two fp32 -> packed bf16 pair, round to nearest even (v_cvt_pk_bf16_f32).
-__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  const bf16x2 v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
-  return __builtin_bit_cast(uint32_t, v);
-}
-__device__ __forceinline__ float lo_f(uint32_t w) { return __uint_as_float(w << 16); }
-__device__ __forceinline__ float hi_f(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
-__device__ __forceinline__ float slot_f(const u32x4& x, int j) {
-  const uint32_t w = x[j >> 1];
-  return (j & 1) ? hi_f(w) : lo_f(w);
-}
-
-// Inclusive prefix sum over each 32-lane half of the wave.
-template <typename F>
-__device__ __forceinline__ F half_scan(F v, int c32) {
-#pragma unroll
-  for (int off = 1; off < 32; off <<= 1) {
-    const F o = __shfl_up(v, off, 32);
-    if (c32 >= off) v += o;
-  }
-  return v;
-}
-
-template <typename F>
-__device__ __forceinline__ F half_last(F v) {
-  return __shfl(v, 31, 32);
-}
-
-// Orders this wave's LDS accesses: earlier writes before later reads of other
-// lanes' data, earlier reads before later writes to the same cells.
-__device__ __forceinline__ void wave_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// Workgroup barrier ordering LDS accesses only. Waves exchange data through LDS
-// alone, so global loads in flight (the next super-chunk's inputs) stay
-// outstanding across it instead of being drained as a full fence would.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
-__device__ __forceinline__ float sigmoid_fast(float x) {
-  return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-x * kLog2e));
-}
-
-// Identity operand for a 32-wide tile: slot j of k-step parity sp is 1.0 where
-// kidx(sp, hh, j) == c32.
-__device__ __forceinline__ u32x4 identity_rows(int sp, int hh, int c32) {
-  u32x4 r;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int j = 2 * q;
-    const uint32_t lo = (16 * sp + 8 * (j >> 2) + 4 * hh + (j & 3)) == c32 ? 0x3f80u : 0u;
-    const uint32_t hi = (16 * sp + 8 * ((j + 1) >> 2) + 4 * hh + ((j + 1) & 3)) == c32 ? 0x3f80u : 0u;
-    r[q] = lo | (hi << 16);
-  }
-  return r;
-}
-
-// Elements k0..k0+3 and k0+8..k0+11 of one bf16 row (two 8-byte loads).
-__device__ __forceinline__ u32x4 load_row8(const uint16_t* row, int k0) {
-  const u32x2 x = *reinterpret_cast<const u32x2*>(row + k0);
-  const u32x2 y = *reinterpret_cast<const u32x2*>(row + k0 + 8);
-  u32x4 r;
-  r[0] = x[0];
-  r[1] = x[1];
-  r[2] = y[0];
-  r[3] = y[1];
-  return r;
-}
-
-__device__ __forceinline__ u32x4 as_u4(const float4& f) { return __builtin_bit_cast(u32x4, f); }
-__device__ __forceinline__ float4 as_f4(const u32x4& u) { return __builtin_bit_cast(float4, u); }
-
-// tanh for |x| < 0.625 by the odd polynomial of the Cephes single-precision
-// tanhf (S. L. Moshier, Cephes Math Library), else 1 - 2/(exp(2|x|) + 1) with the
-// hardware exp2/rcp, evaluated only when some lane of the wave needs it. (The
-// exp form alone is biased by ~1e-7 near 0, which the phase cumsum carries
-// into a visible error after a few thousand steps.)
-__device__ __forceinline__ float tanh_fast(float x) {
-  const float ax = fabsf(x);
-  const float z = x * x;
-  float r = ((((-5.70498872745e-3f * z + 2.06390887954e-2f) * z - 5.37397155531e-2f) * z + 1.33314422036e-1f) * z -
-             3.33332819422e-1f) * z * ax + ax;
-  if (__any(ax >= 0.625f)) {
-    const float e = __builtin_amdgcn_exp2f(2.f * kLog2e * fminf(ax, 40.f));
-    const float big = 1.f - 2.f * __builtin_amdgcn_rcpf(e + 1.f);
-    r = ax < 0.625f ? r : big;
-  }
-  return copysignf(r, x);
-}
-
-// Kernel-side operand block: per-tensor element strides as int32 (the host
-// checks every offset fits) so addressing stays in few registers.
-struct MfmaParams {
-  const uint16_t* q;
-  const uint16_t* k;
-  const uint16_t* v;
-  const uint16_t* z;
-  const void* adt;  // adt and dt, or the raw a and ddt columns (ctl_raw)
-  const void* dt;
-  const void* trap;
-  const void* angles;
-  const float* qb;
-  const float* kb;
-  const float* d;
-  void* out;
-  const int64_t* lengths;
-  int q_sb, q_st, q_sh;
-  int k_sb, k_st, k_sh;
-  int v_sb, v_st, v_sh;
-  int z_sb, z_st, z_sh;
-  int o_sb, o_st, o_sh;
-  int g_sb, g_st, g_sh, g_sr;
-  int a_sb, a_sh, a_st;
-  int d_sb, d_sh, d_st;
-  int r_sb, r_sh, r_st;
-  int T, H, group, R, xcd_per;
-  int out_f32, trap_bf16, angles_dtype;
-  // Raw controls: adt/dt hold the in-projection's a/ddt columns (bf16 when
-  // ctl_bf16), turned into the step and decay in the prologue.
-  int ctl_raw, ctl_bf16;
-  float a_floor;
-  const float* dt_bias;
-  // Reverse: step t < L of a unit reads and writes row L-1-t. The host negates
-  // every time stride; the kernel moves each unit's bases to row L-1.
-  int rev;
-  // Chunk-parallel form: the time axis of each of the `units` (batch, head)
-  // units is cut into G segments of SC chunks, one workgroup per (segment,
-  // unit). Scratch: per (unit, chunk) the phase sum per pair ([NC][64] fp64,
-  // from the phase pre-pass); per record rec = unit * G + segment the state
-  // ([kF4] float4 in kernel layout: the contribution from zero written by the
-  // summary pass, replaced by the state entering the segment by the segment
-  // scan) and the log2 decay. G = 1: no scratch.
-  float4* seg_state;
-  double* chunk_phase;
-  float* seg_decay;
-  int units, G, SC, NC;
-};
 
 template <int NT, int PT, int CW>
 struct Smem {
@@ -231,27 +60,6 @@ struct Smem {
   float qb[32 * NT];
   float kb[32 * NT];
 };
-
-// Scores^T[u][t] = kr_u . qr_t of one 32x32 tile times the decay
-// 2^min(cs_t - cs_u, 0), strictly causal on a diagonal tile, rounded to bf16 as
-// the Y operand of the score . v product (rows t, K = u; mamba_fused.py:144-146).
-__device__ __forceinline__ void score_tile(const f32x16& acc, float cst, const float* csu_base, bool diag, int c32,
-                                           int hh, u32x4 (&out)[2]) {
-#pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    const float4 csu = *reinterpret_cast<const float4*>(csu_base + 8 * g + 4 * hh);
-    const float cu[4] = {csu.x, csu.y, csu.z, csu.w};
-    float vals[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int e = 4 * g + q;
-      const float x = acc[e] * fast_exp2(fminf(cst - cu[q], 0.f));
-      vals[q] = (!diag || c32 > drow(e, hh)) ? x : 0.f;
-    }
-    out[g >> 1][2 * (g & 1)] = pack2(vals[0], vals[1]);
-    out[g >> 1][2 * (g & 1) + 1] = pack2(vals[2], vals[3]);
-  }
-}
 
 // Global inputs of one wave's 32 rows, in two parts loaded at different
 // times. Rows past L read a valid row; their dt is 0, so they reach neither the
@@ -290,10 +98,6 @@ __device__ __forceinline__ void load_rows(const MfmaParams& P, HalfRows<KS, PS>&
   for (int s = 0; s < PS; ++s) in.v[s] = load_row8(v_row, kidx(s, hh, 0));
 }
 
-// Element i of a control tensor (fp32, or bf16 for raw controls).
-__device__ __forceinline__ float ctl_value(const void* base, int bf16, int i) {
-  return bf16 ? to_f32(static_cast<const bf16_t*>(base)[i]) : static_cast<const float*>(base)[i];
-}
 
 // Loads row t's controls (raw values when P.ctl_raw; converted where used, so
 // the loads stay in flight) and the halo step t + 1 when t + 1 < tlim: T, or
@@ -939,12 +743,16 @@ __global__ __launch_bounds__(256) void chunk_phase_kernel(const MfmaParams P) {
   }
 }
 
+}  // namespace
+
 bool aligned(const void* p, int bytes) { return (reinterpret_cast<uintptr_t>(p) % bytes) == 0; }
 
 bool rows_vectorisable(const void* p, const int64_t* st, int elem_bytes, int vec_bytes) {
   const int64_t m = vec_bytes / elem_bytes;
   return aligned(p, vec_bytes) && st[3] == 1 && st[0] % m == 0 && st[1] % m == 0 && st[2] % m == 0;
 }
+
+namespace {
 
 // Largest element offset reachable through `n` dims of sizes/strides; strides
 // must be non-negative.
@@ -956,6 +764,8 @@ bool fits_int32(const int64_t* sizes, const int64_t* strides, int n) {
   }
   return off < 0x7fffffff - 64;
 }
+
+}  // namespace
 
 bool offsets_fit(const tf_mamba_args& a) {
   const int64_t qs[4] = {a.batch, a.time, a.qk_heads, a.state};
@@ -1018,6 +828,8 @@ MfmaParams make_params(const tf_mamba_args& a) {
   return P;
 }
 
+namespace {
+
 // Chunk-parallel plan: with fewer (batch, head) units than half the CUs, each
 // unit's time axis is cut into G segments of SC chunks (whole super-chunks) so
 // about one workgroup per CU runs. The cost is a phase pre-pass over the
@@ -1038,7 +850,7 @@ SegPlan plan_segments(const tf_mamba_args& a, int cw, int kf4) {
   const int64_t units = a.batch * a.heads;
   const int64_t chunks = (a.time + kChunk - 1) / kChunk;
   p.SC = static_cast<int>(chunks);
-  if (units <= 0 || units > kTargetGroups / 2) return p;
+  if (units <= 0 || chunks <= 0 || units > kTargetGroups / 2) return p;
   int64_t g = kTargetGroups / units;
   int64_t sc = (chunks + g - 1) / g;
   sc = (sc + cw - 1) / cw * cw;

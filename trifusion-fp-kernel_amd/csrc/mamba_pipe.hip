@@ -1,0 +1,607 @@
+// Pipelined fused Mamba-3 SISO recurrence on gfx950 bf16 MFMA (N = P = 64).
+//
+// Same arithmetic and bf16 rounding points as the reference kernel
+// (src/trifusion_l4/mamba_fused.py:72-152). One workgroup of twelve waves
+// (three per SIMD) walks one (batch, head) unit chunk by chunk (64 steps). A
+// chunk's work is cut into stages that run in the two intervals (A, B) between
+// the workgroup barriers of consecutive iterations, so the stages of
+// neighbouring chunks overlap:
+//
+//   stage of chunk c       interval   waves                  lane layout
+//   controls               A(c-1)     prologue wave 3        lane = row
+//   phase, cos/sin         B(c-1)     state waves            lane = (pair, row segment)
+//   bias, rotation         A(c)       output + state waves   lane = row, wave = 8 channels
+//   state S_{c+1}          B(c)       state waves            one 32x32 tile of S each
+//   scores                 A(c+1)     prologue waves 0-2     one 32x32 score tile each
+//   skip, inter-chunk      A(c+1)     output waves           one 32x32 tile of y each
+//   scores . v, gate       B(c+1)     output waves           the same tile
+//
+// Waves 0-3 are output waves (time half th = w >> 1, head-dim tile pt = w & 1),
+// waves 4-7 state waves (s = w - 4: state tile nt = s >> 1, pt = s & 1) and
+// waves 8-11 prologue waves, so each SIMD holds one of each. The fp32 state S
+// (64 x 64) lives in the state waves' registers for the whole walk: each holds
+// one 32 x 32 tile in MFMA accumulator layout and applies S <- S 2^tot + dS
+// once per chunk; there is no scan and no state in LDS other than the bf16
+// copies the outputs read.
+//
+// Chunk-local operands pass through LDS as bf16 rows (rotated q, rotated and
+// scaled k, v, decay-scaled v) and are read back either as MFMA row operands
+// (8-byte pieces) or transposed with ds_read_b64_tr_b16, which gives each lane
+// four consecutive rows of one column: the transposes the contractions over
+// time need (v^T, kr^T, vs^T) cost no VALU work.
+//
+// The rotary phase is kept exactly: each increment tanh(theta) dt / 2 (in
+// revolutions) is reduced to [-1/2, 1/2] and converted to 32-bit fixed point,
+// whose wrapping integer sums are the phase mod one revolution; v_sin/v_cos
+// take revolutions directly.
+#include "mfma_tile.h"
+
+namespace tf {
+namespace {
+
+constexpr int kTrigStride = 68;  // floats per row of the cos/sin table: 32 pairs x 2 + 4 pad
+
+typedef __attribute__((ext_vector_type(4))) short s16x4;
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// Element offset of 8-byte unit u (0..15) of row t (0..63) in a [64][64] bf16
+// row buffer. Units are XOR-swizzled by the row, so that the three access
+// patterns each touch 16 distinct units (all 32 banks once) per 16 lanes:
+// row-form reads (16 rows, one unit), transposing reads (4 rows x 4 units) and
+// row writes (16 rows, one unit).
+__device__ __forceinline__ int rb_off(int t, int u) {
+  const int swz = ((t & 3) << 2) | ((t >> 2) & 3);
+  return t * 64 + ((u ^ swz) << 2);
+}
+
+__device__ __forceinline__ u32x2 rb_read(const uint16_t* buf, int t, int u) {
+  return *reinterpret_cast<const u32x2*>(buf + rb_off(t, u));
+}
+
+// Row-form MFMA operand of k-step s (contraction over the 64 columns) of row t:
+// slots j hold columns kidx(s, hh, j).
+__device__ __forceinline__ u32x4 row_operand(const uint16_t* buf, int t, int s, int hh) {
+  const int u = 8 * (s >> 1) + 4 * (s & 1) + hh;
+  const u32x2 lo = rb_read(buf, t, u), hi = rb_read(buf, t, u + 2);
+  return u32x4{lo[0], lo[1], hi[0], hi[1]};
+}
+
+// Transposed MFMA operand of k-step s (contraction over the 64 rows) for the
+// 32 columns of column tile `tile`: lane (c32, hh) receives column
+// 32 tile + c32 at rows kidx(s, hh, j). Within each 16-lane group the source
+// lane i = 4k + c reads row r0 + k, unit u0 + c, and the transposing read
+// hands output lane j column 4 u0 + j of rows r0 .. r0 + 3.
+__device__ __forceinline__ u32x4 tr_operand(const uint16_t* buf, int tile, int s, int lane) {
+  const int g = lane >> 4;
+  const int i = lane & 15;
+  const int r0 = 32 * (s >> 1) + 16 * (s & 1) + 4 * (g >> 1) + (i >> 2);
+  const int u = 8 * tile + 4 * (g & 1) + (i & 3);
+  const uint16_t* p0 = buf + rb_off(r0, u);
+  const uint16_t* p1 = buf + rb_off(r0 + 8, u);
+  const s16x4 a = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p0));
+  const s16x4 b = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p1));
+  const u32x2 ua = __builtin_bit_cast(u32x2, a), ub = __builtin_bit_cast(u32x2, b);
+  return u32x4{ua[0], ua[1], ub[0], ub[1]};
+}
+
+// As tr_operand, over the 32 rows of one time half (k-steps s = 0, 1 of rows
+// 32 half .. 32 half + 31).
+__device__ __forceinline__ u32x4 tr_operand_half(const uint16_t* buf, int tile, int half, int s, int lane) {
+  return tr_operand(buf, tile, 2 * half + s, lane);
+}
+
+__device__ __forceinline__ void rb_write16(uint16_t* buf, int t, int u, const u32x4& x) {
+  *reinterpret_cast<u32x2*>(buf + rb_off(t, u)) = u32x2{x[0], x[1]};
+  *reinterpret_cast<u32x2*>(buf + rb_off(t, u + 1)) = u32x2{x[2], x[3]};
+}
+
+struct PipeSmem {
+  uint16_t qr[2][64 * 64];  // bf16(rot(q + qb))
+  uint16_t kr[2][64 * 64];  // bf16(rot(k + kb) * s)
+  uint16_t v[2][64 * 64];   // v (0 past the valid length)
+  uint16_t vs[2][64 * 64];  // bf16(v * 2^(tot - cs))
+  float trig[2][64 * kTrigStride];  // [row][pair] (cos, sin)
+  u32x4 sb[3][4][2][64];     // bf16 S_c (c mod 3): tiles (nt, pt), k-step halves, in MFMA operand order
+  u32x4 score[2][3][2][64];  // bf16 score tiles (0,0), (1,0), (1,1), k-steps, in operand order
+  float dt[3][64];
+  float sc[3][64];   // trapezoid scale s_t of the keys
+  float cs[3][64];   // inclusive log2 decay within the chunk
+  float wv[3][64];   // 2^(tot - cs_t)
+  float gam[3][64];  // dt_t sigmoid(trap_t)
+  float skip[3][8][64];  // partial (q + qb).(k + kb) of each wave's 8 channels
+  float tot[3][4];       // [0]: the chunk's total log2 decay
+  float qb[64], kb[64];
+};
+
+struct PipeCtl {
+  float dt, dn, adt, tr, tn;
+};
+
+template <bool BF16>
+__device__ __forceinline__ float load_elem(const void* base, int i) {
+  if constexpr (BF16)
+    return bf16_to_f32(static_cast<const uint16_t*>(base)[i]);
+  else
+    return static_cast<const float*>(base)[i];
+}
+
+// Controls of row t and its halo step t + 1 (raw values when P.ctl_raw). Rows
+// are clamped to ones that exist and masked where used, so no load sits behind
+// a branch and the loads stay in flight until then.
+template <bool CTL16, bool TRAP16>
+__device__ __forceinline__ PipeCtl load_pipe_ctl(const MfmaParams& P, int dto, int ado, int trb, int t, int L,
+                                                 int tlim) {
+  const int tc = min(t, L - 1);
+  const int tn = min(t + 1, tlim - 1);
+  PipeCtl c;
+  c.dt = load_elem<CTL16>(P.dt, dto + tc * P.d_st);
+  c.dn = load_elem<CTL16>(P.dt, dto + tn * P.d_st);
+  c.adt = load_elem<CTL16>(P.adt, ado + tc * P.a_st);
+  c.tr = load_elem<TRAP16>(P.trap, trb + tc * P.r_st);
+  c.tn = load_elem<TRAP16>(P.trap, trb + tn * P.r_st);
+  return c;
+}
+
+// Phase lanes: lane = pi * (64 / RPW) + sg takes pair s * RPW + pi over the
+// RPW rows sg * RPW .. sg * RPW + RPW - 1 of the chunk, so the segments of one
+// pair are consecutive lanes (a DPP scan). Lanes of pairs >= R read pair 0's
+// column and are never used.
+template <int RPW, bool ANG16>
+__device__ __forceinline__ void load_pipe_angles(const MfmaParams& P, float (&th)[RPW], int gbase, int pair,
+                                                 int row0, int L) {
+  const int col = gbase + (pair < P.R ? pair : 0) * P.g_sr;
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) th[i] = load_elem<ANG16>(P.angles, col + min(row0 + i, L - 1) * P.g_st);
+}
+
+// Raw 16-byte row pieces of the wave's eight channels (lane = row).
+struct PipeRows {
+  u32x4 q, k, v;
+};
+
+template <int RPW, bool CTL16, bool TRAP16, bool ANG16>
+__global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
+  __shared__ PipeSmem sh;
+  const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int lane = static_cast<int>(threadIdx.x & 63);
+  const int c32 = lane & 31;
+  const int hh = lane >> 5;
+  const bool out_wave = w < 4;
+  const bool state_wave = w >= 4 && w < 8;
+  const int s_idx = w - 4;  // state wave index (state waves)
+  const int p_idx = w - 8;  // prologue wave index (prologue waves)
+  const int unit = P.xcd_per > 0 ? (blockIdx.x & 7) * P.xcd_per + (blockIdx.x >> 3) : static_cast<int>(blockIdx.x);
+  const int b = unit / P.H;
+  const int h = unit - b * P.H;
+  const int qh = h / P.group;
+  const int T = P.T;
+  const int R = P.R;
+  int L = T;
+  if (P.lengths != nullptr) {
+    const int64_t l = P.lengths[b];
+    L = l < 0 ? 0 : (l > T ? T : static_cast<int>(l));
+  }
+  const int nvalid = (L + kChunk - 1) / kChunk;
+  const int tlim = P.rev ? L : T;
+  const int roff = P.rev ? max(L - 1, 0) : 0;
+  const uint16_t* qbase = P.q + b * P.q_sb + qh * P.q_sh - roff * P.q_st;
+  const uint16_t* kbase = P.k + b * P.k_sb + qh * P.k_sh - roff * P.k_st;
+  const uint16_t* vbase = P.v + b * P.v_sb + h * P.v_sh - roff * P.v_st;
+  const uint16_t* zbase = P.z + b * P.z_sb + h * P.z_sh - roff * P.z_st;
+  const int dto = b * P.d_sb + h * P.d_sh - roff * P.d_st;
+  const int ado = b * P.a_sb + h * P.a_sh - roff * P.a_st;
+  const int trb = b * P.r_sb + h * P.r_sh - roff * P.r_st;
+  const int gbase = b * P.g_sb + h * P.g_sh - roff * P.g_st;
+  const int obase = b * P.o_sb + h * P.o_sh - roff * P.o_st;
+  const float step_bias = P.ctl_raw ? P.dt_bias[h] : 0.f;
+  const float skip_d = P.d[h];
+
+  if (nvalid > 0) {
+    if (threadIdx.x < 64) {
+      sh.qb[threadIdx.x] = P.qb[h * 64 + threadIdx.x];
+      sh.kb[threadIdx.x] = P.kb[h * 64 + threadIdx.x];
+    }
+    constexpr int NSEG = 64 / RPW;  // row segments per pair
+    const int pi = lane / NSEG;
+    const int sg = lane & (NSEG - 1);
+    const int pair = s_idx * RPW + pi;
+    const bool phase_wave = state_wave && s_idx * RPW < R;  // wave-uniform
+
+    const int ng = (w + 4) & 7;  // channel group of the rotary stage (waves 0-7)
+    auto load_rows = [&](int c) {
+      const int t = min(c * kChunk + lane, L - 1);
+      PipeRows r;
+      r.q = *reinterpret_cast<const u32x4*>(qbase + t * P.q_st + 8 * ng);
+      r.k = *reinterpret_cast<const u32x4*>(kbase + t * P.k_st + 8 * ng);
+      r.v = *reinterpret_cast<const u32x4*>(vbase + t * P.v_st + 8 * ng);
+      return r;
+    };
+
+    // controls of chunk c (state wave 3, lane = row)
+    auto controls = [&](const PipeCtl& raw, int c) {
+      const int t = c * kChunk + lane;
+      const bool valid = t < L;
+      const bool next = t + 1 < tlim;
+      float dtv = raw.dt, dnv = raw.dn, adv = raw.adt;
+      if (P.ctl_raw) {
+        // step and decay from the raw columns (primitives.py:209-214)
+        dtv = control_step(dtv, step_bias);
+        dnv = control_step(dnv, step_bias);
+        adv = control_decay(adv, dtv, P.a_floor);
+      }
+      // rows without a step keep dt = adt = 0, and a missing halo step loads 0
+      dtv = valid ? dtv : 0.f;
+      adv = valid ? adv : 0.f;
+      dnv = next ? dnv : 0.f;
+      const float trv = valid ? raw.tr : 0.f;
+      const float tnv = next ? raw.tn : 0.f;
+      // mamba_fused.py:96-101, 139-142
+      const float gam = dtv * sigmoid_fast(trv);
+      const float scl = dnv * (1.f - sigmoid_fast(tnv)) + gam;
+      const float cs = wave_scan_dpp(adv * kLog2e);
+      const float tot = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cs), 63));
+      const int cr = c % 3;
+      sh.dt[cr][lane] = dtv;
+      sh.sc[cr][lane] = scl;
+      sh.cs[cr][lane] = cs;
+      sh.wv[cr][lane] = fast_exp2(tot - cs);
+      sh.gam[cr][lane] = gam;
+      if (lane == 0) sh.tot[cr][0] = tot;
+    };
+
+    // rotary phase and cos/sin of chunk c (phase waves)
+    uint32_t carry = 0;  // phase entering the chunk, pair `pair`, 2^-32 revolutions
+    auto phase = [&](const float (&th)[RPW], int c) {
+      const int cr = c % 3;
+      uint32_t loc[RPW];
+      uint32_t run = 0;
+#pragma unroll
+      for (int i = 0; i < RPW; ++i) {
+        // pi tanh(theta) dt radians = tanh(theta) dt / 2 revolutions (mamba_fused.py:102-109)
+        float om = tanh_fast(th[i]) * sh.dt[cr][sg * RPW + i] * 0.5f;
+        om -= rintf(om);
+        const float x = fminf(om * 4294967296.f, 2147483520.f);
+        run += static_cast<uint32_t>(static_cast<int>(x));
+        loc[i] = run;
+      }
+      const uint32_t incl = group_scan_dpp<NSEG>(run, lane);  // over the segments of the pair
+      const uint32_t base = carry + (incl - run);
+      // the chunk's sum for the pair: the last segment's inclusive sum
+      uint32_t total = 0;
+#pragma unroll
+      for (int j = 0; j < RPW; ++j) {
+        const uint32_t tj = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl), NSEG * j + NSEG - 1));
+        total = pi == j ? tj : total;
+      }
+      carry += total;
+      if (pair < R) {
+        float* tg = &sh.trig[c & 1][0];
+#pragma unroll
+        for (int i = 0; i < RPW; ++i) {
+          const float rev = static_cast<float>(static_cast<int>(base + loc[i])) * 2.3283064365386963e-10f;
+          *reinterpret_cast<float2*>(tg + (sg * RPW + i) * kTrigStride + 2 * pair) =
+              make_float2(__builtin_amdgcn_cosf(rev), __builtin_amdgcn_sinf(rev));
+        }
+      }
+    };
+
+    // bias, rotation, scaling and bf16 rounding of chunk c's rows (lane = row,
+    // channels 8 ng .. 8 ng + 7; mamba_fused.py:112-135, 151). The state waves
+    // take channel groups 0-3, which hold the rotated pairs when R <= 16, and
+    // the output waves groups 4-7, so each SIMD gets one of each.
+    auto rotary = [&](const PipeRows& in, int c) {
+      const int cb = c & 1, cr = c % 3;
+      const bool valid = c * kChunk + lane < L;
+      const float scl = sh.sc[cr][lane];
+      const float wvt = sh.wv[cr][lane];
+      // biases of the wave's channels (same address in every lane)
+      float qbv[8], kbv[8];
+      {
+        const float4* qp = reinterpret_cast<const float4*>(&sh.qb[8 * ng]);
+        const float4* kp = reinterpret_cast<const float4*>(&sh.kb[8 * ng]);
+        const float4 q0 = qp[0], q1 = qp[1], k0 = kp[0], k1 = kp[1];
+        qbv[0] = q0.x, qbv[1] = q0.y, qbv[2] = q0.z, qbv[3] = q0.w;
+        qbv[4] = q1.x, qbv[5] = q1.y, qbv[6] = q1.z, qbv[7] = q1.w;
+        kbv[0] = k0.x, kbv[1] = k0.y, kbv[2] = k0.z, kbv[3] = k0.w;
+        kbv[4] = k1.x, kbv[5] = k1.y, kbv[6] = k1.z, kbv[7] = k1.w;
+      }
+      u32x4 qo, ko, vo, vso;
+      float part = 0.f;
+      if (4 * ng < R) {
+        // pairs 4 ng + j >= R turn by the identity: x * 1 - y * 0 is x exactly
+        const float4* tg = reinterpret_cast<const float4*>(&sh.trig[cb][lane * kTrigStride + 8 * ng]);
+        const float4 a = tg[0], bq = tg[1];
+        const float cosv[4] = {a.x, a.z, bq.x, bq.z}, sinv[4] = {a.y, a.w, bq.y, bq.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const bool on = 4 * ng + j < R;
+          const float cv = on ? cosv[j] : 1.f, sv = on ? sinv[j] : 0.f;
+          const float q0 = lo_f(in.q[j]) + qbv[2 * j], q1 = hi_f(in.q[j]) + qbv[2 * j + 1];
+          const float k0 = lo_f(in.k[j]) + kbv[2 * j], k1 = hi_f(in.k[j]) + kbv[2 * j + 1];
+          part += q0 * k0 + q1 * k1;
+          qo[j] = pack2(q0 * cv - q1 * sv, q0 * sv + q1 * cv);
+          ko[j] = pack2((k0 * cv - k1 * sv) * scl, (k0 * sv + k1 * cv) * scl);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float q0 = lo_f(in.q[j]) + qbv[2 * j], q1 = hi_f(in.q[j]) + qbv[2 * j + 1];
+          const float k0 = lo_f(in.k[j]) + kbv[2 * j], k1 = hi_f(in.k[j]) + kbv[2 * j + 1];
+          part += q0 * k0 + q1 * k1;
+          qo[j] = pack2(q0, q1);
+          ko[j] = pack2(k0 * scl, k1 * scl);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t vw = valid ? in.v[j] : 0u;
+        vo[j] = vw;
+        vso[j] = pack2(lo_f(vw) * wvt, hi_f(vw) * wvt);
+      }
+      rb_write16(sh.qr[cb], lane, 2 * ng, qo);
+      rb_write16(sh.kr[cb], lane, 2 * ng, ko);
+      rb_write16(sh.v[cb], lane, 2 * ng, vo);
+      rb_write16(sh.vs[cb], lane, 2 * ng, vso);
+      sh.skip[cr][ng][lane] = part;
+    };
+
+    // loads ahead of use: rows of chunk c at A(c-1), controls of chunk c at
+    // A(c-2), angles of chunk c at B(c-2), z of chunk c at B(c)
+    PipeRows rows = load_rows(0);
+    PipeCtl ctl_next = {};
+    float th[RPW];
+#pragma unroll
+    for (int i = 0; i < RPW; ++i) th[i] = 0.f;
+    if (w == 11) {
+      const PipeCtl c0 = load_pipe_ctl<CTL16, TRAP16>(P, dto, ado, trb, lane, L, tlim);
+      if (nvalid > 1) ctl_next = load_pipe_ctl<CTL16, TRAP16>(P, dto, ado, trb, kChunk + lane, L, tlim);
+      controls(c0, 0);
+    }
+    if (phase_wave) load_pipe_angles<RPW, ANG16>(P, th, gbase, pair, sg * RPW, L);
+    lds_barrier();
+    if (phase_wave) {
+      phase(th, 0);
+      if (nvalid > 1) load_pipe_angles<RPW, ANG16>(P, th, gbase, pair, kChunk + sg * RPW, L);
+    }
+    if (state_wave) {  // S_0 = 0
+      sh.sb[0][s_idx][0][lane] = u32x4{0u, 0u, 0u, 0u};
+      sh.sb[0][s_idx][1][lane] = u32x4{0u, 0u, 0u, 0u};
+    }
+    lds_barrier();
+
+    f32x16 S = zero16();  // state waves: tile (nt, pt) of S^T[n][p]
+    u32x2 zr[4] = {};     // output waves: gate rows of the chunk being finished
+    const int nt = (s_idx >> 1) & 1, spt = s_idx & 1;
+    const int th_o = w >> 1, opt = w & 1;
+
+    f32x16 ybase = zero16();  // output waves: skip and inter-chunk terms of the chunk being finished
+    for (int i = 0; i <= nvalid; ++i) {
+      // ---------------- interval A(i) ----------------
+      if (w < 8 && i < nvalid) {
+        rotary(rows, i);
+        if (i + 1 < nvalid) rows = load_rows(i + 1);
+      }
+      if (out_wave && i >= 1) {
+        // chunk c = i - 1, tile (th, pt) of y^T[p][t]: (D + gamma (q + qb).(k + kb)) v
+        // (mamba_fused.py:124, 147) + 2^cs qr . bf16(S_c)^T (mamba_fused.py:143)
+        const int c = i - 1;
+        const int cb = c & 1, cr = c % 3;
+        const int tl = 32 * th_o + c32;
+        u32x4 sx[4], qy[4];
+        u32x2 vv[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          sx[s] = sh.sb[cr][2 * (s >> 1) + opt][s & 1][lane];
+          qy[s] = row_operand(sh.qr[cb], tl, s, hh);
+        }
+#pragma unroll
+        for (int g = 0; g < 4; ++g) vv[g] = rb_read(sh.v[cb], tl, 8 * opt + 2 * g + hh);
+        float part = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) part += sh.skip[cr][j][tl];
+        const float coef = skip_d + sh.gam[cr][tl] * part;
+        const float decay = fast_exp2(sh.cs[cr][tl]);
+        f32x16 yi = zero16();
+#pragma unroll
+        for (int s = 0; s < 4; ++s) yi = mfma(sx[s], qy[s], yi);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          ybase[4 * g] = coef * lo_f(vv[g][0]) + yi[4 * g] * decay;
+          ybase[4 * g + 1] = coef * hi_f(vv[g][0]) + yi[4 * g + 1] * decay;
+          ybase[4 * g + 2] = coef * lo_f(vv[g][1]) + yi[4 * g + 2] * decay;
+          ybase[4 * g + 3] = coef * hi_f(vv[g][1]) + yi[4 * g + 3] * decay;
+        }
+      }
+      if (w >= 8 && p_idx < 3 && i >= 1) {
+        // scores of chunk i - 1: tile (th, uh) = (0,0), (1,0), (1,1)
+        const int c = i - 1;
+        const int cb = c & 1;
+        const int sth = p_idx > 0 ? 1 : 0;
+        const int suh = p_idx > 1 ? 1 : 0;
+        u32x4 kx[4], qy[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          kx[s] = row_operand(sh.kr[cb], 32 * suh + c32, s, hh);
+          qy[s] = row_operand(sh.qr[cb], 32 * sth + c32, s, hh);
+        }
+        f32x16 acc = zero16();
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc = mfma(kx[s], qy[s], acc);
+        u32x4 sc[2];
+        const float* csr = sh.cs[c % 3];
+        score_tile(acc, csr[32 * sth + c32], csr + 32 * suh, sth == suh, c32, hh, sc);
+        sh.score[cb][p_idx][0][lane] = sc[0];
+        sh.score[cb][p_idx][1][lane] = sc[1];
+      }
+      if (w == 11 && i + 1 < nvalid) {
+        controls(ctl_next, i + 1);
+        if (i + 2 < nvalid) ctl_next = load_pipe_ctl<CTL16, TRAP16>(P, dto, ado, trb, (i + 2) * kChunk + lane, L, tlim);
+      }
+      lds_barrier();
+
+      // ---------------- interval B(i) ----------------
+      if (state_wave && i + 1 < nvalid) {
+        // S_{i+1} = S_i 2^tot + kr^T . bf16(v 2^(tot - cs)) of chunk i (mamba_fused.py:150-152)
+        const int cb = i & 1;
+        u32x4 kx[4], vy[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          kx[s] = tr_operand(sh.kr[cb], nt, s, lane);
+          vy[s] = tr_operand(sh.vs[cb], spt, s, lane);
+        }
+        const float dec = fast_exp2(sh.tot[i % 3][0]);
+        f32x16 d = zero16();
+#pragma unroll
+        for (int s = 0; s < 4; ++s) d = mfma(kx[s], vy[s], d);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) S[e] = S[e] * dec + d[e];
+        u32x4 lo, hi;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          lo[q] = pack2(S[2 * q], S[2 * q + 1]);
+          hi[q] = pack2(S[8 + 2 * q], S[8 + 2 * q + 1]);
+        }
+        sh.sb[(i + 1) % 3][s_idx][0][lane] = lo;
+        sh.sb[(i + 1) % 3][s_idx][1][lane] = hi;
+      }
+      if (phase_wave && i + 1 < nvalid) {
+        phase(th, i + 1);
+        if (i + 2 < nvalid) load_pipe_angles<RPW, ANG16>(P, th, gbase, pair, (i + 2) * kChunk + sg * RPW, L);
+      }
+      if (out_wave) {
+        if (i >= 1) {
+          // chunk c = i - 1: intra-chunk scores . v (mamba_fused.py:144-146), gate, store
+          const int c = i - 1;
+          const int cb = c & 1;
+          const int tl = 32 * th_o + c32;
+          f32x16 y = ybase;
+          if (th_o == 0) {
+            const u32x4 s0 = sh.score[cb][0][0][lane], s1 = sh.score[cb][0][1][lane];
+            const u32x4 v0 = tr_operand_half(sh.v[cb], opt, 0, 0, lane);
+            const u32x4 v1 = tr_operand_half(sh.v[cb], opt, 0, 1, lane);
+            y = mfma(v0, s0, y);
+            y = mfma(v1, s1, y);
+          } else {
+            const u32x4 s0 = sh.score[cb][1][0][lane], s1 = sh.score[cb][1][1][lane];
+            const u32x4 s2 = sh.score[cb][2][0][lane], s3 = sh.score[cb][2][1][lane];
+            const u32x4 v0 = tr_operand_half(sh.v[cb], opt, 0, 0, lane);
+            const u32x4 v1 = tr_operand_half(sh.v[cb], opt, 0, 1, lane);
+            const u32x4 v2 = tr_operand_half(sh.v[cb], opt, 1, 0, lane);
+            const u32x4 v3 = tr_operand_half(sh.v[cb], opt, 1, 1, lane);
+            y = mfma(v0, s0, y);
+            y = mfma(v1, s1, y);
+            y = mfma(v2, s2, y);
+            y = mfma(v3, s3, y);
+          }
+          const int t = c * kChunk + tl;
+          float yv[16];
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int e = 4 * g + q;
+              const uint32_t zw = zr[g][q >> 1];
+              const float zz = (q & 1) ? hi_f(zw) : lo_f(zw);
+              // silu gate (mamba_fused.py:148)
+              yv[e] = y[e] * (zz * sigmoid_fast(zz));
+            }
+          }
+          if (t < L) {  // rows in [L, T) are zero-filled after the walk
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              const int off = obase + t * P.o_st + 32 * opt + 8 * g + 4 * hh;
+              if (P.out_f32) {
+                *reinterpret_cast<float4*>(static_cast<float*>(P.out) + off) =
+                    make_float4(yv[4 * g], yv[4 * g + 1], yv[4 * g + 2], yv[4 * g + 3]);
+              } else {
+                *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(P.out) + off) =
+                    u32x2{pack2(yv[4 * g], yv[4 * g + 1]), pack2(yv[4 * g + 2], yv[4 * g + 3])};
+              }
+            }
+          }
+        }
+        if (i < nvalid) {
+          // gate rows of chunk i, consumed at B(i + 1)
+          const int t = min(i * kChunk + 32 * th_o + c32, L - 1);
+          const uint16_t* zrow = zbase + t * P.z_st + 32 * opt + 4 * hh;
+#pragma unroll
+          for (int g = 0; g < 4; ++g) zr[g] = *reinterpret_cast<const u32x2*>(zrow + 8 * g);
+        }
+      }
+      lds_barrier();
+    }
+  }
+
+  // rows in [L, T), the same rows in either direction: unreversed base and stride
+  constexpr int PD = 64;
+  const int o_st = P.rev ? -P.o_st : P.o_st;
+  const int obase_fwd = b * P.o_sb + h * P.o_sh;
+  for (int e = L * PD + static_cast<int>(threadIdx.x); e < T * PD; e += 768) {
+    const int tt = e / PD, p = e - tt * PD;
+    const int off = obase_fwd + tt * o_st + p;
+    if (P.out_f32)
+      static_cast<float*>(P.out)[off] = 0.f;
+    else
+      static_cast<uint16_t*>(P.out)[off] = 0;
+  }
+}
+
+}  // namespace
+
+bool pipe_supported(const tf_mamba_args& a) {
+  if (a.state != 64 || a.head_dim != 64) return false;
+  if (a.rotary < 0 || a.rotary > 32) return false;
+  if (a.q_dtype != TF_BFLOAT16 || a.k_dtype != TF_BFLOAT16 || a.v_dtype != TF_BFLOAT16 || a.z_dtype != TF_BFLOAT16)
+    return false;
+  if (a.dt_bias == nullptr) {
+    if (a.adt_dtype != TF_FLOAT32 || a.dt_dtype != TF_FLOAT32) return false;
+  } else if (a.adt_dtype != a.dt_dtype || (a.dt_dtype != TF_FLOAT32 && a.dt_dtype != TF_BFLOAT16)) {
+    return false;
+  }
+  if (a.trap_dtype != TF_FLOAT32 && a.trap_dtype != TF_BFLOAT16) return false;
+  if (a.angles_dtype != TF_FLOAT32 && a.angles_dtype != TF_BFLOAT16) return false;
+  if (a.out_dtype != TF_BFLOAT16 && a.out_dtype != TF_FLOAT32) return false;
+  if (a.batch * a.heads > 0x7fffffff) return false;
+  // q, k, v rows in 16-byte pieces; z and out rows in 8-byte (bf16) or 16-byte (fp32) pieces
+  if (!rows_vectorisable(a.q, a.q_stride, 2, 16) || !rows_vectorisable(a.k, a.k_stride, 2, 16) ||
+      !rows_vectorisable(a.v, a.v_stride, 2, 16) || !rows_vectorisable(a.z, a.z_stride, 2, 8))
+    return false;
+  const int ob = a.out_dtype == TF_FLOAT32 ? 4 : 2;
+  if (!rows_vectorisable(a.out, a.out_stride, ob, 4 * ob)) return false;
+  return offsets_fit(a);
+}
+
+namespace {
+
+template <int RPW, bool CTL16, bool TRAP16, bool ANG16>
+int launch_pipe_kernel(const MfmaParams& P, hipStream_t stream) {
+  const dim3 grid(static_cast<uint32_t>(P.units)), block(768);
+  hipLaunchKernelGGL((mamba_pipe_kernel<RPW, CTL16, TRAP16, ANG16>), grid, block, 0, stream, P);
+  return launch_status();
+}
+
+template <int RPW>
+int launch_pipe_rpw(const MfmaParams& P, hipStream_t stream) {
+  const int key = (P.ctl_bf16 ? 4 : 0) | (P.trap_bf16 ? 2 : 0) | (P.angles_dtype == TF_BFLOAT16 ? 1 : 0);
+  switch (key) {
+    case 0: return launch_pipe_kernel<RPW, false, false, false>(P, stream);
+    case 1: return launch_pipe_kernel<RPW, false, false, true>(P, stream);
+    case 2: return launch_pipe_kernel<RPW, false, true, false>(P, stream);
+    case 3: return launch_pipe_kernel<RPW, false, true, true>(P, stream);
+    case 4: return launch_pipe_kernel<RPW, true, false, false>(P, stream);
+    case 5: return launch_pipe_kernel<RPW, true, false, true>(P, stream);
+    case 6: return launch_pipe_kernel<RPW, true, true, false>(P, stream);
+    default: return launch_pipe_kernel<RPW, true, true, true>(P, stream);
+  }
+}
+
+}  // namespace
+
+int launch_pipe(const tf_mamba_args& a, hipStream_t stream) {
+  MfmaParams P = make_params(a);
+  const int64_t units = a.batch * a.heads;
+  P.xcd_per = (units % 8 == 0 && units >= 64) ? static_cast<int>(units / 8) : 0;
+  return a.rotary <= 16 ? launch_pipe_rpw<4>(P, stream) : launch_pipe_rpw<8>(P, stream);
+}
+
+}  // namespace tf

@@ -31,7 +31,7 @@ STATUS = {
     7: "needs more scratch than the library's static area holds",
 }
 
-VARIANTS = {"auto": 0, "generic": 1, "mfma": 2}
+VARIANTS = {"auto": 0, "generic": 1, "mfma": 2, "pipe": 3}
 
 
 class MambaArgs(ctypes.Structure):

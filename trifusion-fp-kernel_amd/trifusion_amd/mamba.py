@@ -66,7 +66,7 @@ class Mamba3Inference(nn.Module):
         self.D = nn.Parameter(torch.ones(self.nheads))
         self.B_norm = RMSNorm(self.d_state)
         self.C_norm = RMSNorm(self.d_state)
-        # "mfma" (chunked MFMA scan), "generic" (fp32-FMA kernel) or "auto"
+        # "pipe" (pipelined MFMA walk), "mfma" (chunked MFMA scan), "generic" (fp32-FMA kernel) or "auto"
         self.variant = "auto"
         self.fuse_controls = True
         self._padded = None

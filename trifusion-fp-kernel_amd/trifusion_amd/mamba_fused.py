@@ -171,8 +171,9 @@ def fused_mamba(
     """Fused Mamba-3 recurrence forward; returns ``out`` ``[B, T, H, P]``.
 
     ``warps`` is accepted for signature compatibility; gfx950 launch shapes are
-    chosen by the library. ``variant`` selects ``"auto"`` (MFMA chunked scan
-    where supported), ``"mfma"`` or ``"generic"``. ``reverse``, ``dt_bias`` and
+    chosen by the library. ``variant`` selects ``"auto"`` (an MFMA kernel
+    where supported), ``"pipe"`` (pipelined walk, N = P = 64), ``"mfma"``
+    (chunked scan) or ``"generic"``. ``reverse``, ``dt_bias`` and
     ``a_floor`` are the extensions described in the module docstring.
     Dispatches through the ``trifusion_amd::fused_mamba`` operator
     (``fused_mamba.out`` with ``out=``).
@@ -195,4 +196,4 @@ def selected_variant(
     code = lib.tf_fused_mamba_variant(ctypes.byref(args))
     if code < 0:
         _lib.check(-code, "fused_mamba")
-    return {1: "generic", 2: "mfma"}[code]
+    return {1: "generic", 2: "mfma", 3: "pipe"}[code]

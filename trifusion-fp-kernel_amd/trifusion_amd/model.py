@@ -117,7 +117,7 @@ class Encoder(nn.Module):
                     nn.init.zeros_(m.bias)
 
     def set_variant(self, variant):
-        """Select the recurrence kernel ("auto", "mfma" or "generic") of every block."""
+        """Select the recurrence kernel ("auto", "pipe", "mfma" or "generic") of every block."""
         for m in self.modules():
             if isinstance(m, Mamba3Inference):
                 m.variant = variant

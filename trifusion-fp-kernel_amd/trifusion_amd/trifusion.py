@@ -504,7 +504,7 @@ class TriFusion(nn.Module):
         self.memory_head = nn.Linear(c.dim, 2)
 
     def set_variant(self, variant):
-        """Select the recurrence kernel ("auto", "mfma" or "generic") of every Mamba."""
+        """Select the recurrence kernel ("auto", "pipe", "mfma" or "generic") of every Mamba."""
         for m in self.modules():
             if isinstance(m, Mamba3Inference):
                 m.variant = variant
