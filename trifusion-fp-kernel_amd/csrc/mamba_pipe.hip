@@ -110,7 +110,6 @@ struct PipeSmem {
   float gam[3][64];  // dt_t sigmoid(trap_t)
   float skip[3][8][64];  // partial (q + qb).(k + kb) of each wave's 8 channels
   float tot[3][4];       // [0]: the chunk's total log2 decay
-  float qb[64], kb[64];
 };
 
 struct PipeCtl {
@@ -197,10 +196,6 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
   const float skip_d = P.d[h];
 
   if (nvalid > 0) {
-    if (threadIdx.x < 64) {
-      sh.qb[threadIdx.x] = P.qb[h * 64 + threadIdx.x];
-      sh.kb[threadIdx.x] = P.kb[h * 64 + threadIdx.x];
-    }
     constexpr int NSEG = 64 / RPW;  // row segments per pair
     const int pi = lane / NSEG;
     const int sg = lane & (NSEG - 1);
@@ -285,6 +280,14 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
       }
     };
 
+    // biases of the wave's eight channels, wave-uniform, kept for the whole walk
+    float qbv[8], kbv[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      qbv[j] = P.qb[h * 64 + 8 * ng + j];
+      kbv[j] = P.kb[h * 64 + 8 * ng + j];
+    }
+
     // bias, rotation, scaling and bf16 rounding of chunk c's rows (lane = row,
     // channels 8 ng .. 8 ng + 7; mamba_fused.py:112-135, 151). The state waves
     // take channel groups 0-3, which hold the rotated pairs when R <= 16, and
@@ -294,17 +297,6 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
       const bool valid = c * kChunk + lane < L;
       const float scl = sh.sc[cr][lane];
       const float wvt = sh.wv[cr][lane];
-      // biases of the wave's channels (same address in every lane)
-      float qbv[8], kbv[8];
-      {
-        const float4* qp = reinterpret_cast<const float4*>(&sh.qb[8 * ng]);
-        const float4* kp = reinterpret_cast<const float4*>(&sh.kb[8 * ng]);
-        const float4 q0 = qp[0], q1 = qp[1], k0 = kp[0], k1 = kp[1];
-        qbv[0] = q0.x, qbv[1] = q0.y, qbv[2] = q0.z, qbv[3] = q0.w;
-        qbv[4] = q1.x, qbv[5] = q1.y, qbv[6] = q1.z, qbv[7] = q1.w;
-        kbv[0] = k0.x, kbv[1] = k0.y, kbv[2] = k0.z, kbv[3] = k0.w;
-        kbv[4] = k1.x, kbv[5] = k1.y, kbv[6] = k1.z, kbv[7] = k1.w;
-      }
       u32x4 qo, ko, vo, vso;
       float part = 0.f;
       if (4 * ng < R) {
