@@ -12,8 +12,11 @@ cache-warm time is reported beside it.
 
 Printed as one JSON line: ``value`` is the algorithmic GB/s (unique input bytes +
 output bytes per call / average call time), ``roofline`` compares it with the
-8 TB/s HBM peak, ``cpu_baseline`` times the CPU oracle (chunked fp32 PyTorch) on
-the same workload on the host cores, ``encoder`` reports the ms per forward
+8 TB/s HBM peak, ``workloads`` times the variable-length channel-folded batch
+(B32 padded L400) and the 72 s long clip (B1 L7200) the same way,
+``cpu_baseline`` times the CPU oracle (chunked fp32 PyTorch) on the clip
+workload and on the reference's CPU-sized case and the long clip on the host
+cores, ``encoder`` reports the ms per forward
 of the 8-block encoder at 4 s mono x 16 with graph replay (``--no-encoder`` to
 skip), and ``trifusion_model`` the same for the full TriFusion-FP model at the
 reference configuration (random init; ``--no-trifusion`` to skip).
@@ -39,12 +42,21 @@ WORKLOADS = {
     "clip": ("fused_mamba clip B16 L400 H16 P64 N64 R16 Hq1", WORKLOAD, None),
     "long": ("fused_mamba long clip B1 L7200 H16 P64 N64 R16 Hq1 (chunk-parallel)",
              dict(WORKLOAD, batch=1, time=7200), None),
-    "varlen": ("fused_mamba varlen B32 L400 (lengths U{50..400}, seed 4) H16 P64 N64 R16 Hq1",
-               dict(WORKLOAD, batch=32), (50, 4)),
+    "varlen": ("fused_mamba varlen B32 padded L400, 16 clips x 2 channel slots (lengths U{50..400}, channels "
+               "U{1,2}, a mono clip's second slot length 0; seed 12) H16 P64 N64 R16 Hq1",
+               dict(WORKLOAD, batch=32), (50, 12)),
 }
+# the reference's CPU-sized case: fp32 everything (reference tests/test_recurrence.py shapes)
+CPU_WORKLOAD = dict(batch=2, time=256, heads=4, head_dim=32, state=16, rotary=4, qk_heads=1)
 METRIC = "fused_mamba GB/s & %HBM peak; ms/forward 4s mono×16 encoder, 1 MI355X"
 TRAFFIC_FILE = ROOT / "profiles" / "fused_mamba_clip_b16_l400_pmc.txt"
 COUNTERS_FILE = ROOT / "profiles" / "fused_mamba_clip_b16_l400_counters.txt"
+# sources of the clip workload's kernel; a profile summary names the hash of
+# these it was measured on, and its figures are reported only if it matches
+KERNEL_SOURCES = [
+    ROOT / "trifusion-fp-kernel_amd" / "csrc" / name
+    for name in ("mamba_pipe.hip", "mfma_tile.h", "mamba_internal.h", "common.h")
+]
 
 
 def parse_args():
@@ -92,9 +104,32 @@ def calibrate_copy(torch, mib):
     print(json.dumps({"calibration_copy_bytes": n * 4, "copies": 20}), flush=True)
 
 
+def kernel_source_hash():
+    """First 16 hex digits of the SHA-256 of the clip kernel's source files."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for path in KERNEL_SOURCES:
+        h.update(path.name.encode())
+        h.update(path.read_bytes())
+    return h.hexdigest()[:16]
+
+
+def profile_matches(path):
+    """The summary at ``path`` was measured on the current kernel source: its
+    ``kernel_source_sha16:`` line equals kernel_source_hash()."""
+    if not path.exists():
+        return False
+    for line in path.read_text().splitlines():
+        if line.startswith("kernel_source_sha16:"):
+            return line.split(":", 1)[1].strip() == kernel_source_hash()
+    return False
+
+
 def traffic_bytes():
-    """HBM bytes per call from the committed rocprofv3 --pmc summary, if any."""
-    if not TRAFFIC_FILE.exists():
+    """HBM bytes per call from the committed rocprofv3 --pmc summary, if it was
+    measured on the current kernel source."""
+    if not profile_matches(TRAFFIC_FILE):
         return None
     for line in TRAFFIC_FILE.read_text().splitlines():
         if line.startswith("traffic_bytes_per_call:"):
@@ -104,8 +139,8 @@ def traffic_bytes():
 
 def utilisation_counters():
     """MfmaUtil / VALUBusy (percent) of the clip kernel from the committed
-    rocprofv3 --pmc summary, if any."""
-    if not COUNTERS_FILE.exists():
+    rocprofv3 --pmc summary, if it was measured on the current kernel source."""
+    if not profile_matches(COUNTERS_FILE):
         return None
     out = {}
     for line in COUNTERS_FILE.read_text().splitlines():
@@ -159,15 +194,24 @@ def time_fused_mamba(args, torch, fused_mamba, sets, steps, warmup, variant, eag
         return start.elapsed_time(end) / steps
 
 
-def cpu_baseline(torch, budget_s):
+def cpu_model():
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return ""
+
+
+def cpu_time_oracle(torch, w, budget_s, dtype):
+    """Median seconds per call of the CPU oracle (chunked PyTorch) at workload
+    ``w`` over a time budget (at least 3 calls), and the algorithmic bytes."""
     from oracle.recurrence import fused_mamba_chunked
     from trifusion_amd.synthetic import algorithmic_bytes, clip_inputs
 
-    threads = len(os.sched_getaffinity(0))
-    torch.set_num_threads(threads)
-    args = clip_inputs(WORKLOAD["batch"], WORKLOAD["time"], heads=WORKLOAD["heads"], head_dim=WORKLOAD["head_dim"],
-                       state=WORKLOAD["state"], rotary=WORKLOAD["rotary"], seed=1)
-    nbytes = algorithmic_bytes(args)
+    args = clip_inputs(w["batch"], w["time"], heads=w["heads"], head_dim=w["head_dim"], state=w["state"],
+                       rotary=w["rotary"], qk_heads=w["qk_heads"], dtype=dtype, seed=1)
     fused_mamba_chunked(*args)  # warm-up
     times = []
     t_end = time.perf_counter() + budget_s
@@ -176,23 +220,33 @@ def cpu_baseline(torch, budget_s):
         fused_mamba_chunked(*args)
         times.append(time.perf_counter() - t0)
     times.sort()
-    med = times[len(times) // 2]
-    model = ""
-    try:
-        for line in Path("/proc/cpuinfo").read_text().splitlines():
-            if line.startswith("model name"):
-                model = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return {
+    return times[len(times) // 2], len(times), algorithmic_bytes(args)
+
+
+def cpu_baseline(torch, budget_s):
+    """The CPU oracle on the host cores at the clip workload (the reported
+    line), and at the reference's CPU-sized case and the long clip (reference
+    benchmarks/benchmark_inference.py:52-65 times its cases the same way)."""
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    model = cpu_model()
+    med, n, nbytes = cpu_time_oracle(torch, WORKLOAD, budget_s, torch.bfloat16)
+    line = {
         "value": round(nbytes / med / 1e9, 4),
         "unit": "GB/s",
         "cores": threads,
         "kind": "port",
         "sample": f"full clip workload B16 L400 H16 P64 N64, CPU oracle (chunked fp32 PyTorch), "
-        f"median of {len(times)} calls ({med * 1e3:.1f} ms/call), {model}",
+        f"median of {n} calls ({med * 1e3:.1f} ms/call), {model}",
+        "configs": {},
     }
+    for key, w, dtype, budget in (("cpu_b2_l256_h4_p32_n16_fp32", CPU_WORKLOAD, torch.float32, budget_s / 4),
+                                  ("long_b1_l7200_h16_p64_n64", dict(WORKLOAD, batch=1, time=7200), torch.bfloat16,
+                                   budget_s / 2)):
+        med, n, nbytes = cpu_time_oracle(torch, w, budget, dtype)
+        line["configs"][key] = {"ms_per_call": round(med * 1e3, 3), "GB/s": round(nbytes / med / 1e9, 4),
+                                "calls": n, "cores": threads, **w}
+    return line
 
 
 def graph_us(torch, fn, steps=100):
@@ -314,6 +368,32 @@ def encoder_ms(torch, trifusion=False):
     return line
 
 
+def time_workload(args, torch, fused_mamba, selected_variant, w, varlen, warm=True):
+    """(ms per call cache-cold, cache-warm ms or None, algorithmic bytes, kernel
+    name, input sets) of ``fused_mamba`` at workload ``w``."""
+    from trifusion_amd.synthetic import algorithmic_bytes, channel_fold_lengths, clip_inputs
+
+    host = clip_inputs(w["batch"], w["time"], heads=w["heads"], head_dim=w["head_dim"], state=w["state"],
+                       rotary=w["rotary"], qk_heads=w["qk_heads"], seed=1)
+    dargs = tuple(x.cuda() for x in host)
+    lengths = None
+    if varlen is not None:
+        lengths_host, _ = channel_fold_lengths(w["batch"] // 2, w["time"], varlen[0], seed=varlen[1])
+        lengths = lengths_host.cuda()
+    nbytes = algorithmic_bytes(host, lengths=None if lengths is None else lengths.cpu())
+    kernel = selected_variant(*dargs, variant=args.variant, lengths=lengths)
+    nsets = args.sets or max(1, -(-2 * LLC_BYTES // nbytes))
+    sets = [dargs] + [tuple(x.clone() for x in dargs) for _ in range(nsets - 1)]
+    ms = time_fused_mamba(args, torch, fused_mamba, sets, args.steps, args.warmup, args.variant, args.eager,
+                          lengths)
+    warm_ms = None
+    if nsets > 1 and warm:
+        warm_ms = time_fused_mamba(args, torch, fused_mamba, [dargs], args.steps, args.warmup, args.variant,
+                                   args.eager, lengths)
+    del sets
+    return ms, warm_ms, nbytes, kernel, nsets
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -327,7 +407,6 @@ def main():
     import torch
 
     from trifusion_amd.mamba_fused import fused_mamba, selected_variant
-    from trifusion_amd.synthetic import algorithmic_bytes, clip_inputs, clip_lengths
 
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
@@ -345,23 +424,8 @@ def main():
         print(json.dumps({"bandwidth_kernels": bandwidth_kernels(torch)}), flush=True)
         return
     label, w, varlen = WORKLOADS[args.workload]
-    host = clip_inputs(w["batch"], w["time"], heads=w["heads"], head_dim=w["head_dim"], state=w["state"],
-                       rotary=w["rotary"], qk_heads=w["qk_heads"], seed=1)
-    dargs = tuple(x.cuda() for x in host)
-    lengths = None
-    if varlen is not None:
-        lengths = clip_lengths(w["batch"], w["time"], varlen[0], seed=varlen[1]).cuda()
-    nbytes = algorithmic_bytes(host, lengths=None if lengths is None else lengths.cpu())
-    kernel = selected_variant(*dargs, variant=args.variant)
-    nsets = args.sets or max(1, -(-2 * LLC_BYTES // nbytes))
-    sets = [dargs] + [tuple(x.clone() for x in dargs) for _ in range(nsets - 1)]
-    ms = time_fused_mamba(args, torch, fused_mamba, sets, args.steps, args.warmup, args.variant, args.eager,
-                          lengths)
-    warm_ms = None
-    if nsets > 1 and not args.no_warm:
-        warm_ms = time_fused_mamba(args, torch, fused_mamba, [dargs], args.steps, args.warmup, args.variant,
-                                   args.eager, lengths)
-    del sets
+    ms, warm_ms, nbytes, kernel, nsets = time_workload(args, torch, fused_mamba, selected_variant, w, varlen,
+                                                       warm=not args.no_warm)
     gbs = nbytes / (ms * 1e-3) / 1e9
     line = {
         "metric": METRIC,
@@ -395,7 +459,17 @@ def main():
         },
     }
     if args.workload == "clip":
+        line["roofline"]["kernel_source_sha16"] = kernel_source_hash()
         line["counters"] = utilisation_counters()
+        line["workloads"] = {}
+        for name in ("varlen", "long"):
+            wlabel, ww, wvarlen = WORKLOADS[name]
+            wms, _, wbytes, wkernel, _ = time_workload(args, torch, fused_mamba, selected_variant, ww, wvarlen,
+                                                        warm=False)
+            wgbs = wbytes / (wms * 1e-3) / 1e9
+            line["workloads"][name] = {"workload": wlabel, "kernel": wkernel, "ms_per_call": round(wms, 6),
+                                       "algorithmic_bytes_per_call": wbytes, "GB/s": round(wgbs, 2),
+                                       "frac": round(wgbs / HBM_PEAK_GBS, 4)}
     if not args.no_kernels and args.workload == "clip":
         line["bandwidth_kernels"] = bandwidth_kernels(torch)
     if not args.no_encoder:
