@@ -1,6 +1,18 @@
-"""Command line of the MI355X package (``src/trifusion_l4/cli.py``):
-``info`` prints versions without touching the GPU; ``predict`` runs
-``submission.run`` over a template directory with a local checkpoint."""
+"""``trifusion-amd`` command line.
+
+Two commands, with the subcommand names and flags of the reference's
+``trifusion-l4`` (src/trifusion_l4/cli.py:12-25, pyproject.toml:42-43):
+
+* ``info`` prints a JSON description of the installation: package version,
+  Python, OS, dependency versions and whether the native library is built.
+  It imports neither torch nor the library, so it never opens a GPU.
+* ``predict --weights W --root R`` writes ``R/output/submission.csv`` and
+  ``R/output/runtime_report.json`` (see ``submission.run``).
+
+Flag values are checked while they are parsed (``type=`` converters), so a
+bad value exits with status 2 and names its flag before any model, audio or
+GPU work starts.
+"""
 
 import argparse
 from importlib import metadata
@@ -11,52 +23,94 @@ import platform
 from . import __version__
 
 DEPENDENCIES = ("torch", "numpy", "scipy", "soundfile", "einops")
+LIBRARY = Path(__file__).with_name("libtrifusion_amd.so")
+
+
+def _file(text):
+    path = Path(text)
+    if not path.is_file():
+        raise argparse.ArgumentTypeError(f"no checkpoint file at {text}")
+    return path.resolve()
+
+
+def _directory(text):
+    path = Path(text)
+    if not path.is_dir():
+        raise argparse.ArgumentTypeError(f"{text} is not a directory")
+    return path.resolve()
+
+
+def _count(text):
+    try:
+        value = int(text)
+    except ValueError:
+        raise argparse.ArgumentTypeError(f"{text!r} is not an integer") from None
+    if value < 1:
+        raise argparse.ArgumentTypeError(f"{value} is too small (the least accepted value is 1)")
+    return value
+
+
+def _installed(name):
+    try:
+        return metadata.version(name)
+    except metadata.PackageNotFoundError:
+        return None
+
+
+def info(_args):
+    report = {
+        "version": __version__,
+        "python": platform.python_version(),
+        "platform": platform.system(),
+        "dependencies": {name: _installed(name) for name in DEPENDENCIES},
+        "native_library": str(LIBRARY) if LIBRARY.exists() else None,
+    }
+    print(json.dumps(report, indent=2))
+    return 0
+
+
+def predict(args):
+    from .submission import run
+
+    run(args.root, args.weights, graphs=args.graphs, padded_seconds=args.padded_seconds,
+        max_batch=args.max_batch, workers=args.workers)
+    return 0
+
+
+def _predict_flags(sub):
+    sub.add_argument("--weights", type=_file, required=True, metavar="CHECKPOINT",
+                     help="student checkpoint written by runtime.save_student")
+    sub.add_argument("--root", type=_directory, required=True,
+                     help="dataset folder; its data/ or open/ subfolder holds sample_submission.csv and the audio")
+    sub.add_argument("--graphs", action=argparse.BooleanOptionalAction, default=True,
+                     help="replay one captured HIP graph per length bucket (--no-graphs: eager launches)")
+    sub.add_argument("--padded-seconds", type=_count, default=64,
+                     help="longest padded clip, in seconds, that a batch may hold")
+    sub.add_argument("--max-batch", type=_count, default=16, help="most clips per batch")
+    sub.add_argument("--workers", type=_count, default=4, help="audio decoding threads")
+
+
+COMMANDS = {
+    "info": ("describe the installation as JSON (opens no GPU)", None, info),
+    "predict": ("score every row of a submission template on the GPU", _predict_flags, predict),
+}
 
 
 def parser():
-    p = argparse.ArgumentParser(prog="trifusion-amd")
-    p.add_argument("--version", action="version", version=f"%(prog)s {__version__}")
-    commands = p.add_subparsers(dest="command", required=True)
-    commands.add_parser("info", help="Print installed versions without initializing the GPU")
-    predict = commands.add_parser("predict", help="Run offline inference with your local checkpoint")
-    predict.add_argument("--weights", type=Path, required=True)
-    predict.add_argument("--root", type=Path, required=True, help="Directory containing data/ or open/")
-    predict.add_argument("--graphs", action=argparse.BooleanOptionalAction, default=True)
-    predict.add_argument("--padded-seconds", type=int, default=64)
-    predict.add_argument("--max-batch", type=int, default=16)
-    predict.add_argument("--workers", type=int, default=4)
-    return p
-
-
-def _versions():
-    found = {}
-    for name in DEPENDENCIES:
-        try:
-            found[name] = metadata.version(name)
-        except metadata.PackageNotFoundError:
-            found[name] = None
-    return found
+    top = argparse.ArgumentParser(prog="trifusion-amd", description="TriFusion-FP inference on AMD Instinct MI355X")
+    top.add_argument("--version", action="version", version=f"%(prog)s {__version__}")
+    subs = top.add_subparsers(dest="command", required=True, metavar="COMMAND")
+    for name, (summary, flags, handler) in COMMANDS.items():
+        sub = subs.add_parser(name, help=summary, description=summary)
+        if flags is not None:
+            flags(sub)
+        sub.set_defaults(handler=handler)
+    return top
 
 
 def main(argv=None):
-    command = parser()
-    args = command.parse_args(argv)
-    if args.command == "info":
-        info = {"version": __version__, "python": platform.python_version(), "platform": platform.system(),
-                "dependencies": _versions()}
-        print(json.dumps(info, indent=2))
-        return 0
-    if not args.weights.is_file():
-        command.error(f"Checkpoint does not exist: {args.weights}")
-    if not args.root.is_dir():
-        command.error(f"Input root does not exist: {args.root}")
-    if min(args.padded_seconds, args.max_batch, args.workers) < 1:
-        command.error("Batch limits and worker count must be positive")
-    from .submission import run
-
-    run(args.root.resolve(), args.weights.resolve(), graphs=args.graphs, padded_seconds=args.padded_seconds,
-        max_batch=args.max_batch, workers=args.workers)
-    return 0
+    args = parser().parse_args(argv)
+    return args.handler(args)
 
 
 if __name__ == "__main__":
