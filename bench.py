@@ -250,19 +250,20 @@ def cpu_baseline(torch, budget_s):
 
 
 def graph_us(torch, fn, steps=100):
-    """Average µs of ``fn()`` over a replayed graph of ``steps`` calls (HIP events)."""
+    """Average µs of ``fn(i)`` for i = 0 .. steps-1 over a replayed graph of
+    ``steps`` calls (HIP events on the launch stream)."""
     stream = torch.cuda.current_stream()
     with torch.inference_mode():
-        for _ in range(3):
-            fn()
+        for i in range(3):
+            fn(i)
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         side = torch.cuda.Stream()
         side.wait_stream(stream)
         with torch.cuda.stream(side):
             with torch.cuda.graph(graph, stream=side):
-                for _ in range(steps):
-                    fn()
+                for i in range(steps):
+                    fn(i)
         stream.wait_stream(side)
         graph.replay()
         torch.cuda.synchronize()
@@ -275,11 +276,17 @@ def graph_us(torch, fn, steps=100):
         return start.elapsed_time(end) * 1e3 / steps
 
 
+COLD_BYTES = 640 << 20  # input copies cycled per cold timing: 2.5x the 256 MB last-level cache
+
+
 def bandwidth_kernels(torch):
     """Each single-pass kernel of the encoder at its 4 s mono x 16 shape (16 x 400
     frames, dim 512, in-proj width 2240 in rows of 2304, FFN 2 x 1365 run at
     2 x 1408): algorithmic bytes (each input element read once, each output
-    written once) / time vs 8 TB/s."""
+    written once) / time vs 8 TB/s. ``us`` repeats one input (cache-warm, as in
+    a forward where the producer just wrote it); ``us_cold`` cycles through
+    enough copies of the inputs that each call reads them from HBM. The first
+    line, a one-element fill, is what any launch costs in this protocol."""
     from trifusion_amd.kernels import rms, swiglu
     from trifusion_amd.kernels.buffers import mamba_controls, mask_buffer
     from trifusion_amd.kernels.native import add, add_rms, mask_rms, rms_pair
@@ -289,41 +296,62 @@ def bandwidth_kernels(torch):
     g = torch.Generator(device="cuda").manual_seed(5)
     b, t, dim, proj, ffn, heads, n = 16, 400, 512, 2304, 1408, 16, 64
     rows = b * t
-    x = torch.randn(b, t, dim, device="cuda", generator=g)
-    br = torch.randn(b, t, dim, device="cuda", generator=g).bfloat16()
     w = torch.ones(dim, device="cuda")
-    p = torch.randn(b, t, proj, device="cuda", generator=g).bfloat16()
-    bcview = p[..., 2 * 1024: 2 * 1024 + 2 * n]  # B and C columns of the in-proj output
-    a_cols = p[..., 2 * 1024 + 2 * n + heads: 2 * 1024 + 2 * n + 2 * heads]
-    d_cols = p[..., 2 * 1024 + 2 * n: 2 * 1024 + 2 * n + heads]
-    gu = torch.randn(b, t, 2 * ffn, device="cuda", generator=g).bfloat16()
+    wn = torch.ones(n, device="cuda")
+    bias = torch.zeros(heads, device="cuda")
     lengths = torch.full((b,), t, dtype=torch.int64, device="cuda")
     mask = time_mask(lengths, t)
-    bias = torch.zeros(heads, device="cuda")
-    audio = torch.rand(b, 1, 64000, device="cuda", generator=g) * 2 - 1
     chans = torch.ones(b, dtype=torch.int64, device="cuda")
-    wn = torch.ones(n, device="cuda")
+    bc0, ad0 = 2 * 1024, 2 * 1024 + 2 * n  # B|C columns, then the D and A columns of the in-proj output
+
+    def x32():
+        return (torch.randn(b, t, dim, device="cuda", generator=g),)
+
+    def xb():
+        return torch.randn(b, t, dim, device="cuda", generator=g), torch.randn(b, t, dim, device="cuda",
+                                                                             generator=g).bfloat16()
+
+    def pb():
+        return (torch.randn(b, t, proj, device="cuda", generator=g).bfloat16(),)
+
     cases = [
-        ("rms fp32->bf16 [6400,512]", lambda: rms(x, w, out_dtype=torch.bfloat16), rows * dim * (4 + 2)),
-        ("add_rms fp32+bf16 -> fp32,bf16 [6400,512]", lambda: add_rms(x, br, w, mask),
+        ("launch floor: 1-element fill", lambda: (torch.empty(1, device="cuda"),), lambda o: o.fill_(1.0), 4),
+        ("rms fp32->bf16 [6400,512]", x32, lambda x: rms(x, w, out_dtype=torch.bfloat16), rows * dim * (4 + 2)),
+        ("add_rms fp32+bf16 -> fp32,bf16 [6400,512]", xb, lambda x, br: add_rms(x, br, w, mask),
          rows * dim * (4 + 2 + 4 + 2) + rows),
-        ("rms pair bf16 strided B|C columns [6400,2x64]", lambda: rms_pair(bcview, wn, wn), rows * 2 * n * (2 + 2)),
-        ("swiglu bf16 [6400,2816] -> [6400,1408]", lambda: swiglu(gu), rows * 3 * ffn * 2),
-        ("mamba_controls bf16 [16,400,16] x2 -> fp32 [16,16,400] x2", lambda: mamba_controls(a_cols, d_cols, bias, 1e-4),
+        ("rms pair bf16 strided B|C columns [6400,2x64]", pb, lambda p: rms_pair(p[..., bc0: bc0 + 2 * n], wn, wn),
+         rows * 2 * n * (2 + 2)),
+        ("swiglu bf16 [6400,2816] -> [6400,1408]",
+         lambda: (torch.randn(b, t, 2 * ffn, device="cuda", generator=g).bfloat16(),), lambda gu: swiglu(gu),
+         rows * 3 * ffn * 2),
+        ("mamba_controls bf16 [16,400,16] x2 -> fp32 [16,16,400] x2", pb,
+         lambda p: mamba_controls(p[..., ad0 + heads: ad0 + 2 * heads], p[..., ad0: ad0 + heads], bias, 1e-4),
          rows * heads * (2 + 2 + 4 + 4)),
-        ("masked_mean fp32 [16,400,512] -> [16,512]", lambda: masked_mean(x, lengths), rows * dim * 4 + b * dim * 4),
-        ("mask_rows fp32 [6400,512]", lambda: mask_buffer(x, mask), rows * dim * 8 + rows),
-        ("add fp32+bf16 -> fp32 [6400,512]", lambda: add(x, br, mask), rows * dim * (4 + 2 + 4) + rows),
-        ("mask_rms bf16 -> fp32,bf16 [6400,512]", lambda: mask_rms(br, mask, w), rows * dim * (2 + 4 + 2) + rows),
-        ("frame_audio fp32 [16,1,64000] -> bf16 [16,400,448]", lambda: frame_audio(audio, chans, 400, 160, 120, 448),
-         b * 64000 * 4 + rows * 448 * 2),
+        ("masked_mean fp32 [16,400,512] -> [16,512]", x32, lambda x: masked_mean(x, lengths),
+         rows * dim * 4 + b * dim * 4),
+        ("mask_rows fp32 [6400,512]", x32, lambda x: mask_buffer(x, mask), rows * dim * 8 + rows),
+        ("add fp32+bf16 -> fp32 [6400,512]", xb, lambda x, br: add(x, br, mask), rows * dim * (4 + 2 + 4) + rows),
+        ("mask_rms bf16 -> fp32,bf16 [6400,512]", lambda: (x32()[0].bfloat16(),), lambda x: mask_rms(x, mask, w),
+         rows * dim * (2 + 4 + 2) + rows),
+        ("frame_audio fp32 [16,1,64000] -> bf16 [16,400,448]",
+         lambda: (torch.rand(b, 1, 64000, device="cuda", generator=g) * 2 - 1,),
+         lambda audio: frame_audio(audio, chans, 400, 160, 120, 448), b * 64000 * 4 + rows * 448 * 2),
     ]
     out = []
-    for name, fn, nbytes in cases:
-        us = graph_us(torch, fn)
-        gbs = nbytes / (us * 1e-6) / 1e9
-        out.append({"kernel": name, "us": round(us, 2), "bytes": nbytes, "GB/s": round(gbs, 1),
-                    "frac": round(gbs / HBM_PEAK_GBS, 4)})
+    for name, make, fn, nbytes in cases:
+        one = make()
+        us = graph_us(torch, lambda i: fn(*one))
+        line = {"kernel": name, "us": round(us, 2), "bytes": nbytes,
+                "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1), "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+        if nbytes > 4:
+            copies = [one] + [make() for _ in range(min(255, -(-COLD_BYTES // nbytes) - 1))]
+            cold = graph_us(torch, lambda i: fn(*copies[i % len(copies)]), steps=max(100, len(copies)))
+            line.update({"us_cold": round(cold, 2), "frac_cold": round(nbytes / (cold * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                         "cold_copies": len(copies)})
+            del copies
+        del one
+        torch.cuda.empty_cache()
+        out.append(line)
     return out
 
 

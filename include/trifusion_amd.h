@@ -210,9 +210,18 @@ int tf_mamba_controls(const void *a, const void *ddt, int32_t dtype, int64_t sb,
  * Masked mean over time: y[b, :] = sum_{t < lengths[b]} x[b, t, :] / lengths[b]
  * in fp32; x contiguous [B, T, D], y fp32 [B, D]. Replaces the global-feature
  * pooling of src/trifusion_l4/decoder.py:60-62.
+ * When B * D is too small to occupy the whole GPU with one workgroup per
+ * 128-byte column slice, the time axis is split and the partial sums go to
+ * `workspace` (tf_masked_mean_workspace_size bytes, 4-byte aligned), then are
+ * added in split order. With a NULL or smaller workspace the mean is computed
+ * without the split. For a given split, the result does not depend on timing.
  */
 int tf_masked_mean(const void *x, int32_t dtype, const int64_t *lengths, float *y,
-                   int64_t batch, int64_t time, int64_t d, void *stream);
+                   int64_t batch, int64_t time, int64_t d, void *workspace,
+                   int64_t workspace_bytes, void *stream);
+
+/* Workspace bytes tf_masked_mean uses for these sizes (0: no time split). */
+int64_t tf_masked_mean_workspace_size(int32_t dtype, int64_t batch, int64_t time, int64_t d);
 
 /* Row mask from lengths: mask[b*T + t] = t < lengths[b] (uint8). Replaces
  * time_mask (src/trifusion_l4/masking.py:6-7) on the device. */

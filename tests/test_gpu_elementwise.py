@@ -111,11 +111,75 @@ def test_mamba_controls(dtype):
     torch.testing.assert_close(adt.cpu(), adt_ref, rtol=2e-6, atol=1e-7)
 
 
+MEAN_SHAPES = [
+    # batch, time, d: the encoder pool (one split in fp32, two in bf16), a long
+    # single clip (16 time splits), few frames (no split), d that is not a whole
+    # number of 16-byte lanes (the per-column kernel)
+    (16, 400, 512),
+    (1, 3000, 96),
+    (3, 50, 8),
+    (4, 130, 6),
+]
+
+
+def mean64(x, lengths):
+    """fp64 masked mean of the valid prefix (lengths >= 1)."""
+    t = x.shape[1]
+    mask = (torch.arange(t)[None, :] < lengths[:, None]).double()
+    return (x.double() * mask[..., None]).sum(1) / lengths[:, None].double()
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_masked_mean(dtype):
-    g = gen(9)
-    x = torch.randn(16, 400, 512, generator=g).to(dtype)
-    lengths = torch.randint(1, 401, (16,), generator=g)
-    lengths[0] = 400
-    y = masked_mean(x.to(DEV), lengths.to(DEV)).cpu()
-    torch.testing.assert_close(y, E.masked_mean(x, lengths), rtol=1e-5, atol=1e-6)
+@pytest.mark.parametrize("b,t,d", MEAN_SHAPES)
+def test_masked_mean(dtype, b, t, d):
+    """Against the oracle (fp32) and an fp64 sum: a dropped or repeated frame
+    moves a mean by |x| / length, at least 3e-4 here, far above the tolerance.
+    Two calls are bitwise equal (the split sums are added in a fixed order)."""
+    g = gen(9 + t)
+    x = torch.randn(b, t, d, generator=g).to(dtype)
+    lengths = torch.randint(1, t + 1, (b,), generator=g)
+    lengths[0] = t
+    print(f"case masked_mean b={b} t={t} d={d} dtype={dtype}", flush=True)
+    dx, dl = x.to(DEV), lengths.to(DEV)
+    y = masked_mean(dx, dl)
+    assert torch.equal(y, masked_mean(dx, dl))
+    y = y.cpu()
+    torch.testing.assert_close(y, E.masked_mean(x, lengths), rtol=1e-5, atol=2e-6)
+    assert (y.double() - mean64(x, lengths)).abs().max().item() <= 2e-6
+
+
+def test_masked_mean_split_and_unsplit_agree():
+    """A shape that splits time (bf16 encoder pool) computed with and without
+    the workspace: both within fp32 rounding of the fp64 mean; zero and
+    negative lengths give the oracle's non-finite or zero rows."""
+    import ctypes
+
+    from trifusion_amd import _lib
+
+    lib = _lib.load()
+    g = gen(11)
+    b, t, d = 16, 400, 512
+    x = torch.randn(b, t, d, generator=g).to(torch.bfloat16)
+    lengths = torch.randint(1, t + 1, (b,), generator=g)
+    lengths[1], lengths[2] = 0, -3
+    code = _lib.dtype_code(x, "masked_mean")
+    need = lib.tf_masked_mean_workspace_size(code, b, t, d)
+    assert need == 2 * b * d * 4
+    dx, dl = x.to(DEV), lengths.to(DEV)
+    work = torch.empty(need // 4, device=DEV)
+    outs = []
+    for ws, nbytes in ((work.data_ptr(), need), (None, 0), (work.data_ptr(), need - 4)):
+        y = torch.empty(b, d, device=DEV)
+        status = lib.tf_masked_mean(dx.data_ptr(), code, dl.data_ptr(), y.data_ptr(), b, t, d, ws, nbytes,
+                                    ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        assert status == 0
+        torch.cuda.synchronize()
+        outs.append(y.cpu())
+    ref = E.masked_mean(x, lengths)
+    valid = lengths > 0
+    for y in outs:
+        torch.testing.assert_close(y, ref, rtol=1e-5, atol=2e-6, equal_nan=True)
+        assert (y[valid].double() - mean64(x[valid], lengths[valid])).abs().max().item() <= 2e-6
+        assert torch.isnan(y[1]).all() and (y[2] == 0).all()
+    # too small a workspace: the unsplit form, bit for bit (NaN rows included)
+    torch.testing.assert_close(outs[1], outs[2], rtol=0, atol=0, equal_nan=True)

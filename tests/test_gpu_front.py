@@ -14,15 +14,30 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-@pytest.mark.parametrize("chans,width,n", [(1, 400, 4000), (2, 400, 4000), (2, 448, 4000), (2, 448, 3999)])
-def test_frame_audio_is_exact(chans, width, n):
-    """Vector loads inside the clip, scalar loads at its edges and for a
-    sample count that leaves rows unaligned (n = 3999)."""
-    g = torch.Generator().manual_seed(chans)
+FRAMING = [
+    # chans, width, samples, kernel, stride, pad
+    (1, 400, 4000, 400, 160, 120),   # staged blocks, float4 span loads
+    (2, 400, 4000, 400, 160, 120),
+    (2, 448, 4000, 400, 160, 120),   # zero columns past the kernel
+    (2, 448, 3999, 400, 160, 120),   # samples % 4 != 0: scalar span loads
+    (2, 408, 4000, 401, 160, 122),   # kernel % 8 != 0 (a chunk straddles it), pad % 4 != 0
+    (1, 448, 64000, 400, 160, 120),  # the encoder's 4 s clip: 400 frames, 50 blocks of 8
+    (2, 400, 3000, 400, 100, 120),   # stride % 8 != 0: one workgroup per frame
+    (1, 64, 300, 64, 16, 0),         # fewer frames than a block's last one needs
+]
+
+
+@pytest.mark.parametrize("chans,width,n,kernel,stride,pad", FRAMING)
+def test_frame_audio_is_exact(chans, width, n, kernel, stride, pad):
+    """Bitwise equal to the oracle for the staged block form (vector and scalar
+    span loads, a kernel that is not a multiple of 8, zero columns) and the
+    per-frame form (stride not a multiple of 8)."""
+    g = torch.Generator().manual_seed(chans * 7 + n)
     audio = torch.randn(3, chans, n, generator=g)
     channels = torch.tensor([chans, 1, chans])
-    got = frame_audio(audio.to(DEV), channels.to(DEV), 400, 160, 120, width).cpu()
-    assert torch.equal(got, O.frame_audio(audio, channels, 400, 160, 120, width))
+    print(f"case frame_audio chans={chans} width={width} n={n} kernel={kernel} stride={stride} pad={pad}", flush=True)
+    got = frame_audio(audio.to(DEV), channels.to(DEV), kernel, stride, pad, width).cpu()
+    assert torch.equal(got, O.frame_audio(audio, channels, kernel, stride, pad, width))
 
 
 def test_frames_mask_is_exact():

@@ -363,51 +363,121 @@ __global__ __launch_bounds__(256) void masked_mean_kernel(const T* __restrict__ 
                      static_cast<float>(len);
 }
 
-// Masked mean with 4-column vectors (d % 4 == 0, aligned): block = 16 waves
-// over (batch b, 256 columns), wave w sums frames t = w (mod 16) with four
-// rows' loads in flight; LDS adds the 16 partials in wave order.
+// Masked mean over 128-byte column slices. Workgroup (slice, b, split) sums
+// frames [split*span, (split+1)*span) of clip b, clipped to its valid prefix,
+// for the V*8 columns of the slice (V = 16 / sizeof(T) per lane): lane l of
+// wave w loads 16 bytes at column V*(l % 8) of frame 8*w + l / 8 + 128*j, four
+// frames in flight per lane. The 8 lanes of a column block meet by xor
+// shuffles, the 16 waves through LDS in wave order, so the sum's order is fixed
+// by (span, split count) alone. One split: y = sum / lengths[b]; more: the sum
+// goes to partial[split, b, :] and masked_mean_finish_kernel adds the splits in
+// order.
 template <typename T>
-__global__ __launch_bounds__(1024) void masked_mean_vec_kernel(const T* __restrict__ x,
-                                                               const int64_t* __restrict__ lengths,
-                                                               float* __restrict__ y, int64_t time, int64_t d) {
-  __shared__ float4 part[16][64];
+__global__ __launch_bounds__(1024) void masked_mean_slice_kernel(const T* __restrict__ x,
+                                                                 const int64_t* __restrict__ lengths,
+                                                                 float* __restrict__ y, float* __restrict__ partial,
+                                                                 int64_t time, int64_t d, int64_t span) {
+  constexpr int V = 16 / sizeof(T);
+  constexpr int kWaves = 16;
+  constexpr int kStep = 8 * kWaves;  // frames per pass of the workgroup
+  __shared__ float part[kWaves][8][V];
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
   const int64_t b = blockIdx.y;
-  const int64_t col = (static_cast<int64_t>(blockIdx.x) * 64 + lane) * 4;
+  const int split = blockIdx.z;
+  const int64_t col = static_cast<int64_t>(blockIdx.x) * 8 * V + V * (lane & 7);
   const int64_t len = lengths[b];
   const int64_t L = len < 0 ? 0 : (len > time ? time : len);
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  const int64_t t0 = split * span;
+  const int64_t t1 = t0 + span < L ? t0 + span : L;
+  float acc[V];
+#pragma unroll
+  for (int e = 0; e < V; ++e) acc[e] = 0.f;
   if (col < d) {
     const T* base = x + b * time * d + col;
-#pragma unroll 4
-    for (int64_t t = w; t < L; t += 16) {
-      float v[4];
-      if constexpr (sizeof(T) == 4) {
-        const float4 f = *reinterpret_cast<const float4*>(base + t * d);
-        v[0] = f.x, v[1] = f.y, v[2] = f.z, v[3] = f.w;
-      } else {
-        const uint2 u = *reinterpret_cast<const uint2*>(base + t * d);
-        v[0] = to_f32(__builtin_bit_cast(T, static_cast<uint16_t>(u.x & 0xffffu)));
-        v[1] = to_f32(__builtin_bit_cast(T, static_cast<uint16_t>(u.x >> 16)));
-        v[2] = to_f32(__builtin_bit_cast(T, static_cast<uint16_t>(u.y & 0xffffu)));
-        v[3] = to_f32(__builtin_bit_cast(T, static_cast<uint16_t>(u.y >> 16)));
-      }
-      acc.x += v[0], acc.y += v[1], acc.z += v[2], acc.w += v[3];
-    }
-  }
-  part[w][lane] = acc;
-  __syncthreads();
-  if (w == 0 && col < d) {
-    float4 s = part[0][lane];
+    for (int64_t t = t0 + 8 * w + (lane >> 3); t < t1; t += 4 * kStep) {
+      float v[4][V];
 #pragma unroll
-    for (int k = 1; k < 16; ++k) {
-      const float4 p = part[k][lane];
-      s.x += p.x, s.y += p.y, s.z += p.z, s.w += p.w;
+      for (int u = 0; u < 4; ++u) {
+        // every lane loads from a valid frame (t < t1); frames past t1 are dropped after the load
+        const int64_t tu = t + u * kStep;
+        const T* src = base + (tu < t1 ? tu : t) * d;
+        if constexpr (sizeof(T) == 4) {
+          const float4 f = *reinterpret_cast<const float4*>(src);
+          v[u][0] = f.x, v[u][1] = f.y, v[u][2] = f.z, v[u][3] = f.w;
+        } else {
+          const uint4 q = *reinterpret_cast<const uint4*>(src);
+          const uint32_t wd[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            v[u][2 * e] = to_f32(__builtin_bit_cast(T, static_cast<uint16_t>(wd[e] & 0xffffu)));
+            v[u][2 * e + 1] = to_f32(__builtin_bit_cast(T, static_cast<uint16_t>(wd[e] >> 16)));
+          }
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (t + u * kStep < t1)
+#pragma unroll
+          for (int e = 0; e < V; ++e) acc[e] += v[u][e];
     }
-    const float n = static_cast<float>(len);
-    *reinterpret_cast<float4*>(y + b * d + col) = make_float4(s.x / n, s.y / n, s.z / n, s.w / n);
   }
+#pragma unroll
+  for (int e = 0; e < V; ++e) {
+    acc[e] += __shfl_xor(acc[e], 8);
+    acc[e] += __shfl_xor(acc[e], 16);
+    acc[e] += __shfl_xor(acc[e], 32);
+  }
+  if (lane < 8)
+#pragma unroll
+    for (int e = 0; e < V; ++e) part[w][lane][e] = acc[e];
+  __syncthreads();
+  const int c = threadIdx.x;  // column of the slice this thread finishes
+  if (c >= 8 * V) return;
+  const int64_t out_col = static_cast<int64_t>(blockIdx.x) * 8 * V + c;
+  if (out_col >= d) return;
+  float sum = 0.f;
+#pragma unroll
+  for (int i = 0; i < kWaves; ++i) sum += part[i][c / V][c % V];
+  if (gridDim.z == 1)
+    y[b * d + out_col] = sum / static_cast<float>(len);
+  else
+    partial[(static_cast<int64_t>(split) * gridDim.y + b) * d + out_col] = sum;
+}
+
+// y[b, c] = (partial[0, b, c] + ... + partial[splits-1, b, c]) / lengths[b].
+__global__ __launch_bounds__(256) void masked_mean_finish_kernel(const float* __restrict__ partial,
+                                                                 const int64_t* __restrict__ lengths,
+                                                                 float* __restrict__ y, int64_t batch, int64_t d,
+                                                                 int splits) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= batch * d) return;
+  float sum = 0.f;
+  for (int s = 0; s < splits; ++s) sum += partial[s * batch * d + i];
+  y[i] = sum / static_cast<float>(lengths[i / d]);
+}
+
+// Time splits of the slice kernel: enough workgroups to give each CU one
+// (256), each split at least 64 frames, at most 16 splits.
+struct MeanPlan {
+  int64_t slices = 0;
+  int splits = 1;
+  int64_t span = 0;
+};
+
+MeanPlan mean_plan(int64_t batch, int64_t time, int64_t d, int64_t elem_bytes) {
+  MeanPlan m;
+  const int64_t cols = 128 / elem_bytes;
+  m.slices = (d + cols - 1) / cols;
+  const int64_t groups = m.slices * batch;
+  int64_t splits = groups > 0 ? (256 + groups - 1) / groups : 1;
+  const int64_t by_time = time / 64;
+  if (splits > by_time) splits = by_time;
+  if (splits > 16) splits = 16;
+  m.splits = splits < 1 ? 1 : static_cast<int>(splits);
+  m.span = (time + m.splits - 1) / m.splits;
+  if (m.span < 1) m.span = 1;
+  return m;
 }
 
 __global__ __launch_bounds__(256) void time_mask_kernel(const int64_t* __restrict__ lengths,
@@ -625,23 +695,51 @@ extern "C" int tf_mamba_controls(const void* a, const void* ddt, int32_t dtype, 
   return TF_ERR_DTYPE;
 }
 
-extern "C" int tf_masked_mean(const void* x, int32_t dtype, const int64_t* lengths, float* y,
-                              int64_t batch, int64_t time, int64_t d, void* stream) {
+namespace {
+
+bool mean_slices_ok(const void* x, int32_t dtype, int64_t d) {
+  return tf::dtype_ok(dtype) && d % (16 / tf::dtype_size(dtype)) == 0 && tf::aligned16(x);
+}
+
+}  // namespace
+
+extern "C" int64_t tf_masked_mean_workspace_size(int32_t dtype, int64_t batch, int64_t time, int64_t d) {
+  if (!tf::dtype_ok(dtype) || batch < 0 || time < 0 || d < 1) return -TF_ERR_SHAPE;
+  const tf::MeanPlan m = tf::mean_plan(batch, time, d, tf::dtype_size(dtype));
+  return m.splits > 1 ? static_cast<int64_t>(m.splits) * batch * d * 4 : 0;
+}
+
+extern "C" int tf_masked_mean(const void* x, int32_t dtype, const int64_t* lengths, float* y, int64_t batch,
+                              int64_t time, int64_t d, void* workspace, int64_t workspace_bytes, void* stream) {
   if (!x || !lengths || !y) return TF_ERR_NULL;
   if (batch < 0 || time < 0 || d < 1 || batch > 65535) return TF_ERR_SHAPE;
   if (batch == 0) return TF_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool vec = d % 4 == 0 && tf::aligned16(x) && tf::aligned16(y);
+  if (mean_slices_ok(x, dtype, d)) {
+    tf::MeanPlan m = tf::mean_plan(batch, time, d, tf::dtype_size(dtype));
+    const int64_t need = static_cast<int64_t>(m.splits) * batch * d * 4;
+    if (m.splits > 1 && (workspace == nullptr || workspace_bytes < need ||
+                         (reinterpret_cast<uintptr_t>(workspace) & 3) != 0)) {
+      m.splits = 1;  // no room for the partial sums: one workgroup per slice over all frames
+      m.span = time > 0 ? time : 1;
+    }
+    if (m.slices > 0x7fffffff) return TF_ERR_SHAPE;
+    const dim3 grid(static_cast<uint32_t>(m.slices), static_cast<uint32_t>(batch), static_cast<uint32_t>(m.splits));
+    float* partial = static_cast<float*>(workspace);
+    TF_DISPATCH(dtype, T,
+                hipLaunchKernelGGL(tf::masked_mean_slice_kernel<T>, grid, dim3(1024), 0, s,
+                                   static_cast<const T*>(x), lengths, y, partial, time, d, m.span);
+                if (m.splits > 1) hipLaunchKernelGGL(tf::masked_mean_finish_kernel,
+                                                     dim3(tf::blocks_for(batch * d, 256)), dim3(256), 0, s,
+                                                     partial, lengths, y, batch, d, m.splits);
+                return tf::launch_status());
+    return TF_ERR_DTYPE;
+  }
   TF_DISPATCH(dtype, T,
-              if (vec) {
-                const dim3 grid(tf::blocks_for(d, 256), static_cast<uint32_t>(batch));
-                hipLaunchKernelGGL(tf::masked_mean_vec_kernel<T>, grid, dim3(1024), 0, s,
-                                   static_cast<const T*>(x), lengths, y, time, d);
-              } else {
-                const dim3 grid(tf::blocks_for(d, 64), static_cast<uint32_t>(batch));
-                hipLaunchKernelGGL(tf::masked_mean_kernel<T>, grid, dim3(256), 0, s, static_cast<const T*>(x),
-                                   lengths, y, time, d);
-              } return tf::launch_status());
+              const dim3 grid(tf::blocks_for(d, 64), static_cast<uint32_t>(batch));
+              hipLaunchKernelGGL(tf::masked_mean_kernel<T>, grid, dim3(256), 0, s, static_cast<const T*>(x),
+                                 lengths, y, time, d);
+              return tf::launch_status());
   return TF_ERR_DTYPE;
 }
 

@@ -65,6 +65,80 @@ __global__ __launch_bounds__(64) void frame_audio_kernel(const float* __restrict
   }
 }
 
+// The same framing for a block of F consecutive frames per workgroup when the
+// stride is a multiple of 8 samples: the block's audio span (F-1)*stride + K
+// samples is read once, coalesced, mixed to mono and rounded to bf16 into LDS
+// (zero outside [0, N)); frame t0 + r, columns k0..k0+7, is then the 16 bytes
+// at LDS sample r*stride + k0 (16-byte aligned), written as one 16-byte store,
+// consecutive threads covering consecutive output bytes. VEC: the span is read
+// as float4 (N, pad and the audio base 16-byte aligned, so each 4-sample group
+// lies wholly inside or wholly outside the clip). 512 threads: one pass of
+// span loads and one of output stores for the stem's 8-frame blocks.
+template <bool VEC>
+__global__ __launch_bounds__(512) void frame_block_kernel(const float* __restrict__ audio,
+                                                          const int64_t* __restrict__ channels,
+                                                          uint16_t* __restrict__ framed, int C, int N, int T, int K,
+                                                          int width, int stride, int pad, int F) {
+  extern __shared__ uint16_t span_bf16[];
+  const int b = blockIdx.y;
+  const int t0 = static_cast<int>(blockIdx.x) * F;
+  const int nf = T - t0 < F ? T - t0 : F;
+  const int64_t chl = channels[b];
+  const int nch = chl < C ? static_cast<int>(chl < 0 ? 0 : chl) : C;
+  const float denom = static_cast<float>(chl);
+  const float* src = audio + static_cast<int64_t>(b) * C * N;
+  const int n0 = t0 * stride - pad;
+  const int span = (nf - 1) * stride + K;
+  if constexpr (VEC) {
+    for (int g = threadIdx.x; 4 * g < span; g += 512) {
+      const int n = n0 + 4 * g;
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+      const bool inside = n >= 0 && n < N;
+      if (inside)
+        for (int c = 0; c < nch; ++c) {
+          const float4 a = *reinterpret_cast<const float4*>(src + static_cast<int64_t>(c) * N + n);
+          acc.x += a.x, acc.y += a.y, acc.z += a.z, acc.w += a.w;
+        }
+      const uint32_t lo = inside ? f32_to_bf16(acc.x / denom) | (uint32_t(f32_to_bf16(acc.y / denom)) << 16) : 0u;
+      const uint32_t hi = inside ? f32_to_bf16(acc.z / denom) | (uint32_t(f32_to_bf16(acc.w / denom)) << 16) : 0u;
+      *reinterpret_cast<uint2*>(span_bf16 + 4 * g) = make_uint2(lo, hi);
+    }
+  } else {
+    for (int i = threadIdx.x; i < span; i += 512) {
+      const int n = n0 + i;
+      uint16_t v = 0;
+      if (n >= 0 && n < N) {
+        float acc = 0.f;
+        for (int c = 0; c < nch; ++c) acc += src[static_cast<int64_t>(c) * N + n];
+        v = f32_to_bf16(acc / denom);
+      }
+      span_bf16[i] = v;
+    }
+  }
+  __syncthreads();
+  const int per_row = width / 8;
+  uint16_t* dst = framed + (static_cast<int64_t>(b) * T + t0) * width;
+  for (int q = threadIdx.x; q < nf * per_row; q += 512) {
+    const int r = q / per_row;
+    const int k0 = 8 * (q - r * per_row);
+    const uint16_t* row = span_bf16 + r * stride;
+    uint4 out;
+    if (k0 + 8 <= K) {
+      out = *reinterpret_cast<const uint4*>(row + k0);
+    } else {
+      uint32_t wd[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t lo = k0 + 2 * e < K ? row[k0 + 2 * e] : 0u;
+        const uint32_t hi = k0 + 2 * e + 1 < K ? row[k0 + 2 * e + 1] : 0u;
+        wd[e] = lo | (hi << 16);
+      }
+      out = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+    }
+    *reinterpret_cast<uint4*>(dst + static_cast<int64_t>(q) * 8) = out;
+  }
+}
+
 // frames[b] = clamp(floor(lengths[b] / stride), 1, T); mask[b, t] = t < frames[b].
 __global__ __launch_bounds__(256) void frames_mask_kernel(const int64_t* __restrict__ lengths,
                                                           int64_t* __restrict__ frames,
@@ -122,8 +196,23 @@ extern "C" int tf_frame_audio(const float* audio, const int64_t* channels, void*
   const int64_t rows = batch * frames;
   if (rows == 0) return TF_OK;
   if (rows > 0x7fffffff) return TF_ERR_SHAPE;
-  hipLaunchKernelGGL(tf::frame_audio_kernel, dim3(static_cast<uint32_t>(rows)), dim3(64), 0,
-                     static_cast<hipStream_t>(stream), audio, channels, static_cast<uint16_t*>(framed),
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  // frames per workgroup of the staged form, and its LDS span (samples, padded to 4)
+  constexpr int64_t kBlockFrames = 8;
+  const int64_t nf = frames < kBlockFrames ? frames : kBlockFrames;
+  const int64_t span = ((nf - 1) * stride + kernel + 3) / 4 * 4;
+  if (stride % 8 == 0 && span * 2 <= 64 * 1024 && batch <= 65535) {
+    const bool vec = samples % 4 == 0 && pad % 4 == 0 && (reinterpret_cast<uintptr_t>(audio) & 15) == 0;
+    const dim3 grid(static_cast<uint32_t>((frames + nf - 1) / nf), static_cast<uint32_t>(batch));
+    const size_t lds = static_cast<size_t>(span) * 2;
+    auto kernel_fn = vec ? tf::frame_block_kernel<true> : tf::frame_block_kernel<false>;
+    hipLaunchKernelGGL(kernel_fn, grid, dim3(512), lds, s, audio, channels, static_cast<uint16_t*>(framed),
+                       static_cast<int>(chans), static_cast<int>(samples), static_cast<int>(frames),
+                       static_cast<int>(kernel), static_cast<int>(width), static_cast<int>(stride),
+                       static_cast<int>(pad), static_cast<int>(nf));
+    return tf::launch_status();
+  }
+  hipLaunchKernelGGL(tf::frame_audio_kernel, dim3(static_cast<uint32_t>(rows)), dim3(64), 0, s, audio, channels, static_cast<uint16_t*>(framed),
                      static_cast<int>(chans), static_cast<int>(samples), static_cast<int>(frames),
                      static_cast<int>(kernel), static_cast<int>(width), static_cast<int>(stride),
                      static_cast<int>(pad));

@@ -91,7 +91,8 @@ _SIGNATURES = {
         [c_ptr, c_ptr, c_i32, c_i64, c_i64, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_f32, c_ptr],
         c_i32,
     ),
-    "tf_masked_mean": ([c_ptr, c_i32, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_ptr], c_i32),
+    "tf_masked_mean": ([c_ptr, c_i32, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_ptr, c_i64, c_ptr], c_i32),
+    "tf_masked_mean_workspace_size": ([c_i32, c_i64, c_i64, c_i64], c_i64),
     "tf_time_mask": ([c_ptr, c_ptr, c_i64, c_i64, c_ptr], c_i32),
     "tf_reverse_valid": ([c_ptr, c_ptr, c_i32, c_ptr, c_i64, c_i64, c_i64, c_ptr], c_i32),
     "tf_mean_rmsnorm": ([c_ptr, c_i32, c_ptr, c_i32, c_ptr, c_ptr, c_i64, c_i64, c_f32, c_ptr], c_i32),

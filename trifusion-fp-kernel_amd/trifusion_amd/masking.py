@@ -41,9 +41,15 @@ def launch_masked_mean(x, lengths):
     x = x.contiguous()
     lengths = lengths.to(torch.int64).contiguous()
     b, t, d = x.shape
+    code = _lib.dtype_code(x, "masked_mean")
     y = torch.empty((b, d), device=x.device, dtype=torch.float32)
+    need = lib.tf_masked_mean_workspace_size(code, b, t, d)
+    if need < 0:
+        _lib.check(-need, "masked_mean")
+    work = torch.empty(need // 4, device=x.device, dtype=torch.float32) if need else None
     status = lib.tf_masked_mean(
-        x.data_ptr(), _lib.dtype_code(x, "masked_mean"), lengths.data_ptr(), y.data_ptr(), b, t, d, _lib.stream_of(x)
+        x.data_ptr(), code, lengths.data_ptr(), y.data_ptr(), b, t, d, work.data_ptr() if work is not None else None,
+        need, _lib.stream_of(x),
     )
     _lib.check(status, "masked_mean")
     return y
