@@ -73,7 +73,7 @@ def step_controls(dt, trap):
     return gamma, dn * (1 - tn) + gamma
 
 
-def phase_chunked(angles, dt, pairs, chunk=CHUNK):
+def phase_chunked(angles, dt, pairs, chunk=CHUNK, accumulate=torch.float64):
     """Rotary phase ``(cumsum_t pi*tanh(theta)*dt) mod 2pi`` with a per-chunk carry.
 
     Follows the structure of ``src/trifusion_l4/angle.py:103-144`` and
@@ -88,9 +88,16 @@ def phase_chunked(angles, dt, pairs, chunk=CHUNK):
     of rounding noise over long clips; after the bf16 rounding of the rotated
     q/k that noise alone moves outputs by up to ~6e-4 of max|y|, so the oracle
     keeps the phase exact to fp32 resolution and so do the HIP kernels.
+
+    ``accumulate=torch.float32`` keeps every step in fp32 instead, as the
+    reference's kernel does (``mamba_fused.py:105-109``: fp32 products, an fp32
+    in-chunk cumsum plus the carried state, fp32 reductions; exact tanh and a
+    sequential cumsum here, where the reference uses ``tanh_approx`` and a
+    parallel scan). It measures how far the reference's own phase arithmetic
+    sits from the exact phase; it is not the parity oracle.
     """
     b, t, h, r = angles.shape
-    vals = (torch.tanh(angles.double()) * math.pi) * dt.double().transpose(1, 2)[..., None]
+    vals = (torch.tanh(angles.to(accumulate)) * math.pi) * dt.to(accumulate).transpose(1, 2)[..., None]
     out = torch.empty_like(vals)
     state = vals.new_zeros(b, h, r)
     two_pi = 2 * math.pi
@@ -114,7 +121,8 @@ def rotate_pairs(x, cos, sin):
 
 
 def fused_mamba_chunked(
-    q, k, v, adt, dt, trap, qb, kb, angles, d, z, chunk=CHUNK, out_dtype=None, lengths=None
+    q, k, v, adt, dt, trap, qb, kb, angles, d, z, chunk=CHUNK, out_dtype=None, lengths=None,
+    phase_accumulate=torch.float64,
 ):
     """Chunked fp32 restatement of ``fused_mamba`` (mamba_fused.py:72-152).
 
@@ -124,6 +132,7 @@ def fused_mamba_chunked(
     (or ``out_dtype``). ``lengths`` (optional ``[B]``) zeroes rows ``t >= lengths[b]``
     after the recurrence, the masking the model applies to the output
     (``src/trifusion_l4/model.py:174``); causality leaves valid rows unchanged.
+    ``phase_accumulate`` selects the rotary phase arithmetic (``phase_chunked``).
     """
     bsz, t, hq, n = q.shape
     h, p = v.shape[2], v.shape[3]
@@ -131,7 +140,7 @@ def fused_mamba_chunked(
     qf = q.float()[:, :, idx]
     kf = k.float()[:, :, idx]
     gamma, scale = step_controls(dt.float(), trap.float())
-    phase = phase_chunked(angles, dt, n // 2, chunk)
+    phase = phase_chunked(angles, dt, n // 2, chunk, phase_accumulate)
     cos, sin = torch.cos(phase), torch.sin(phase)
     qt = qf + qb.float()[None, None]
     kt = kf + kb.float()[None, None]

@@ -97,3 +97,43 @@ def test_segments_graph_replay_matches_eager():
             graph.replay()
             torch.cuda.synchronize()
             assert torch.equal(out, eager)
+
+
+def test_segments_bitwise_equal_serial_walk_b1_l1000_h4():
+    """B1 L1000 H4 (16 chunks, 4 units) runs in two segments. The second
+    segment's entering state is the first segment's summary from zero, the
+    same operations in the same order as the serial walk's state after 8
+    chunks, so the two forms agree bit for bit."""
+    args = clip_inputs(1, 1000, heads=4, head_dim=64, state=64, rotary=16, qk_heads=1, seed=11)
+    dargs = tuple(x.to(DEV) for x in args)
+    print("case segments_vs_serial_bitwise_b1_l1000_h4", flush=True)
+    with torch.inference_mode():
+        out = torch.empty(dargs[2].shape, device=DEV, dtype=torch.float32)
+        assert _workspace_bytes(dargs, out, None) > 0
+        y = fused_mamba(*dargs, out=out, variant="mfma").clone()
+        ys = _serial(dargs, torch.empty_like(out), None)
+    torch.cuda.synchronize()
+    assert torch.equal(y, ys)
+
+
+def test_long_clip_distance_from_reference_phase_arithmetic():
+    """The long clip B1 L7200 H16 P64 N64 R16 (bf16 operands, chunk-parallel
+    form) against the oracle with the exact (fp64) phase, the parity bar, and
+    against the oracle with the reference's fp32 phase arithmetic
+    (mamba_fused.py:105-109). The two oracles differ by 9.4e-4 of max|y| here,
+    so the HIP output sits within 2e-3 of the second."""
+    args = clip_inputs(1, 7200, heads=16, head_dim=64, state=64, rotary=16, qk_heads=1, seed=7,
+                       dtype=torch.bfloat16)
+    dargs = tuple(x.to(DEV) for x in args)
+    print("case long_clip_b1_l7200_h16 phase arithmetic distances", flush=True)
+    with torch.inference_mode():
+        out = torch.empty(dargs[2].shape, device=DEV, dtype=torch.float32)  # fp32 out: no output rounding
+        y = fused_mamba(*dargs, out=out).cpu()
+    exact = fused_mamba_chunked(*args)
+    fp32_phase = fused_mamba_chunked(*args, phase_accumulate=torch.float32)
+    d_exact, d_fp32, d_oracles = max_rel(y, exact), max_rel(y, fp32_phase), max_rel(fp32_phase, exact)
+    print(f"  HIP vs exact-phase oracle max_rel {d_exact:.3e} rel_fro {rel_fro(y, exact):.3e}; "
+          f"HIP vs fp32-phase oracle max_rel {d_fp32:.3e} rel_fro {rel_fro(y, fp32_phase):.3e}; "
+          f"oracles apart {d_oracles:.3e}", flush=True)
+    assert d_exact <= MAX_REL
+    assert d_fp32 <= 2 * MAX_REL

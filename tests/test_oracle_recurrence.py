@@ -130,6 +130,32 @@ def test_phase_matches_f64_cumsum():
     assert torch.allclose(ph[..., :r].double().sin(), exact.sin(), atol=2e-4)
 
 
+def test_fp32_phase_arithmetic_against_closed_form():
+    """The reference-arithmetic phase option: a constant increment c per step has
+    phase (t + 1) c mod 2 pi. The fp64 form meets it to its final fp32 rounding;
+    the fp32 form drifts, since the rounding of the increment and of each carry
+    has one sign at every step here (7.8e-4 rad after 7200 steps; random
+    increments, as at the long-clip workload, drift ~6e-6), but stays within
+    2e-3 rad. A dropped carry or a missing reduction misses by whole radians."""
+    t, theta, step = 7200, 0.7, 0.37
+    angles = torch.full((1, t, 1, 2), theta)
+    dt = torch.full((1, 1, t), step)
+    theta32, step32 = (float(torch.tensor(x, dtype=torch.float32)) for x in (theta, step))
+    c = math.pi * math.tanh(theta32) * step32
+    exact = torch.tensor([((i + 1) * c) % (2 * math.pi) for i in range(t)], dtype=torch.float64)
+
+    def wrapped_gap(ph):
+        d = (ph[0, :, 0, 0].double() - exact).abs()
+        return torch.minimum(d, 2 * math.pi - d).max().item()
+
+    ph64 = R.phase_chunked(angles, dt, pairs=2)
+    ph32 = R.phase_chunked(angles, dt, pairs=2, accumulate=torch.float32)
+    assert wrapped_gap(ph64) <= 1e-6  # the final fp32 rounding of a value below 2 pi
+    assert 1e-5 <= wrapped_gap(ph32) <= 2e-3
+    assert not torch.equal(ph32, ph64)
+    assert torch.all((ph32 >= 0) & (ph32 <= 2 * math.pi))
+
+
 def test_rotation_is_interleaved_and_norm_preserving():
     x = torch.tensor([[1.0, 2.0, 3.0, 4.0]])
     c = torch.tensor([[0.0, 1.0]])
@@ -259,7 +285,7 @@ def test_planted_half_split_pairs_is_caught(monkeypatch):
 
 
 def test_planted_missing_phase_carry_is_caught(monkeypatch):
-    def no_carry(angles, dt, pairs, chunk=R.CHUNK):
+    def no_carry(angles, dt, pairs, chunk=R.CHUNK, accumulate=None):
         vals = (torch.tanh(angles.float()) * math.pi) * dt.float().transpose(1, 2)[..., None]
         out = torch.cat([torch.cumsum(vals[:, c : c + chunk], 1) for c in range(0, vals.shape[1], chunk)], 1)
         return F.pad(out, (0, pairs - angles.shape[-1]))
