@@ -41,6 +41,11 @@ namespace {
 
 constexpr int kTrigStride = 68;  // floats per row of the cos/sin table: 32 pairs x 2 + 4 pad
 
+// Fourth word of a raw (unswizzled, stride 0) buffer descriptor on gfx9-family
+// parts: 32-bit data format; loads and stores past num_records are dropped.
+constexpr int kRawBufferWord3 = 0x00020000;
+constexpr int kOutOfRange = static_cast<int>(0x80000000u);  // a lane offset no buffer here reaches
+
 typedef __attribute__((ext_vector_type(4))) short s16x4;
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
@@ -158,7 +163,7 @@ struct PipeRows {
   u32x4 q, k, v;
 };
 
-template <int RPW, bool CTL16, bool TRAP16, bool ANG16>
+template <int RPW, bool CTL16, bool TRAP16, bool ANG16, bool OUT32>
 __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
   __shared__ PipeSmem sh;
   const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
@@ -191,7 +196,6 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
   const int ado = b * P.a_sb + h * P.a_sh - roff * P.a_st;
   const int trb = b * P.r_sb + h * P.r_sh - roff * P.r_st;
   const int gbase = b * P.g_sb + h * P.g_sh - roff * P.g_st;
-  const int obase = b * P.o_sb + h * P.o_sh - roff * P.o_st;
   const float step_bias = P.ctl_raw ? P.dt_bias[h] : 0.f;
   const float skip_d = P.d[h];
 
@@ -199,8 +203,8 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
     constexpr int NSEG = 64 / RPW;  // row segments per pair
     const int pi = lane / NSEG;
     const int sg = lane & (NSEG - 1);
-    const int pair = s_idx * RPW + pi;
-    const bool phase_wave = state_wave && s_idx * RPW < R;  // wave-uniform
+    const int pair = p_idx * RPW + pi;                // phase pair of a prologue wave's lane
+    const bool phase_wave = w >= 8 && p_idx * RPW < R;  // wave-uniform
 
     const int ng = (w + 4) & 7;  // channel group of the rotary stage (waves 0-7)
     auto load_rows = [&](int c) {
@@ -337,135 +341,136 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
       sh.skip[cr][ng][lane] = part;
     };
 
-    // loads ahead of use: rows of chunk c at A(c-1), controls of chunk c at
-    // A(c-2), angles of chunk c at B(c-2), z of chunk c at B(c)
-    PipeRows rows = load_rows(0);
-    PipeCtl ctl_next = {};
+    // Each role runs its own copy of the walk, with the same two barriers per
+    // iteration, and issues its global loads (and, output waves, its stores)
+    // unconditionally: rows clamped to ones that exist, stores past the length
+    // dropped by the buffer's range check. So the wait the compiler places
+    // before each use counts exactly the role's own younger memory operations
+    // and never waits for one issued later than the one it needs.
+    // Loads ahead of use: rows and z of chunk c at A(c-1), controls at A(c-2),
+    // angles at the start of A(c).
     float th[RPW];
 #pragma unroll
     for (int i = 0; i < RPW; ++i) th[i] = 0.f;
-    if (w == 11) {
+    PipeRows rows = {};
+    PipeCtl ctl_next = {};
+    if (w >= 8) {
+      // every prologue wave loads the controls rows (wave 11 uses them), so
+      // their count in each wave's outstanding loads is the same on every path
       const PipeCtl c0 = load_pipe_ctl<CTL16, TRAP16>(P, dto, ado, trb, lane, L, tlim);
-      if (nvalid > 1) ctl_next = load_pipe_ctl<CTL16, TRAP16>(P, dto, ado, trb, kChunk + lane, L, tlim);
-      controls(c0, 0);
+      ctl_next = load_pipe_ctl<CTL16, TRAP16>(P, dto, ado, trb, kChunk + lane, L, tlim);
+      load_pipe_angles<RPW, ANG16>(P, th, gbase, pair, sg * RPW, L);
+      if (w == 11) controls(c0, 0);
     }
-    if (phase_wave) load_pipe_angles<RPW, ANG16>(P, th, gbase, pair, sg * RPW, L);
     lds_barrier();
-    if (phase_wave) {
-      phase(th, 0);
-      if (nvalid > 1) load_pipe_angles<RPW, ANG16>(P, th, gbase, pair, kChunk + sg * RPW, L);
-    }
-    if (state_wave) {  // S_0 = 0
-      sh.sb[0][s_idx][0][lane] = u32x4{0u, 0u, 0u, 0u};
+    if (phase_wave) phase(th, 0);
+    if (state_wave) {
+      sh.sb[0][s_idx][0][lane] = u32x4{0u, 0u, 0u, 0u};  // S_0 = 0
       sh.sb[0][s_idx][1][lane] = u32x4{0u, 0u, 0u, 0u};
     }
     lds_barrier();
 
-    f32x16 S = zero16();  // state waves: tile (nt, pt) of S^T[n][p]
-    u32x2 zr[4] = {};     // output waves: gate rows of the chunk being finished
-    const int nt = (s_idx >> 1) & 1, spt = s_idx & 1;
-    const int th_o = w >> 1, opt = w & 1;
-
-    f32x16 ybase = zero16();  // output waves: skip and inter-chunk terms of the chunk being finished
-    for (int i = 0; i <= nvalid; ++i) {
-      // ---------------- interval A(i) ----------------
-      if (w < 8 && i < nvalid) {
-        rotary(rows, i);
-        if (i + 1 < nvalid) rows = load_rows(i + 1);
+    if (out_wave) {
+      const int th_o = w >> 1, opt = w & 1;
+      // the unit's valid output rows as one buffer: memory row r (r = t, or
+      // L - 1 - t reversed) at element r * o_row from memory row 0; its size
+      // ends with row L - 1, so any row t >= L is out of range
+      const int o_row = P.rev ? -P.o_st : P.o_st;
+      constexpr int esz = OUT32 ? 4 : 2;
+      const __amdgpu_buffer_rsrc_t out_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+          static_cast<char*>(P.out) + static_cast<int64_t>(b * P.o_sb + h * P.o_sh) * esz, static_cast<short>(0),
+          ((L - 1) * o_row + 64) * esz, kRawBufferWord3);
+      // gate rows of chunk c (lane = row 32 th + c32 of the chunk, the tile's
+      // columns), loaded at A(c) and turned into silu factors at A(c + 1)
+      auto load_z = [&](int c, u32x2 (&zr)[4]) {
+        const int t = min(c * kChunk + 32 * th_o + c32, L - 1);
+        const uint16_t* zrow = zbase + t * P.z_st + 32 * opt + 4 * hh;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) zr[g] = *reinterpret_cast<const u32x2*>(zrow + 8 * g);
+      };
+      // rows, then z, then stores: the order of every later iteration
+      rows = load_rows(0);
+      __builtin_amdgcn_sched_barrier(0);
+      u32x2 zr[4];
+      load_z(0, zr);
+      __builtin_amdgcn_sched_barrier(0);
+      // four dropped stores, so the walk starts with the same outstanding
+      // operations (rows, z, stores) as every later iteration
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        if constexpr (OUT32)
+          __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, out_rsrc, kOutOfRange, 0, 0);
+        else
+          __builtin_amdgcn_raw_buffer_store_b64(u32x2{0u, 0u}, out_rsrc, kOutOfRange, 0, 0);
       }
-      if (out_wave && i >= 1) {
-        // chunk c = i - 1, tile (th, pt) of y^T[p][t]: (D + gamma (q + qb).(k + kb)) v
-        // (mamba_fused.py:124, 147) + 2^cs qr . bf16(S_c)^T (mamba_fused.py:143)
-        const int c = i - 1;
-        const int cb = c & 1, cr = c % 3;
-        const int tl = 32 * th_o + c32;
-        u32x4 sx[4], qy[4];
-        u32x2 vv[4];
+      float gate[16];           // silu(z) of the chunk being finished (mamba_fused.py:148)
+      f32x16 ybase = zero16();  // skip and inter-chunk terms of the chunk being finished
 #pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          sx[s] = sh.sb[cr][2 * (s >> 1) + opt][s & 1][lane];
-          qy[s] = row_operand(sh.qr[cb], tl, s, hh);
-        }
-#pragma unroll
-        for (int g = 0; g < 4; ++g) vv[g] = rb_read(sh.v[cb], tl, 8 * opt + 2 * g + hh);
-        float part = 0.f;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) part += sh.skip[cr][j][tl];
-        const float coef = skip_d + sh.gam[cr][tl] * part;
-        const float decay = fast_exp2(sh.cs[cr][tl]);
-        f32x16 yi = zero16();
-#pragma unroll
-        for (int s = 0; s < 4; ++s) yi = mfma(sx[s], qy[s], yi);
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          ybase[4 * g] = coef * lo_f(vv[g][0]) + yi[4 * g] * decay;
-          ybase[4 * g + 1] = coef * hi_f(vv[g][0]) + yi[4 * g + 1] * decay;
-          ybase[4 * g + 2] = coef * lo_f(vv[g][1]) + yi[4 * g + 2] * decay;
-          ybase[4 * g + 3] = coef * hi_f(vv[g][1]) + yi[4 * g + 3] * decay;
-        }
-      }
-      if (w >= 8 && p_idx < 3 && i >= 1) {
-        // scores of chunk i - 1: tile (th, uh) = (0,0), (1,0), (1,1)
-        const int c = i - 1;
-        const int cb = c & 1;
-        const int sth = p_idx > 0 ? 1 : 0;
-        const int suh = p_idx > 1 ? 1 : 0;
-        u32x4 kx[4], qy[4];
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          kx[s] = row_operand(sh.kr[cb], 32 * suh + c32, s, hh);
-          qy[s] = row_operand(sh.qr[cb], 32 * sth + c32, s, hh);
-        }
-        f32x16 acc = zero16();
-#pragma unroll
-        for (int s = 0; s < 4; ++s) acc = mfma(kx[s], qy[s], acc);
-        u32x4 sc[2];
-        const float* csr = sh.cs[c % 3];
-        score_tile(acc, csr[32 * sth + c32], csr + 32 * suh, sth == suh, c32, hh, sc);
-        sh.score[cb][p_idx][0][lane] = sc[0];
-        sh.score[cb][p_idx][1][lane] = sc[1];
-      }
-      if (w == 11 && i + 1 < nvalid) {
-        controls(ctl_next, i + 1);
-        if (i + 2 < nvalid) ctl_next = load_pipe_ctl<CTL16, TRAP16>(P, dto, ado, trb, (i + 2) * kChunk + lane, L, tlim);
-      }
-      lds_barrier();
-
-      // ---------------- interval B(i) ----------------
-      if (state_wave && i + 1 < nvalid) {
-        // S_{i+1} = S_i 2^tot + kr^T . bf16(v 2^(tot - cs)) of chunk i (mamba_fused.py:150-152)
-        const int cb = i & 1;
-        u32x4 kx[4], vy[4];
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          kx[s] = tr_operand(sh.kr[cb], nt, s, lane);
-          vy[s] = tr_operand(sh.vs[cb], spt, s, lane);
-        }
-        const float dec = fast_exp2(sh.tot[i % 3][0]);
-        f32x16 d = zero16();
-#pragma unroll
-        for (int s = 0; s < 4; ++s) d = mfma(kx[s], vy[s], d);
-#pragma unroll
-        for (int e = 0; e < 16; ++e) S[e] = S[e] * dec + d[e];
-        u32x4 lo, hi;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          lo[q] = pack2(S[2 * q], S[2 * q + 1]);
-          hi[q] = pack2(S[8 + 2 * q], S[8 + 2 * q + 1]);
-        }
-        sh.sb[(i + 1) % 3][s_idx][0][lane] = lo;
-        sh.sb[(i + 1) % 3][s_idx][1][lane] = hi;
-      }
-      if (phase_wave && i + 1 < nvalid) {
-        phase(th, i + 1);
-        if (i + 2 < nvalid) load_pipe_angles<RPW, ANG16>(P, th, gbase, pair, (i + 2) * kChunk + sg * RPW, L);
-      }
-      if (out_wave) {
+      for (int e = 0; e < 16; ++e) gate[e] = 0.f;
+      for (int i = 0; i <= nvalid; ++i) {
+        // ---------------- interval A(i) ----------------
+        if (i < nvalid) rotary(rows, i);
         if (i >= 1) {
-          // chunk c = i - 1: intra-chunk scores . v (mamba_fused.py:144-146), gate, store
+          // silu factors of chunk i - 1 from its gate rows (loaded at A(i - 1))
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const uint32_t zw = zr[g][q >> 1];
+              const float zz = (q & 1) ? hi_f(zw) : lo_f(zw);
+              gate[4 * g + q] = zz * sigmoid_fast(zz);
+            }
+          }
+          // computed here, in interval A: left to itself the compiler sinks
+          // this next to its use in B, which keeps the old gate rows live past
+          // the next load_z and adds a copy that waits for those loads
+#pragma unroll
+          for (int e = 0; e < 16; ++e) asm volatile("" : "+v"(gate[e]));
+        }
+        rows = load_rows(i + 1);
+        load_z(i, zr);
+        if (i >= 1) {
+          // chunk c = i - 1, tile (th, pt) of y^T[p][t]: (D + gamma (q + qb).(k + kb)) v
+          // (mamba_fused.py:124, 147) + 2^cs qr . bf16(S_c)^T (mamba_fused.py:143)
           const int c = i - 1;
-          const int cb = c & 1;
+          const int cb = c & 1, cr = c % 3;
           const int tl = 32 * th_o + c32;
+          u32x4 sx[4], qy[4];
+          u32x2 vv[4];
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            sx[s] = sh.sb[cr][2 * (s >> 1) + opt][s & 1][lane];
+            qy[s] = row_operand(sh.qr[cb], tl, s, hh);
+          }
+#pragma unroll
+          for (int g = 0; g < 4; ++g) vv[g] = rb_read(sh.v[cb], tl, 8 * opt + 2 * g + hh);
+          float part = 0.f;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) part += sh.skip[cr][j][tl];
+          const float coef = skip_d + sh.gam[cr][tl] * part;
+          const float decay = fast_exp2(sh.cs[cr][tl]);
+          f32x16 yi = zero16();
+#pragma unroll
+          for (int s = 0; s < 4; ++s) yi = mfma(sx[s], qy[s], yi);
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            ybase[4 * g] = coef * lo_f(vv[g][0]) + yi[4 * g] * decay;
+            ybase[4 * g + 1] = coef * hi_f(vv[g][0]) + yi[4 * g + 1] * decay;
+            ybase[4 * g + 2] = coef * lo_f(vv[g][1]) + yi[4 * g + 2] * decay;
+            ybase[4 * g + 3] = coef * hi_f(vv[g][1]) + yi[4 * g + 3] * decay;
+          }
+        }
+        lds_barrier();
+
+        // ---------------- interval B(i) ----------------
+        // chunk c = i - 1: intra-chunk scores . v (mamba_fused.py:144-146), gate, store
+        const int c = i - 1;
+        const int t = c * kChunk + 32 * th_o + c32;
+        float yv[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) yv[e] = 0.f;
+        if (i >= 1) {
+          const int cb = c & 1;
           f32x16 y = ybase;
           if (th_o == 0) {
             const u32x4 s0 = sh.score[cb][0][0][lane], s1 = sh.score[cb][0][1][lane];
@@ -485,42 +490,106 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
             y = mfma(v2, s2, y);
             y = mfma(v3, s3, y);
           }
-          const int t = c * kChunk + tl;
-          float yv[16];
 #pragma unroll
-          for (int g = 0; g < 4; ++g) {
+          for (int e = 0; e < 16; ++e) yv[e] = y[e] * gate[e];
+        }
+        // Every lane stores in every iteration, through the unit's range-checked
+        // output buffer: rows t >= L (and the whole first iteration, which has
+        // no chunk to finish) take an offset past any buffer size and the
+        // hardware drops them; rows in [L, T) are zero-filled after the walk.
+        const int mrow = P.rev ? L - 1 - t : t;  // row in memory order
+        const int lane_off = (i >= 1 && t < L) ? (mrow * o_row + 32 * opt + 4 * hh) * esz : kOutOfRange;
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              const int e = 4 * g + q;
-              const uint32_t zw = zr[g][q >> 1];
-              const float zz = (q & 1) ? hi_f(zw) : lo_f(zw);
-              // silu gate (mamba_fused.py:148)
-              yv[e] = y[e] * (zz * sigmoid_fast(zz));
-            }
-          }
-          if (t < L) {  // rows in [L, T) are zero-filled after the walk
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-              const int off = obase + t * P.o_st + 32 * opt + 8 * g + 4 * hh;
-              if (P.out_f32) {
-                *reinterpret_cast<float4*>(static_cast<float*>(P.out) + off) =
-                    make_float4(yv[4 * g], yv[4 * g + 1], yv[4 * g + 2], yv[4 * g + 3]);
-              } else {
-                *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(P.out) + off) =
-                    u32x2{pack2(yv[4 * g], yv[4 * g + 1]), pack2(yv[4 * g + 2], yv[4 * g + 3])};
-              }
-            }
+        for (int g = 0; g < 4; ++g) {
+          if constexpr (OUT32) {
+            __builtin_amdgcn_raw_buffer_store_b128(
+                u32x4{__builtin_bit_cast(uint32_t, yv[4 * g]), __builtin_bit_cast(uint32_t, yv[4 * g + 1]),
+                      __builtin_bit_cast(uint32_t, yv[4 * g + 2]), __builtin_bit_cast(uint32_t, yv[4 * g + 3])},
+                out_rsrc, lane_off + 32 * g, 0, 0);
+          } else {
+            __builtin_amdgcn_raw_buffer_store_b64(
+                u32x2{pack2(yv[4 * g], yv[4 * g + 1]), pack2(yv[4 * g + 2], yv[4 * g + 3])}, out_rsrc,
+                lane_off + 16 * g, 0, 0);
           }
         }
-        if (i < nvalid) {
-          // gate rows of chunk i, consumed at B(i + 1)
-          const int t = min(i * kChunk + 32 * th_o + c32, L - 1);
-          const uint16_t* zrow = zbase + t * P.z_st + 32 * opt + 4 * hh;
-#pragma unroll
-          for (int g = 0; g < 4; ++g) zr[g] = *reinterpret_cast<const u32x2*>(zrow + 8 * g);
-        }
+        lds_barrier();
       }
-      lds_barrier();
+    } else if (state_wave) {
+      const int nt = (s_idx >> 1) & 1, spt = s_idx & 1;
+      f32x16 S = zero16();  // tile (nt, pt) of S^T[n][p]
+      rows = load_rows(0);
+      for (int i = 0; i <= nvalid; ++i) {
+        // ---------------- interval A(i) ----------------
+        if (i < nvalid) rotary(rows, i);
+        rows = load_rows(i + 1);
+        lds_barrier();
+
+        // ---------------- interval B(i) ----------------
+        if (i + 1 < nvalid) {
+          // S_{i+1} = S_i 2^tot + kr^T . bf16(v 2^(tot - cs)) of chunk i (mamba_fused.py:150-152)
+          const int cb = i & 1;
+          u32x4 kx[4], vy[4];
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            kx[s] = tr_operand(sh.kr[cb], nt, s, lane);
+            vy[s] = tr_operand(sh.vs[cb], spt, s, lane);
+          }
+          const float dec = fast_exp2(sh.tot[i % 3][0]);
+          f32x16 d = zero16();
+#pragma unroll
+          for (int s = 0; s < 4; ++s) d = mfma(kx[s], vy[s], d);
+#pragma unroll
+          for (int e = 0; e < 16; ++e) S[e] = S[e] * dec + d[e];
+          u32x4 lo, hi;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            lo[q] = pack2(S[2 * q], S[2 * q + 1]);
+            hi[q] = pack2(S[8 + 2 * q], S[8 + 2 * q + 1]);
+          }
+          sh.sb[(i + 1) % 3][s_idx][0][lane] = lo;
+          sh.sb[(i + 1) % 3][s_idx][1][lane] = hi;
+        }
+        lds_barrier();
+      }
+    } else {
+      // The prologue waves carry each interval's longest chain (the score
+      // tiles and controls in A, the phase in B) but are the workgroup's
+      // youngest waves, so oldest-first issue would serve them last: raise
+      // their issue priority over the output and state waves on their SIMD.
+      __builtin_amdgcn_s_setprio(2);
+      for (int i = 0; i <= nvalid; ++i) {
+        // ---------------- interval A(i) ----------------
+        // angles of chunk i + 1, for the phase at B(i)
+        load_pipe_angles<RPW, ANG16>(P, th, gbase, pair, (i + 1) * kChunk + sg * RPW, L);
+        if (p_idx < 3 && i >= 1) {
+          // scores of chunk i - 1: tile (th, uh) = (0,0), (1,0), (1,1)
+          const int c = i - 1;
+          const int cb = c & 1;
+          const int sth = p_idx > 0 ? 1 : 0;
+          const int suh = p_idx > 1 ? 1 : 0;
+          u32x4 kx[4], qy[4];
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            kx[s] = row_operand(sh.kr[cb], 32 * suh + c32, s, hh);
+            qy[s] = row_operand(sh.qr[cb], 32 * sth + c32, s, hh);
+          }
+          f32x16 acc = zero16();
+#pragma unroll
+          for (int s = 0; s < 4; ++s) acc = mfma(kx[s], qy[s], acc);
+          u32x4 sc[2];
+          const float* csr = sh.cs[c % 3];
+          score_tile(acc, csr[32 * sth + c32], csr + 32 * suh, sth == suh, c32, hh, sc);
+          sh.score[cb][p_idx][0][lane] = sc[0];
+          sh.score[cb][p_idx][1][lane] = sc[1];
+        }
+        if (p_idx == 3 && i + 1 < nvalid) controls(ctl_next, i + 1);
+        ctl_next = load_pipe_ctl<CTL16, TRAP16>(P, dto, ado, trb, (i + 2) * kChunk + lane, L, tlim);
+        lds_barrier();
+
+        // ---------------- interval B(i) ----------------
+        if (phase_wave && i + 1 < nvalid) phase(th, i + 1);
+        lds_barrier();
+      }
     }
   }
 
@@ -531,7 +600,7 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
   for (int e = L * PD + static_cast<int>(threadIdx.x); e < T * PD; e += 768) {
     const int tt = e / PD, p = e - tt * PD;
     const int off = obase_fwd + tt * o_st + p;
-    if (P.out_f32)
+    if constexpr (OUT32)
       static_cast<float*>(P.out)[off] = 0.f;
     else
       static_cast<uint16_t*>(P.out)[off] = 0;
@@ -560,6 +629,10 @@ bool pipe_supported(const tf_mamba_args& a) {
     return false;
   const int ob = a.out_dtype == TF_FLOAT32 ? 4 : 2;
   if (!rows_vectorisable(a.out, a.out_stride, ob, 4 * ob)) return false;
+  // output rows through a range-checked buffer: rows apart by at least one
+  // row (so a row past the length is out of range) and a byte range below 2^31
+  if (a.out_stride[1] < 64 || a.out_stride[3] != 1) return false;
+  if ((a.time * a.out_stride[1] + 64) * ob >= (int64_t(1) << 31)) return false;
   return offsets_fit(a);
 }
 
@@ -568,7 +641,10 @@ namespace {
 template <int RPW, bool CTL16, bool TRAP16, bool ANG16>
 int launch_pipe_kernel(const MfmaParams& P, hipStream_t stream) {
   const dim3 grid(static_cast<uint32_t>(P.units)), block(768);
-  hipLaunchKernelGGL((mamba_pipe_kernel<RPW, CTL16, TRAP16, ANG16>), grid, block, 0, stream, P);
+  if (P.out_f32)
+    hipLaunchKernelGGL((mamba_pipe_kernel<RPW, CTL16, TRAP16, ANG16, true>), grid, block, 0, stream, P);
+  else
+    hipLaunchKernelGGL((mamba_pipe_kernel<RPW, CTL16, TRAP16, ANG16, false>), grid, block, 0, stream, P);
   return launch_status();
 }
 
@@ -591,6 +667,13 @@ int launch_pipe_rpw(const MfmaParams& P, hipStream_t stream) {
 
 int launch_pipe(const tf_mamba_args& a, hipStream_t stream) {
   MfmaParams P = make_params(a);
+  if (a.rotary == 0) {
+    // no angles to read: the state waves' (unused) angle loads read q's rows of
+    // the unit's batch row instead, so every load address exists
+    P.angles = a.q;
+    P.angles_dtype = TF_BFLOAT16;
+    P.g_sb = P.q_sb, P.g_st = P.q_st, P.g_sh = 0, P.g_sr = 1;
+  }
   const int64_t units = a.batch * a.heads;
   P.xcd_per = (units % 8 == 0 && units >= 64) ? static_cast<int>(units / 8) : 0;
   return a.rotary <= 16 ? launch_pipe_rpw<4>(P, stream) : launch_pipe_rpw<8>(P, stream);
