@@ -40,12 +40,11 @@ typedef enum tf_status {
 
 /* Kernel selection for tf_fused_mamba. */
 typedef enum tf_mamba_variant {
-  TF_MAMBA_AUTO = 0,      /* pipelined kernel when supported and the chunked kernel
-                             would not cut the sequence into time segments, else
-                             the chunked kernel when supported, else generic */
+  TF_MAMBA_AUTO = 0,      /* pipelined kernel when supported, else the chunked
+                             kernel when supported, else generic */
   TF_MAMBA_GENERIC = 1,   /* fp32-FMA kernel: any dtype, N <= 128, P <= 64 */
   TF_MAMBA_MFMA = 2,      /* bf16 MFMA chunked-scan kernel (gfx950) */
-  TF_MAMBA_PIPE = 3,      /* bf16 MFMA pipelined serial walk, N = P = 64 (gfx950) */
+  TF_MAMBA_PIPE = 3,      /* bf16 MFMA pipelined walk, N = P = 64 (gfx950) */
 } tf_mamba_variant;
 
 /*

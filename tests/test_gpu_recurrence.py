@@ -198,7 +198,7 @@ def test_empty_inputs():
     [
         (16, 400, 16, 64, 16, "pipe"),  # clip workload: pipelined walk
         (16, 101, 32, 128, 32, "mfma"),  # the model's bidirectional shape (N = 128)
-        (1, 7200, 16, 64, 16, "mfma"),  # long clip: chunked kernel, cut into time segments
+        (1, 7200, 16, 64, 16, "pipe"),  # long clip: pipelined kernel, cut into time segments
         (2, 64, 16, 64, 16, "pipe"),
     ],
 )

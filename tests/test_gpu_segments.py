@@ -1,10 +1,12 @@
-"""Chunk-parallel form of the MFMA recurrence (long sequences over few units).
+"""Chunk-parallel form of the matrix-core recurrences (long sequences over few
+units), for the chunked kernel and, at N = P = 64, the pipelined kernel.
 
 With fewer (batch, head) units than half the CUs, the time axis is cut into
-segments run by separate workgroups: a summary pass (each segment's state
-contribution, log2 decay and phase sum from zero), a scan of the segment
-records, then the output pass seeded with each segment's entering state. The
-tests check, on shapes that take this path (the workspace query is > 0):
+segments run by separate workgroups: a phase pre-pass, a summary pass (each
+segment's state contribution and log2 decay from zero), a scan of the segment
+records, then the output pass seeded with each segment's entering state and
+phase. The tests check, on shapes that take this path (the workspace query is
+> 0):
 
 * parity with the CPU oracle at the recurrence tolerance, for both phase-lane
   widths, N = 32/64/128 and variable lengths;
@@ -39,32 +41,36 @@ SEGMENT_CASES = {
 }
 
 
-def _serial(dargs, out, lengths):
+def _serial(dargs, out, lengths, variant="mfma"):
     """The same C entry with no workspace: one workgroup walks each unit."""
-    a = build_args(*dargs, out, lengths, "mfma")
+    a = build_args(*dargs, out, lengths, variant)
     lib = _lib.load()
     _lib.check(lib.tf_fused_mamba(ctypes.byref(a), _lib.stream_of(out)), "fused_mamba")
     return out
 
 
-def _workspace_bytes(dargs, out, lengths):
-    a = build_args(*dargs, out, lengths, "mfma")
+def _workspace_bytes(dargs, out, lengths, variant="mfma"):
+    a = build_args(*dargs, out, lengths, variant)
     return _lib.load().tf_fused_mamba_workspace_size(ctypes.byref(a))
 
 
-@pytest.mark.parametrize("name", list(SEGMENT_CASES))
-def test_segments_match_oracle_and_serial_walk(name):
+CASE_VARIANTS = [(name, "mfma") for name in SEGMENT_CASES] + [
+    (name, "pipe") for name, c in SEGMENT_CASES.items() if c[3] == 64 and c[4] == 64 and c[6] == 1]
+
+
+@pytest.mark.parametrize("name,variant", CASE_VARIANTS)
+def test_segments_match_oracle_and_serial_walk(name, variant):
     b, t, h, p, n, r, hq, lens = SEGMENT_CASES[name]
     args = clip_inputs(b, t, heads=h, head_dim=p, state=n, rotary=r, qk_heads=hq, seed=11)
     lengths = None if lens is None else torch.tensor(lens, dtype=torch.int64)
     dargs = tuple(x.to(DEV) for x in args)
     dlen = None if lengths is None else lengths.to(DEV)
-    print(f"case {name}", flush=True)
+    print(f"case {name} variant={variant}", flush=True)
     with torch.inference_mode():
         out = torch.empty(dargs[2].shape, device=DEV, dtype=torch.float32)
-        assert _workspace_bytes(dargs, out, dlen) > 0, "shape does not take the chunk-parallel path"
-        y = fused_mamba(*dargs, out=out, lengths=dlen, variant="mfma").cpu()
-        ys = _serial(dargs, torch.empty_like(out), dlen).cpu()
+        assert _workspace_bytes(dargs, out, dlen, variant) > 0, "shape does not take the chunk-parallel path"
+        y = fused_mamba(*dargs, out=out, lengths=dlen, variant=variant).cpu()
+        ys = _serial(dargs, torch.empty_like(out), dlen, variant).cpu()
     torch.cuda.synchronize()
     ref = fused_mamba_chunked(*args, lengths=lengths)
     assert torch.isfinite(y).all()
@@ -75,6 +81,7 @@ def test_segments_match_oracle_and_serial_walk(name):
     if lens is not None:
         for i, n_i in enumerate(lens):
             assert torch.all(y[i, n_i:] == 0)
+            assert torch.all(ys[i, n_i:] == 0)
 
 
 def test_segments_graph_replay_matches_eager():

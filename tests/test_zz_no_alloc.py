@@ -64,9 +64,16 @@ def test_static_scratch_matches_workspace_entry():
         assert torch.equal(got, ref), f"{name}: max diff {(got - ref).abs().max().item():.3e}"
 
 
-def test_static_scratch_rejects_oversized_plans():
+@pytest.mark.parametrize("variant,t,h", [("mfma", 16384, 128)])
+def test_static_scratch_rejects_oversized_plans(variant, t, h):
+    """Plans whose scratch exceeds the static area are refused before any
+    launch: the chunked kernel's at B1 T16384 H128 (its phase sums grow with the
+    chunk count). The pipelined kernel's plan has at most one record per CU
+    (16 KB of state, 128 B of phase sums, 4 B of decay each) whatever the
+    length, so it always fits."""
     lib = _lib.load()
-    b, t, h, n, p, r = 1, 16384, 128, 64, 64, 16
+    b, n, p, r = 1, 64, 64, 16
+    print(f"case oversized variant={variant} t={t} h={h}", flush=True)
     bf = dict(device=DEV, dtype=torch.bfloat16)
     f32 = dict(device=DEV, dtype=torch.float32)
     q = torch.zeros(b, t, 1, n, **bf)
@@ -76,8 +83,9 @@ def test_static_scratch_rejects_oversized_plans():
     ctl = [torch.zeros(b, h, t, **f32) for _ in range(3)]
     angles = torch.zeros(b, t, h, r, **f32)
     qb, kb, d = torch.zeros(h, n, **f32), torch.zeros(h, n, **f32), torch.ones(h, **f32)
-    out = torch.full((b, t, h, p), -1.0, **f32)
-    args = build_args(q, k, v, *ctl, qb, kb, angles, d, z, out, None, "auto", False, None, 1e-4)
+    out = torch.full((b, t, h, p), -1.0, **bf)
+    args = build_args(q, k, v, *ctl, qb, kb, angles, d, z, out, None, variant, False, None, 1e-4)
+    assert lib.tf_fused_mamba_variant(ctypes.byref(args)) == {"pipe": 3, "mfma": 2}[variant]
     need = lib.tf_fused_mamba_workspace_size(ctypes.byref(args))
     assert need > lib.tf_fused_mamba_static_scratch_bytes()
     rc = lib.tf_fused_mamba_static(ctypes.byref(args), _lib.stream_of(v))

@@ -10,7 +10,7 @@
 namespace tf {
 namespace {
 
-// Library-owned scratch of tf_fused_mamba_static: the chunk-parallel form's
+// Library-owned scratch of tf_fused_mamba_static: the chunk-parallel forms'
 // segment states, chunk phase sums and segment decays, for callers that cannot
 // allocate. Each device holds its own copy for the life of the process. In
 // host code `scratch` names a host-side stand-in, never the device memory:
@@ -66,9 +66,7 @@ int select(const tf_mamba_args* a) {
   if (a->variant == TF_MAMBA_PIPE) return pipe_supported(*a) ? TF_MAMBA_PIPE : -TF_ERR_VARIANT;
   if (a->variant == TF_MAMBA_MFMA) return mfma_supported(*a) ? TF_MAMBA_MFMA : -TF_ERR_VARIANT;
   if (a->variant == TF_MAMBA_GENERIC) return generic_supported(*a) ? TF_MAMBA_GENERIC : -TF_ERR_SHAPE;
-  // the pipelined walk, unless the chunked kernel would cut few long units
-  // into time segments (its chunk-parallel form)
-  if (pipe_supported(*a) && mfma_workspace_bytes(*a) == 0) return TF_MAMBA_PIPE;
+  if (pipe_supported(*a)) return TF_MAMBA_PIPE;
   if (mfma_supported(*a)) return TF_MAMBA_MFMA;
   if (generic_supported(*a)) return TF_MAMBA_GENERIC;
   return -TF_ERR_SHAPE;
@@ -91,8 +89,9 @@ extern "C" int tf_fused_mamba(const tf_mamba_args* a, void* stream) {
 extern "C" int64_t tf_fused_mamba_workspace_size(const tf_mamba_args* a) {
   const int which = tf::select(a);
   if (which < 0) return which;
-  if (tf::empty(a) || which != TF_MAMBA_MFMA) return 0;
-  return tf::mfma_workspace_bytes(*a);
+  if (tf::empty(a)) return 0;
+  if (which == TF_MAMBA_PIPE) return tf::pipe_workspace_bytes(*a);
+  return which == TF_MAMBA_MFMA ? tf::mfma_workspace_bytes(*a) : 0;
 }
 
 extern "C" int tf_fused_mamba_static(const tf_mamba_args* a, void* stream) {
@@ -100,9 +99,8 @@ extern "C" int tf_fused_mamba_static(const tf_mamba_args* a, void* stream) {
   if (which < 0) return -which;
   if (tf::empty(a)) return TF_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (which == TF_MAMBA_PIPE) return tf::launch_pipe(*a, s);
-  if (which != TF_MAMBA_MFMA) return tf::launch_generic(*a, s);
-  const int64_t need = tf::mfma_workspace_bytes(*a);
+  if (which == TF_MAMBA_GENERIC) return tf::launch_generic(*a, s);
+  const int64_t need = which == TF_MAMBA_PIPE ? tf::pipe_workspace_bytes(*a) : tf::mfma_workspace_bytes(*a);
   tf_mamba_args local = *a;
   local.workspace = nullptr;
   local.workspace_bytes = 0;
@@ -116,7 +114,7 @@ extern "C" int tf_fused_mamba_static(const tf_mamba_args* a, void* stream) {
     local.workspace = ptr;
     local.workspace_bytes = tf::kStaticScratchBytes;
   }
-  return tf::launch_mfma(local, s);
+  return which == TF_MAMBA_PIPE ? tf::launch_pipe(local, s) : tf::launch_mfma(local, s);
 }
 
 extern "C" int64_t tf_fused_mamba_static_scratch_bytes(void) { return tf::kStaticScratchBytes; }

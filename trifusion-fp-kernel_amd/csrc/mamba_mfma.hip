@@ -816,6 +816,7 @@ MfmaParams make_params(const tf_mamba_args& a) {
   P.seg_state = nullptr;
   P.chunk_phase = nullptr;
   P.seg_decay = nullptr;
+  P.phase_fx = nullptr;
   P.ctl_raw = a.dt_bias != nullptr;
   P.ctl_bf16 = a.dt_dtype == TF_BFLOAT16;
   P.a_floor = a.a_floor;
@@ -911,6 +912,13 @@ int launch_shape(const tf_mamba_args& a, hipStream_t stream) {
 }
 
 }  // namespace
+
+int launch_segment_scan(float4* state, const float* decay, int units, int kf4, int G, hipStream_t stream) {
+  if (kf4 % kScanSlice != 0) return TF_ERR_SHAPE;
+  hipLaunchKernelGGL(segment_scan_kernel, dim3(static_cast<uint32_t>(units) * (kf4 / kScanSlice)), dim3(kScanSlice),
+                     0, stream, state, decay, kf4, G);
+  return launch_status();
+}
 
 int64_t mfma_workspace_bytes(const tf_mamba_args& a) {
   if (!mfma_supported(a)) return 0;

@@ -163,8 +163,13 @@ struct PipeRows {
   u32x4 q, k, v;
 };
 
-template <int RPW, bool CTL16, bool TRAP16, bool ANG16, bool OUT32>
+// MODE 0 walks the unit (or, P.G > 1, one time segment of it, seeded with the
+// state and phase entering the segment) and writes the outputs; MODE 1 walks a
+// segment from zero state without outputs and writes the state it leaves and
+// its total log2 decay (the chunk-parallel form's summary pass).
+template <int RPW, bool CTL16, bool TRAP16, bool ANG16, bool OUT32, int MODE>
 __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
+  constexpr bool kSummary = MODE == 1;
   __shared__ PipeSmem sh;
   const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int lane = static_cast<int>(threadIdx.x & 63);
@@ -174,9 +179,17 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
   const bool state_wave = w >= 4 && w < 8;
   const int s_idx = w - 4;  // state wave index (state waves)
   const int p_idx = w - 8;  // prologue wave index (prologue waves)
-  const int unit = P.xcd_per > 0 ? (blockIdx.x & 7) * P.xcd_per + (blockIdx.x >> 3) : static_cast<int>(blockIdx.x);
-  const int b = unit / P.H;
-  const int h = unit - b * P.H;
+  // work item (batch row, segment, head): the heads of one batch row and
+  // segment read the same q/k rows, so they are consecutive items, and items
+  // are dealt to the 8 XCDs in contiguous ranges so that those heads share an
+  // L2. The segment's state record is [unit][segment], as the scan reads it.
+  const int item = P.xcd_per > 0 ? (blockIdx.x & 7) * P.xcd_per + (blockIdx.x >> 3) : static_cast<int>(blockIdx.x);
+  const int bseg = item / P.H;
+  const int h = item - bseg * P.H;
+  const int b = bseg / P.G;
+  const int seg = bseg - b * P.G;
+  const int unit = b * P.H + h;
+  const int rec = unit * P.G + seg;
   const int qh = h / P.group;
   const int T = P.T;
   const int R = P.R;
@@ -186,6 +199,10 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
     L = l < 0 ? 0 : (l > T ? T : static_cast<int>(l));
   }
   const int nvalid = (L + kChunk - 1) / kChunk;
+  // the segment's chunks [c0, c1) of the valid prefix
+  const int c0 = min(seg * P.SC, nvalid);
+  const int c1 = min(c0 + P.SC, nvalid);
+  const bool seeded = P.G > 1 && !kSummary;
   const int tlim = P.rev ? L : T;
   const int roff = P.rev ? max(L - 1, 0) : 0;
   const uint16_t* qbase = P.q + b * P.q_sb + qh * P.q_sh - roff * P.q_st;
@@ -199,7 +216,7 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
   const float step_bias = P.ctl_raw ? P.dt_bias[h] : 0.f;
   const float skip_d = P.d[h];
 
-  if (nvalid > 0) {
+  if (c1 > c0) {
     constexpr int NSEG = 64 / RPW;  // row segments per pair
     const int pi = lane / NSEG;
     const int sg = lane & (NSEG - 1);
@@ -210,7 +227,10 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
     auto load_rows = [&](int c) {
       const int t = min(c * kChunk + lane, L - 1);
       PipeRows r;
-      r.q = *reinterpret_cast<const u32x4*>(qbase + t * P.q_st + 8 * ng);
+      if constexpr (kSummary)
+        r.q = u32x4{0u, 0u, 0u, 0u};  // the summary needs no queries
+      else
+        r.q = *reinterpret_cast<const u32x4*>(qbase + t * P.q_st + 8 * ng);
       r.k = *reinterpret_cast<const u32x4*>(kbase + t * P.k_st + 8 * ng);
       r.v = *reinterpret_cast<const u32x4*>(vbase + t * P.v_st + 8 * ng);
       return r;
@@ -250,6 +270,20 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
 
     // rotary phase and cos/sin of chunk c (phase waves)
     uint32_t carry = 0;  // phase entering the chunk, pair `pair`, 2^-32 revolutions
+    if (P.G > 1 && phase_wave) {
+      // a segment's walk starts from the phase of the segments before it: the
+      // wrapping sum of their fixed-point sums (the same integers the serial
+      // walk adds), lanes of a pair splitting the segments
+      uint32_t part = 0;
+      if (pair < R)
+        for (int g = sg; g < seg; g += NSEG) part += P.phase_fx[(static_cast<size_t>(unit) * P.G + g) * 32 + pair];
+      const uint32_t incl = group_scan_dpp<NSEG>(part, lane);
+#pragma unroll
+      for (int j = 0; j < RPW; ++j) {
+        const uint32_t tj = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl), NSEG * j + NSEG - 1));
+        carry = pi == j ? tj : carry;
+      }
+    }
     auto phase = [&](const float (&th)[RPW], int c) {
       const int cr = c % 3;
       uint32_t loc[RPW];
@@ -334,11 +368,11 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
         vo[j] = vw;
         vso[j] = pack2(lo_f(vw) * wvt, hi_f(vw) * wvt);
       }
-      rb_write16(sh.qr[cb], lane, 2 * ng, qo);
+      if constexpr (!kSummary) rb_write16(sh.qr[cb], lane, 2 * ng, qo);
       rb_write16(sh.kr[cb], lane, 2 * ng, ko);
-      rb_write16(sh.v[cb], lane, 2 * ng, vo);
+      if constexpr (!kSummary) rb_write16(sh.v[cb], lane, 2 * ng, vo);
       rb_write16(sh.vs[cb], lane, 2 * ng, vso);
-      sh.skip[cr][ng][lane] = part;
+      if constexpr (!kSummary) sh.skip[cr][ng][lane] = part;
     };
 
     // Each role runs its own copy of the walk, with the same two barriers per
@@ -357,17 +391,13 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
     if (w >= 8) {
       // every prologue wave loads the controls rows (wave 11 uses them), so
       // their count in each wave's outstanding loads is the same on every path
-      const PipeCtl c0 = load_pipe_ctl<CTL16, TRAP16>(P, dto, ado, trb, lane, L, tlim);
-      ctl_next = load_pipe_ctl<CTL16, TRAP16>(P, dto, ado, trb, kChunk + lane, L, tlim);
-      load_pipe_angles<RPW, ANG16>(P, th, gbase, pair, sg * RPW, L);
-      if (w == 11) controls(c0, 0);
+      const PipeCtl ctl0 = load_pipe_ctl<CTL16, TRAP16>(P, dto, ado, trb, c0 * kChunk + lane, L, tlim);
+      ctl_next = load_pipe_ctl<CTL16, TRAP16>(P, dto, ado, trb, (c0 + 1) * kChunk + lane, L, tlim);
+      load_pipe_angles<RPW, ANG16>(P, th, gbase, pair, c0 * kChunk + sg * RPW, L);
+      if (w == 11) controls(ctl0, c0);
     }
     lds_barrier();
-    if (phase_wave) phase(th, 0);
-    if (state_wave) {
-      sh.sb[0][s_idx][0][lane] = u32x4{0u, 0u, 0u, 0u};  // S_0 = 0
-      sh.sb[0][s_idx][1][lane] = u32x4{0u, 0u, 0u, 0u};
-    }
+    if (phase_wave) phase(th, c0);
     lds_barrier();
 
     if (out_wave) {
@@ -389,10 +419,19 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
         for (int g = 0; g < 4; ++g) zr[g] = *reinterpret_cast<const u32x2*>(zrow + 8 * g);
       };
       // rows, then z, then stores: the order of every later iteration
-      rows = load_rows(0);
+      rows = load_rows(c0);
+      if constexpr (kSummary) {
+        for (int i = c0; i < c1; ++i) {
+          rotary(rows, i);
+          rows = load_rows(i + 1);
+          lds_barrier();
+          lds_barrier();
+        }
+        return;
+      }
       __builtin_amdgcn_sched_barrier(0);
       u32x2 zr[4];
-      load_z(0, zr);
+      load_z(c0, zr);
       __builtin_amdgcn_sched_barrier(0);
       // four dropped stores, so the walk starts with the same outstanding
       // operations (rows, z, stores) as every later iteration
@@ -407,10 +446,10 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
       f32x16 ybase = zero16();  // skip and inter-chunk terms of the chunk being finished
 #pragma unroll
       for (int e = 0; e < 16; ++e) gate[e] = 0.f;
-      for (int i = 0; i <= nvalid; ++i) {
+      for (int i = c0; i <= c1; ++i) {
         // ---------------- interval A(i) ----------------
-        if (i < nvalid) rotary(rows, i);
-        if (i >= 1) {
+        if (i < c1) rotary(rows, i);
+        if (i > c0) {
           // silu factors of chunk i - 1 from its gate rows (loaded at A(i - 1))
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
@@ -429,7 +468,7 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
         }
         rows = load_rows(i + 1);
         load_z(i, zr);
-        if (i >= 1) {
+        if (i > c0) {
           // chunk c = i - 1, tile (th, pt) of y^T[p][t]: (D + gamma (q + qb).(k + kb)) v
           // (mamba_fused.py:124, 147) + 2^cs qr . bf16(S_c)^T (mamba_fused.py:143)
           const int c = i - 1;
@@ -469,7 +508,7 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
         float yv[16];
 #pragma unroll
         for (int e = 0; e < 16; ++e) yv[e] = 0.f;
-        if (i >= 1) {
+        if (i > c0) {
           const int cb = c & 1;
           f32x16 y = ybase;
           if (th_o == 0) {
@@ -498,7 +537,7 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
         // no chunk to finish) take an offset past any buffer size and the
         // hardware drops them; rows in [L, T) are zero-filled after the walk.
         const int mrow = P.rev ? L - 1 - t : t;  // row in memory order
-        const int lane_off = (i >= 1 && t < L) ? (mrow * o_row + 32 * opt + 4 * hh) * esz : kOutOfRange;
+        const int lane_off = (i > c0 && t < L) ? (mrow * o_row + 32 * opt + 4 * hh) * esz : kOutOfRange;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           if constexpr (OUT32) {
@@ -516,16 +555,39 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
       }
     } else if (state_wave) {
       const int nt = (s_idx >> 1) & 1, spt = s_idx & 1;
-      f32x16 S = zero16();  // tile (nt, pt) of S^T[n][p]
-      rows = load_rows(0);
-      for (int i = 0; i <= nvalid; ++i) {
+      // tile (nt, pt) of S^T[n][p]; a seeded segment starts from the state the
+      // segment scan left in its record ([tile][16 / 4][lane] float4)
+      f32x16 S = zero16();
+      float4* rec_state =
+          (seeded || kSummary) ? P.seg_state + static_cast<size_t>(rec) * 1024 + s_idx * 256 + lane : nullptr;
+      if (seeded) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float4 x = rec_state[64 * q];
+          S[4 * q] = x.x, S[4 * q + 1] = x.y, S[4 * q + 2] = x.z, S[4 * q + 3] = x.w;
+        }
+      }
+      if constexpr (!kSummary) {
+        u32x4 lo, hi;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          lo[q] = pack2(S[2 * q], S[2 * q + 1]);
+          hi[q] = pack2(S[8 + 2 * q], S[8 + 2 * q + 1]);
+        }
+        sh.sb[c0 % 3][s_idx][0][lane] = lo;  // bf16 S_c0 (read by the outputs of chunk c0)
+        sh.sb[c0 % 3][s_idx][1][lane] = hi;
+      }
+      rows = load_rows(c0);
+      float seg_log2 = 0.f;  // summary: the segment's log2 decay, summed chunk by chunk
+      for (int i = c0; i < (kSummary ? c1 : c1 + 1); ++i) {
         // ---------------- interval A(i) ----------------
-        if (i < nvalid) rotary(rows, i);
+        if (i < c1) rotary(rows, i);
         rows = load_rows(i + 1);
         lds_barrier();
 
         // ---------------- interval B(i) ----------------
-        if (i + 1 < nvalid) {
+        // the walk needs S_{i+1} for a later chunk; the summary, every chunk's
+        if (kSummary || i + 1 < c1) {
           // S_{i+1} = S_i 2^tot + kr^T . bf16(v 2^(tot - cs)) of chunk i (mamba_fused.py:150-152)
           const int cb = i & 1;
           u32x4 kx[4], vy[4];
@@ -534,7 +596,9 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
             kx[s] = tr_operand(sh.kr[cb], nt, s, lane);
             vy[s] = tr_operand(sh.vs[cb], spt, s, lane);
           }
-          const float dec = fast_exp2(sh.tot[i % 3][0]);
+          const float tot_i = sh.tot[i % 3][0];
+          const float dec = fast_exp2(tot_i);
+          seg_log2 += tot_i;
           f32x16 d = zero16();
 #pragma unroll
           for (int s = 0; s < 4; ++s) d = mfma(kx[s], vy[s], d);
@@ -546,10 +610,17 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
             lo[q] = pack2(S[2 * q], S[2 * q + 1]);
             hi[q] = pack2(S[8 + 2 * q], S[8 + 2 * q + 1]);
           }
-          sh.sb[(i + 1) % 3][s_idx][0][lane] = lo;
-          sh.sb[(i + 1) % 3][s_idx][1][lane] = hi;
+          if constexpr (!kSummary) {
+            sh.sb[(i + 1) % 3][s_idx][0][lane] = lo;
+            sh.sb[(i + 1) % 3][s_idx][1][lane] = hi;
+          }
         }
         lds_barrier();
+      }
+      if constexpr (kSummary) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) rec_state[64 * q] = make_float4(S[4 * q], S[4 * q + 1], S[4 * q + 2], S[4 * q + 3]);
+        if (s_idx == 0 && lane == 0) P.seg_decay[rec] = seg_log2;
       }
     } else {
       // The prologue waves carry each interval's longest chain (the score
@@ -557,11 +628,11 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
       // youngest waves, so oldest-first issue would serve them last: raise
       // their issue priority over the output and state waves on their SIMD.
       __builtin_amdgcn_s_setprio(2);
-      for (int i = 0; i <= nvalid; ++i) {
+      for (int i = c0; i < (kSummary ? c1 : c1 + 1); ++i) {
         // ---------------- interval A(i) ----------------
         // angles of chunk i + 1, for the phase at B(i)
         load_pipe_angles<RPW, ANG16>(P, th, gbase, pair, (i + 1) * kChunk + sg * RPW, L);
-        if (p_idx < 3 && i >= 1) {
+        if (!kSummary && p_idx < 3 && i > c0) {
           // scores of chunk i - 1: tile (th, uh) = (0,0), (1,0), (1,1)
           const int c = i - 1;
           const int cb = c & 1;
@@ -582,29 +653,139 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
           sh.score[cb][p_idx][0][lane] = sc[0];
           sh.score[cb][p_idx][1][lane] = sc[1];
         }
-        if (p_idx == 3 && i + 1 < nvalid) controls(ctl_next, i + 1);
+        if (p_idx == 3 && i + 1 < c1) controls(ctl_next, i + 1);
         ctl_next = load_pipe_ctl<CTL16, TRAP16>(P, dto, ado, trb, (i + 2) * kChunk + lane, L, tlim);
         lds_barrier();
 
         // ---------------- interval B(i) ----------------
-        if (phase_wave && i + 1 < nvalid) phase(th, i + 1);
+        if (phase_wave && i + 1 < c1) phase(th, i + 1);
         lds_barrier();
       }
     }
   }
 
-  // rows in [L, T), the same rows in either direction: unreversed base and stride
-  constexpr int PD = 64;
-  const int o_st = P.rev ? -P.o_st : P.o_st;
-  const int obase_fwd = b * P.o_sb + h * P.o_sh;
-  for (int e = L * PD + static_cast<int>(threadIdx.x); e < T * PD; e += 768) {
-    const int tt = e / PD, p = e - tt * PD;
-    const int off = obase_fwd + tt * o_st + p;
-    if constexpr (OUT32)
-      static_cast<float*>(P.out)[off] = 0.f;
-    else
-      static_cast<uint16_t*>(P.out)[off] = 0;
+  if constexpr (kSummary) {
+    // a segment past the valid prefix leaves no state and no decay
+    if (c1 <= c0 && state_wave) {
+      float4* rec_state = P.seg_state + static_cast<size_t>(rec) * 1024 + s_idx * 256 + lane;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) rec_state[64 * q] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (s_idx == 0 && lane == 0) P.seg_decay[rec] = 0.f;
+    }
+  } else {
+    // rows in [L, T) of the segment's time range (the whole range with one
+    // segment), the same rows in either direction: unreversed base and stride
+    constexpr int PD = 64;
+    const int o_st = P.rev ? -P.o_st : P.o_st;
+    const int obase_fwd = b * P.o_sb + h * P.o_sh;
+    const int r0 = max(L, seg * P.SC * kChunk);
+    const int r1 = seg == P.G - 1 ? T : min(T, (seg + 1) * P.SC * kChunk);
+    for (int e = r0 * PD + static_cast<int>(threadIdx.x); e < r1 * PD; e += 768) {
+      const int tt = e / PD, p = e - tt * PD;
+      const int off = obase_fwd + tt * o_st + p;
+      if constexpr (OUT32)
+        static_cast<float*>(P.out)[off] = 0.f;
+      else
+        static_cast<uint16_t*>(P.out)[off] = 0;
+    }
   }
+}
+
+// Fixed-point phase sums of each (unit, segment) and rotary pair for the
+// chunk-parallel form: the increments the walk's phase stage forms (tanh(theta)
+// dt / 2 revolutions, reduced to [-1/2, 1/2], times 2^32; rows past the length
+// add nothing), added as wrapping 32-bit integers, so that any order of
+// addition gives the serial walk's bits. Thread (pair, row lane) of 16 x 64
+// (R <= 16; 32 x 32 above) strides over the segment's rows, loads batched 8 at
+// a time (one batch for a 512-row segment at R <= 16); LDS adds the row lanes.
+template <bool CTL16, bool ANG16, int PAIRS>
+__global__ __launch_bounds__(1024) void pipe_phase_sums_kernel(const MfmaParams P) {
+  constexpr int kLanes = 1024 / PAIRS;  // row lanes per pair
+  constexpr int kBatch = 8;
+  __shared__ uint32_t part[kLanes][PAIRS];
+  const int unit = blockIdx.x / P.G;
+  const int seg = blockIdx.x - unit * P.G;
+  const int b = unit / P.H;
+  const int h = unit - b * P.H;
+  int L = P.T;
+  if (P.lengths != nullptr) {
+    const int64_t l = P.lengths[b];
+    L = l < 0 ? 0 : (l > P.T ? P.T : static_cast<int>(l));
+  }
+  const int roff = P.rev ? max(L - 1, 0) : 0;
+  const int dto = b * P.d_sb + h * P.d_sh - roff * P.d_st;
+  const int gbase = b * P.g_sb + h * P.g_sh - roff * P.g_st;
+  const float step_bias = P.ctl_raw ? P.dt_bias[h] : 0.f;
+  const int r = threadIdx.x % PAIRS;
+  const int rl = threadIdx.x / PAIRS;
+  const int t_begin = seg * P.SC * kChunk;
+  const int t_end = min(t_begin + P.SC * kChunk, L);
+  uint32_t acc = 0;
+  if (r < P.R) {
+    for (int t0 = t_begin + rl; t0 < t_end; t0 += kBatch * kLanes) {
+      float dt[kBatch], th[kBatch];
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        // rows clamped to the segment's last valid row, masked below: every
+        // load of the batch is issued before the first use
+        const int t = min(t0 + j * kLanes, t_end - 1);
+        dt[j] = load_elem<CTL16>(P.dt, dto + t * P.d_st);
+        th[j] = load_elem<ANG16>(P.angles, gbase + r * P.g_sr + t * P.g_st);
+      }
+#pragma unroll
+      for (int j = 0; j < kBatch; ++j) {
+        float step = dt[j];
+        if (P.ctl_raw) step = control_step(step, step_bias);
+        float om = tanh_fast(th[j]) * step * 0.5f;
+        om -= rintf(om);
+        const float x = fminf(om * 4294967296.f, 2147483520.f);
+        if (t0 + j * kLanes < t_end) acc += static_cast<uint32_t>(static_cast<int>(x));
+      }
+    }
+  }
+  part[rl][r] = acc;
+  __syncthreads();
+  if (threadIdx.x < 32) {
+    uint32_t sum = 0;
+    if (static_cast<int>(threadIdx.x) < PAIRS)
+#pragma unroll
+      for (int g = 0; g < kLanes; ++g) sum += part[g][threadIdx.x];
+    P.phase_fx[static_cast<size_t>(blockIdx.x) * 32 + threadIdx.x] = sum;
+  }
+}
+
+// Chunk-parallel plan: with at most 128 (batch, head) units, each unit's time
+// axis is cut into G segments of SC chunks so that units * G is about one
+// workgroup per CU. Scratch: states [units][G][4096] fp32, phase sums
+// [units][G][32] uint32, decays [units][G] fp32, each 256-byte aligned.
+constexpr int64_t kMinSegmentChunks = 4;
+
+struct PipePlan {
+  int G = 1;
+  int SC = 0;
+  int64_t phase_off = 0, decay_off = 0, bytes = 0;
+};
+
+PipePlan pipe_plan(const tf_mamba_args& a) {
+  PipePlan p;
+  const int64_t units = a.batch * a.heads;
+  const int64_t chunks = (a.time + kChunk - 1) / kChunk;
+  p.SC = static_cast<int>(chunks);
+  if (units <= 0 || chunks <= 0 || units > 128) return p;
+  int64_t g = 256 / units;
+  // at least kMinSegmentChunks per segment: shorter walks gain less from the
+  // extra workgroups than the three extra passes cost
+  const int64_t sc = std::max<int64_t>((chunks + g - 1) / g, kMinSegmentChunks);
+  g = (chunks + sc - 1) / sc;
+  if (g < 2) return p;
+  p.G = static_cast<int>(g);
+  p.SC = static_cast<int>(sc);
+  auto up = [](int64_t x) { return (x + 255) & ~int64_t(255); };
+  const int64_t recs = units * g;
+  p.phase_off = up(recs * 4096 * 4);
+  p.decay_off = p.phase_off + up(recs * 32 * 4);
+  p.bytes = p.decay_off + up(recs * 4);
+  return p;
 }
 
 }  // namespace
@@ -640,11 +821,25 @@ namespace {
 
 template <int RPW, bool CTL16, bool TRAP16, bool ANG16>
 int launch_pipe_kernel(const MfmaParams& P, hipStream_t stream) {
-  const dim3 grid(static_cast<uint32_t>(P.units)), block(768);
+  const dim3 grid(static_cast<uint32_t>(P.units) * P.G), block(768);
+  if (P.G > 1) {
+    // phase sums -> segment summaries (from zero state) -> scan of the
+    // segment states -> the seeded walks that write the outputs
+    if (P.R > 0) {
+      if (P.R <= 16)
+        hipLaunchKernelGGL((pipe_phase_sums_kernel<CTL16, ANG16, 16>), grid, dim3(1024), 0, stream, P);
+      else
+        hipLaunchKernelGGL((pipe_phase_sums_kernel<CTL16, ANG16, 32>), grid, dim3(1024), 0, stream, P);
+      if (const int rc = launch_status()) return rc;
+    }
+    hipLaunchKernelGGL((mamba_pipe_kernel<RPW, CTL16, TRAP16, ANG16, false, 1>), grid, block, 0, stream, P);
+    if (const int rc = launch_status()) return rc;
+    if (const int rc = launch_segment_scan(P.seg_state, P.seg_decay, P.units, 1024, P.G, stream)) return rc;
+  }
   if (P.out_f32)
-    hipLaunchKernelGGL((mamba_pipe_kernel<RPW, CTL16, TRAP16, ANG16, true>), grid, block, 0, stream, P);
+    hipLaunchKernelGGL((mamba_pipe_kernel<RPW, CTL16, TRAP16, ANG16, true, 0>), grid, block, 0, stream, P);
   else
-    hipLaunchKernelGGL((mamba_pipe_kernel<RPW, CTL16, TRAP16, ANG16, false>), grid, block, 0, stream, P);
+    hipLaunchKernelGGL((mamba_pipe_kernel<RPW, CTL16, TRAP16, ANG16, false, 0>), grid, block, 0, stream, P);
   return launch_status();
 }
 
@@ -665,17 +860,32 @@ int launch_pipe_rpw(const MfmaParams& P, hipStream_t stream) {
 
 }  // namespace
 
+int64_t pipe_workspace_bytes(const tf_mamba_args& a) {
+  if (!pipe_supported(a)) return 0;
+  const PipePlan plan = pipe_plan(a);
+  return plan.G > 1 ? plan.bytes : 0;
+}
+
 int launch_pipe(const tf_mamba_args& a, hipStream_t stream) {
   MfmaParams P = make_params(a);
   if (a.rotary == 0) {
-    // no angles to read: the state waves' (unused) angle loads read q's rows of
-    // the unit's batch row instead, so every load address exists
+    // no angles to read: the (unused) angle loads read q's rows of the unit's
+    // batch row instead, so every load address exists
     P.angles = a.q;
     P.angles_dtype = TF_BFLOAT16;
     P.g_sb = P.q_sb, P.g_st = P.q_st, P.g_sh = 0, P.g_sr = 1;
   }
-  const int64_t units = a.batch * a.heads;
-  P.xcd_per = (units % 8 == 0 && units >= 64) ? static_cast<int>(units / 8) : 0;
+  const PipePlan plan = pipe_plan(a);
+  if (plan.G > 1 && a.workspace != nullptr && aligned(a.workspace, 256) && a.workspace_bytes >= plan.bytes) {
+    char* ws = static_cast<char*>(a.workspace);
+    P.G = plan.G;
+    P.SC = plan.SC;
+    P.seg_state = reinterpret_cast<float4*>(ws);
+    P.phase_fx = reinterpret_cast<uint32_t*>(ws + plan.phase_off);
+    P.seg_decay = reinterpret_cast<float*>(ws + plan.decay_off);
+  }
+  const int64_t items = static_cast<int64_t>(P.units) * P.G;
+  P.xcd_per = (items % 8 == 0 && items >= 64) ? static_cast<int>(items / 8) : 0;
   return a.rotary <= 16 ? launch_pipe_rpw<4>(P, stream) : launch_pipe_rpw<8>(P, stream);
 }
 

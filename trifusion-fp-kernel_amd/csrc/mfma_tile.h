@@ -228,6 +228,9 @@ struct MfmaParams {
   double* chunk_phase;
   float* seg_decay;
   int units, G, SC, NC;
+  // Pipelined kernel's chunk-parallel form: per (unit, segment) and rotary
+  // pair the wrapping sum of its fixed-point phase increments ([G][32]).
+  uint32_t* phase_fx;
 };
 
 // Element i of a control tensor (fp32, or bf16 for raw controls).
