@@ -81,12 +81,16 @@ def test_workspace_size_query():
 
     lib = _lib.load()
     size = lambda a: lib.tf_fused_mamba_workspace_size(ctypes.byref(a))  # noqa: E731
-    # long clip over 16 units: chunk-parallel, 15 segments of 8 chunks
-    # (per segment a 16 KB state and a 4 B decay, per chunk 512 B of phase sums;
-    # 256-byte aligned blocks)
+    # long clip over 16 units: chunk-parallel, 15 segments of 8 chunks; 256-byte
+    # aligned blocks. The pipelined kernel (auto): per segment a 16 KB state,
+    # 128 B of fixed-point phase sums and a 4 B decay. The chunked kernel: per
+    # segment a 16 KB state and a 4 B decay, per chunk 512 B of fp64 phase sums.
     recs, chunks = 16 * 15, 16 * 113
     up = lambda x: (x + 255) // 256 * 256  # noqa: E731
-    assert size(_host_args(1, 7200, 16)) == up(recs * 16384) + up(chunks * 512) + up(recs * 4)
+    assert size(_host_args(1, 7200, 16)) == up(recs * 16384) + up(recs * 128) + up(recs * 4)
+    forced = _host_args(1, 7200, 16)
+    forced.variant = 2
+    assert size(forced) == up(recs * 16384) + up(chunks * 512) + up(recs * 4)
     assert size(_host_args(16, 400, 16)) == 0  # 256 units: one workgroup each
     assert size(_host_args(1, 64, 16)) == 0  # one chunk: nothing to split
     assert size(_host_args(1, 7200, 16, state=16, head_dim=32, rotary=4)) == 0  # generic kernel
