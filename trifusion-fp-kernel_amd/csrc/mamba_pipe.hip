@@ -284,14 +284,13 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
         carry = pi == j ? tj : carry;
       }
     }
-    auto phase = [&](const float (&th)[RPW], int c) {
-      const int cr = c % 3;
+    auto phase_steps = [&](const float (&th)[RPW], const float (&dts)[RPW], int c) {
       uint32_t loc[RPW];
       uint32_t run = 0;
 #pragma unroll
       for (int i = 0; i < RPW; ++i) {
         // pi tanh(theta) dt radians = tanh(theta) dt / 2 revolutions (mamba_fused.py:102-109)
-        float om = tanh_fast(th[i]) * sh.dt[cr][sg * RPW + i] * 0.5f;
+        float om = tanh_fast(th[i]) * dts[i] * 0.5f;
         om -= rintf(om);
         const float x = fminf(om * 4294967296.f, 2147483520.f);
         run += static_cast<uint32_t>(static_cast<int>(x));
@@ -316,6 +315,13 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
               make_float2(__builtin_amdgcn_cosf(rev), __builtin_amdgcn_sinf(rev));
         }
       }
+    };
+    auto phase = [&](const float (&th)[RPW], int c) {
+      const int cr = c % 3;
+      float dts[RPW];
+#pragma unroll
+      for (int i = 0; i < RPW; ++i) dts[i] = sh.dt[cr][sg * RPW + i];
+      phase_steps(th, dts, c);
     };
 
     // biases of the wave's eight channels, wave-uniform, kept for the whole walk
@@ -394,10 +400,19 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
       const PipeCtl ctl0 = load_pipe_ctl<CTL16, TRAP16>(P, dto, ado, trb, c0 * kChunk + lane, L, tlim);
       ctl_next = load_pipe_ctl<CTL16, TRAP16>(P, dto, ado, trb, (c0 + 1) * kChunk + lane, L, tlim);
       load_pipe_angles<RPW, ANG16>(P, th, gbase, pair, c0 * kChunk + sg * RPW, L);
+      // chunk c0's steps for the phase, read here rather than from the
+      // controls' LDS rows, so that the phase does not wait for a barrier
+      float dts[RPW];
+#pragma unroll
+      for (int i = 0; i < RPW; ++i) {
+        const int t = c0 * kChunk + sg * RPW + i;
+        float d = load_elem<CTL16>(P.dt, dto + min(t, L - 1) * P.d_st);
+        if (P.ctl_raw) d = control_step(d, step_bias);
+        dts[i] = t < L ? d : 0.f;
+      }
       if (w == 11) controls(ctl0, c0);
+      if (phase_wave) phase_steps(th, dts, c0);
     }
-    lds_barrier();
-    if (phase_wave) phase(th, c0);
     lds_barrier();
 
     if (out_wave) {
