@@ -394,6 +394,19 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
     for (int i = 0; i < RPW; ++i) th[i] = 0.f;
     PipeRows rows = {};
     PipeCtl ctl_next = {};
+    // output and state waves: chunk c0's rows (and a seeded segment's entering
+    // state) before the start's barriers, so that their latency overlaps the
+    // first controls and phase
+    if (w < 8) rows = load_rows(c0);
+    float4 seed[4];  // state waves: [tile][16 / 4][lane] float4 of the segment's record
+    float4* rec_state =
+        state_wave && (seeded || kSummary) ? P.seg_state + static_cast<size_t>(rec) * 1024 + s_idx * 256 + lane : nullptr;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) seed[q] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (state_wave && seeded) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) seed[q] = rec_state[64 * q];
+    }
     if (w >= 8) {
       // every prologue wave loads the controls rows (wave 11 uses them), so
       // their count in each wave's outstanding loads is the same on every path
@@ -433,8 +446,7 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) zr[g] = *reinterpret_cast<const u32x2*>(zrow + 8 * g);
       };
-      // rows, then z, then stores: the order of every later iteration
-      rows = load_rows(c0);
+      // rows (loaded above), then z, then stores: the order of every later iteration
       if constexpr (kSummary) {
         for (int i = c0; i < c1; ++i) {
           rotary(rows, i);
@@ -571,16 +583,11 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
     } else if (state_wave) {
       const int nt = (s_idx >> 1) & 1, spt = s_idx & 1;
       // tile (nt, pt) of S^T[n][p]; a seeded segment starts from the state the
-      // segment scan left in its record ([tile][16 / 4][lane] float4)
-      f32x16 S = zero16();
-      float4* rec_state =
-          (seeded || kSummary) ? P.seg_state + static_cast<size_t>(rec) * 1024 + s_idx * 256 + lane : nullptr;
-      if (seeded) {
+      // segment scan left in its record (zero otherwise)
+      f32x16 S;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const float4 x = rec_state[64 * q];
-          S[4 * q] = x.x, S[4 * q + 1] = x.y, S[4 * q + 2] = x.z, S[4 * q + 3] = x.w;
-        }
+      for (int q = 0; q < 4; ++q) {
+        S[4 * q] = seed[q].x, S[4 * q + 1] = seed[q].y, S[4 * q + 2] = seed[q].z, S[4 * q + 3] = seed[q].w;
       }
       if constexpr (!kSummary) {
         u32x4 lo, hi;
@@ -592,7 +599,6 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
         sh.sb[c0 % 3][s_idx][0][lane] = lo;  // bf16 S_c0 (read by the outputs of chunk c0)
         sh.sb[c0 % 3][s_idx][1][lane] = hi;
       }
-      rows = load_rows(c0);
       float seg_log2 = 0.f;  // summary: the segment's log2 decay, summed chunk by chunk
       for (int i = c0; i < (kSummary ? c1 : c1 + 1); ++i) {
         // ---------------- interval A(i) ----------------
