@@ -663,34 +663,10 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
 constexpr int kScanSlice = 64;  // one wave per slice (256 float4 per slice: 1 us slower at B1 L7200)
 
 __global__ __launch_bounds__(kScanSlice) void segment_scan_kernel(float4* state, const float* decay, int kf4, int G) {
-  constexpr int kBatch = 16;  // records loaded ahead of the serial chain
   const int slices = kf4 / kScanSlice;
   const int unit = blockIdx.x / slices;
   const int f = (blockIdx.x - unit * slices) * kScanSlice + threadIdx.x;
-  float4* st = state + static_cast<size_t>(unit) * G * kf4;
-  const float* dec = decay + unit * G;
-  {
-    float4 run = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int g0 = 0; g0 < G; g0 += kBatch) {
-      float4 d[kBatch];
-      float m[kBatch];
-#pragma unroll
-      for (int j = 0; j < kBatch; ++j) {
-        if (g0 + j < G) {
-          d[j] = st[static_cast<size_t>(g0 + j) * kf4 + f];
-          m[j] = fast_exp2(dec[g0 + j]);
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < kBatch; ++j) {
-        if (g0 + j < G) {
-          st[static_cast<size_t>(g0 + j) * kf4 + f] = run;
-          run = make_float4(run.x * m[j] + d[j].x, run.y * m[j] + d[j].y, run.z * m[j] + d[j].z,
-                            run.w * m[j] + d[j].w);
-        }
-      }
-    }
-  }
+  scan_unit_records(state + static_cast<size_t>(unit) * G * kf4, decay + unit * G, kf4, G, f);
 }
 
 // Phase increments of each (unit, chunk): per rotary pair, the fp64 sum over

@@ -163,13 +163,89 @@ struct PipeRows {
   u32x4 q, k, v;
 };
 
-// MODE 0 walks the unit (or, P.G > 1, one time segment of it, seeded with the
-// state and phase entering the segment) and writes the outputs; MODE 1 walks a
-// segment from zero state without outputs and writes the state it leaves and
-// its total log2 decay (the chunk-parallel form's summary pass).
-template <int RPW, bool CTL16, bool TRAP16, bool ANG16, bool OUT32, int MODE>
+// Work item of workgroup blockIdx.x: (batch row, segment, head). The heads of
+// one batch row and segment read the same q/k rows, so they are consecutive
+// items, and items are dealt to the 8 XCDs in contiguous ranges so that those
+// heads share an L2. A segment's state record is [unit][segment].
+struct PipeItem {
+  int b, h, seg, unit, rec;
+};
+
+__device__ __forceinline__ PipeItem pipe_item(const MfmaParams& P) {
+  const int item = P.xcd_per > 0 ? (blockIdx.x & 7) * P.xcd_per + (blockIdx.x >> 3) : static_cast<int>(blockIdx.x);
+  const int bseg = item / P.H;
+  PipeItem it;
+  it.h = item - bseg * P.H;
+  it.b = bseg / P.G;
+  it.seg = bseg - it.b * P.G;
+  it.unit = it.b * P.H + it.h;
+  it.rec = it.unit * P.G + it.seg;
+  return it;
+}
+
+// Fixed-point phase increment of one (row, pair): pi tanh(theta) dt radians
+// (mamba_fused.py:102-109) = tanh(theta) dt / 2 revolutions, reduced to
+// [-1/2, 1/2] and scaled by 2^32. A row without a step (dt = 0) adds 0.
+__device__ __forceinline__ uint32_t phase_inc(float th, float dt) {
+  float om = tanh_fast(th) * dt * 0.5f;
+  om -= rintf(om);
+  const float x = fminf(om * 4294967296.f, 2147483520.f);
+  return static_cast<uint32_t>(static_cast<int>(x));
+}
+
+// (cos, sin) of a fixed-point phase (2^-32 revolutions): v_cos/v_sin take revolutions.
+__device__ __forceinline__ float2 phase_trig(uint32_t ph) {
+  const float rev = static_cast<float>(static_cast<int>(ph)) * 2.3283064365386963e-10f;
+  return make_float2(__builtin_amdgcn_cosf(rev), __builtin_amdgcn_sinf(rev));
+}
+
+// Controls of one chunk, one wave, lane = row (mamba_fused.py:96-101, 139-142):
+// step, key scale, inclusive log2 decay, 2^(tot - cs), dt sigmoid(trap), and
+// the chunk's total log2 decay (every lane).
+struct RowControls {
+  float dt, sc, cs, wv, gam, tot;
+};
+
+__device__ __forceinline__ RowControls row_controls(const MfmaParams& P, const PipeCtl& raw, bool valid, bool next,
+                                                    float step_bias) {
+  float dtv = raw.dt, dnv = raw.dn, adv = raw.adt;
+  if (P.ctl_raw) {
+    // step and decay from the raw columns (primitives.py:209-214)
+    dtv = control_step(dtv, step_bias);
+    dnv = control_step(dnv, step_bias);
+    adv = control_decay(adv, dtv, P.a_floor);
+  }
+  // rows without a step keep dt = adt = 0, and a missing halo step loads 0
+  dtv = valid ? dtv : 0.f;
+  adv = valid ? adv : 0.f;
+  dnv = next ? dnv : 0.f;
+  const float trv = valid ? raw.tr : 0.f;
+  const float tnv = next ? raw.tn : 0.f;
+  RowControls r;
+  r.dt = dtv;
+  r.gam = dtv * sigmoid_fast(trv);
+  r.sc = __builtin_fmaf(dnv, 1.f - sigmoid_fast(tnv), r.gam);
+  r.cs = wave_scan_dpp(adv * kLog2e);
+  r.tot = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, r.cs), 63));
+  r.wv = fast_exp2(r.tot - r.cs);
+  return r;
+}
+
+// bf16 pair of a key rotated by (cv, sv) and scaled by the trapezoid scale
+// (mamba_fused.py:126-131), and of a value scaled by 2^(tot - cs) (:151).
+// The fused multiply-adds are spelled out, so that every kernel rounds a key
+// the same way whatever the compiler would contract in its context.
+__device__ __forceinline__ uint32_t key_pair(float k0, float k1, float cv, float sv, float scl) {
+  return pack2(__builtin_fmaf(k0, cv, -(k1 * sv)) * scl, __builtin_fmaf(k0, sv, k1 * cv) * scl);
+}
+__device__ __forceinline__ uint32_t scaled_pair(uint32_t vw, float wvt) {
+  return pack2(lo_f(vw) * wvt, hi_f(vw) * wvt);
+}
+
+// Walks the unit (or, P.G > 1, one time segment of it, seeded with the state
+// and phase entering the segment) and writes the outputs.
+template <int RPW, bool CTL16, bool TRAP16, bool ANG16, bool OUT32>
 __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
-  constexpr bool kSummary = MODE == 1;
   __shared__ PipeSmem sh;
   const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int lane = static_cast<int>(threadIdx.x & 63);
@@ -179,17 +255,8 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
   const bool state_wave = w >= 4 && w < 8;
   const int s_idx = w - 4;  // state wave index (state waves)
   const int p_idx = w - 8;  // prologue wave index (prologue waves)
-  // work item (batch row, segment, head): the heads of one batch row and
-  // segment read the same q/k rows, so they are consecutive items, and items
-  // are dealt to the 8 XCDs in contiguous ranges so that those heads share an
-  // L2. The segment's state record is [unit][segment], as the scan reads it.
-  const int item = P.xcd_per > 0 ? (blockIdx.x & 7) * P.xcd_per + (blockIdx.x >> 3) : static_cast<int>(blockIdx.x);
-  const int bseg = item / P.H;
-  const int h = item - bseg * P.H;
-  const int b = bseg / P.G;
-  const int seg = bseg - b * P.G;
-  const int unit = b * P.H + h;
-  const int rec = unit * P.G + seg;
+  const PipeItem it = pipe_item(P);
+  const int b = it.b, h = it.h, seg = it.seg, unit = it.unit, rec = it.rec;
   const int qh = h / P.group;
   const int T = P.T;
   const int R = P.R;
@@ -202,7 +269,7 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
   // the segment's chunks [c0, c1) of the valid prefix
   const int c0 = min(seg * P.SC, nvalid);
   const int c1 = min(c0 + P.SC, nvalid);
-  const bool seeded = P.G > 1 && !kSummary;
+  const bool seeded = P.G > 1;
   const int tlim = P.rev ? L : T;
   const int roff = P.rev ? max(L - 1, 0) : 0;
   const uint16_t* qbase = P.q + b * P.q_sb + qh * P.q_sh - roff * P.q_st;
@@ -223,14 +290,14 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
     const int pair = p_idx * RPW + pi;                // phase pair of a prologue wave's lane
     const bool phase_wave = w >= 8 && p_idx * RPW < R;  // wave-uniform
 
-    const int ng = (w + 4) & 7;  // channel group of the rotary stage (waves 0-7)
+    // rotary tasks of waves 0-7: row rrow of the chunk, channel group ng (the
+    // state waves groups 0-3, the output waves 4-7; 16 rows per wave)
+    const int rrow = 16 * (w & 3) + (lane >> 2);
+    const int ng = (w < 4 ? 4 : 0) + (lane & 3);
     auto load_rows = [&](int c) {
-      const int t = min(c * kChunk + lane, L - 1);
+      const int t = min(c * kChunk + rrow, L - 1);
       PipeRows r;
-      if constexpr (kSummary)
-        r.q = u32x4{0u, 0u, 0u, 0u};  // the summary needs no queries
-      else
-        r.q = *reinterpret_cast<const u32x4*>(qbase + t * P.q_st + 8 * ng);
+      r.q = *reinterpret_cast<const u32x4*>(qbase + t * P.q_st + 8 * ng);
       r.k = *reinterpret_cast<const u32x4*>(kbase + t * P.k_st + 8 * ng);
       r.v = *reinterpret_cast<const u32x4*>(vbase + t * P.v_st + 8 * ng);
       return r;
@@ -239,33 +306,14 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
     // controls of chunk c (state wave 3, lane = row)
     auto controls = [&](const PipeCtl& raw, int c) {
       const int t = c * kChunk + lane;
-      const bool valid = t < L;
-      const bool next = t + 1 < tlim;
-      float dtv = raw.dt, dnv = raw.dn, adv = raw.adt;
-      if (P.ctl_raw) {
-        // step and decay from the raw columns (primitives.py:209-214)
-        dtv = control_step(dtv, step_bias);
-        dnv = control_step(dnv, step_bias);
-        adv = control_decay(adv, dtv, P.a_floor);
-      }
-      // rows without a step keep dt = adt = 0, and a missing halo step loads 0
-      dtv = valid ? dtv : 0.f;
-      adv = valid ? adv : 0.f;
-      dnv = next ? dnv : 0.f;
-      const float trv = valid ? raw.tr : 0.f;
-      const float tnv = next ? raw.tn : 0.f;
-      // mamba_fused.py:96-101, 139-142
-      const float gam = dtv * sigmoid_fast(trv);
-      const float scl = dnv * (1.f - sigmoid_fast(tnv)) + gam;
-      const float cs = wave_scan_dpp(adv * kLog2e);
-      const float tot = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cs), 63));
+      const RowControls rc = row_controls(P, raw, t < L, t + 1 < tlim, step_bias);
       const int cr = c % 3;
-      sh.dt[cr][lane] = dtv;
-      sh.sc[cr][lane] = scl;
-      sh.cs[cr][lane] = cs;
-      sh.wv[cr][lane] = fast_exp2(tot - cs);
-      sh.gam[cr][lane] = gam;
-      if (lane == 0) sh.tot[cr][0] = tot;
+      sh.dt[cr][lane] = rc.dt;
+      sh.sc[cr][lane] = rc.sc;
+      sh.cs[cr][lane] = rc.cs;
+      sh.wv[cr][lane] = rc.wv;
+      sh.gam[cr][lane] = rc.gam;
+      if (lane == 0) sh.tot[cr][0] = rc.tot;
     };
 
     // rotary phase and cos/sin of chunk c (phase waves)
@@ -289,11 +337,7 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
       uint32_t run = 0;
 #pragma unroll
       for (int i = 0; i < RPW; ++i) {
-        // pi tanh(theta) dt radians = tanh(theta) dt / 2 revolutions (mamba_fused.py:102-109)
-        float om = tanh_fast(th[i]) * dts[i] * 0.5f;
-        om -= rintf(om);
-        const float x = fminf(om * 4294967296.f, 2147483520.f);
-        run += static_cast<uint32_t>(static_cast<int>(x));
+        run += phase_inc(th[i], dts[i]);
         loc[i] = run;
       }
       const uint32_t incl = group_scan_dpp<NSEG>(run, lane);  // over the segments of the pair
@@ -309,11 +353,8 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
       if (pair < R) {
         float* tg = &sh.trig[c & 1][0];
 #pragma unroll
-        for (int i = 0; i < RPW; ++i) {
-          const float rev = static_cast<float>(static_cast<int>(base + loc[i])) * 2.3283064365386963e-10f;
-          *reinterpret_cast<float2*>(tg + (sg * RPW + i) * kTrigStride + 2 * pair) =
-              make_float2(__builtin_amdgcn_cosf(rev), __builtin_amdgcn_sinf(rev));
-        }
+        for (int i = 0; i < RPW; ++i)
+          *reinterpret_cast<float2*>(tg + (sg * RPW + i) * kTrigStride + 2 * pair) = phase_trig(base + loc[i]);
       }
     };
     auto phase = [&](const float (&th)[RPW], int c) {
@@ -332,20 +373,22 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
       kbv[j] = P.kb[h * 64 + 8 * ng + j];
     }
 
-    // bias, rotation, scaling and bf16 rounding of chunk c's rows (lane = row,
-    // channels 8 ng .. 8 ng + 7; mamba_fused.py:112-135, 151). The state waves
-    // take channel groups 0-3, which hold the rotated pairs when R <= 16, and
-    // the output waves groups 4-7, so each SIMD gets one of each.
+    // bias, rotation, scaling and bf16 rounding of chunk c's rows (lane = row
+    // rrow, channels 8 ng .. 8 ng + 7; mamba_fused.py:112-135, 151). The state
+    // waves take channel groups 0-3, which hold the rotated pairs when R <= 16,
+    // and the output waves groups 4-7, so each SIMD gets one of each; a wave's
+    // 16 rows x 4 groups make its row loads 16 pieces of 64 contiguous bytes
+    // (a row per lane would touch 64 cache lines per load).
     auto rotary = [&](const PipeRows& in, int c) {
       const int cb = c & 1, cr = c % 3;
-      const bool valid = c * kChunk + lane < L;
-      const float scl = sh.sc[cr][lane];
-      const float wvt = sh.wv[cr][lane];
+      const bool valid = c * kChunk + rrow < L;
+      const float scl = sh.sc[cr][rrow];
+      const float wvt = sh.wv[cr][rrow];
       u32x4 qo, ko, vo, vso;
       float part = 0.f;
       if (4 * ng < R) {
         // pairs 4 ng + j >= R turn by the identity: x * 1 - y * 0 is x exactly
-        const float4* tg = reinterpret_cast<const float4*>(&sh.trig[cb][lane * kTrigStride + 8 * ng]);
+        const float4* tg = reinterpret_cast<const float4*>(&sh.trig[cb][rrow * kTrigStride + 8 * ng]);
         const float4 a = tg[0], bq = tg[1];
         const float cosv[4] = {a.x, a.z, bq.x, bq.z}, sinv[4] = {a.y, a.w, bq.y, bq.w};
 #pragma unroll
@@ -356,7 +399,7 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
           const float k0 = lo_f(in.k[j]) + kbv[2 * j], k1 = hi_f(in.k[j]) + kbv[2 * j + 1];
           part += q0 * k0 + q1 * k1;
           qo[j] = pack2(q0 * cv - q1 * sv, q0 * sv + q1 * cv);
-          ko[j] = pack2((k0 * cv - k1 * sv) * scl, (k0 * sv + k1 * cv) * scl);
+          ko[j] = key_pair(k0, k1, cv, sv, scl);
         }
       } else {
 #pragma unroll
@@ -372,13 +415,13 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
       for (int j = 0; j < 4; ++j) {
         const uint32_t vw = valid ? in.v[j] : 0u;
         vo[j] = vw;
-        vso[j] = pack2(lo_f(vw) * wvt, hi_f(vw) * wvt);
+        vso[j] = scaled_pair(vw, wvt);
       }
-      if constexpr (!kSummary) rb_write16(sh.qr[cb], lane, 2 * ng, qo);
-      rb_write16(sh.kr[cb], lane, 2 * ng, ko);
-      if constexpr (!kSummary) rb_write16(sh.v[cb], lane, 2 * ng, vo);
-      rb_write16(sh.vs[cb], lane, 2 * ng, vso);
-      if constexpr (!kSummary) sh.skip[cr][ng][lane] = part;
+      rb_write16(sh.qr[cb], rrow, 2 * ng, qo);
+      rb_write16(sh.kr[cb], rrow, 2 * ng, ko);
+      rb_write16(sh.v[cb], rrow, 2 * ng, vo);
+      rb_write16(sh.vs[cb], rrow, 2 * ng, vso);
+      sh.skip[cr][ng][rrow] = part;
     };
 
     // Each role runs its own copy of the walk, with the same two barriers per
@@ -399,11 +442,10 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
     // first controls and phase
     if (w < 8) rows = load_rows(c0);
     float4 seed[4];  // state waves: [tile][16 / 4][lane] float4 of the segment's record
-    float4* rec_state =
-        state_wave && (seeded || kSummary) ? P.seg_state + static_cast<size_t>(rec) * 1024 + s_idx * 256 + lane : nullptr;
 #pragma unroll
     for (int q = 0; q < 4; ++q) seed[q] = make_float4(0.f, 0.f, 0.f, 0.f);
     if (state_wave && seeded) {
+      const float4* rec_state = P.seg_state + static_cast<size_t>(rec) * 1024 + s_idx * 256 + lane;
 #pragma unroll
       for (int q = 0; q < 4; ++q) seed[q] = rec_state[64 * q];
     }
@@ -447,15 +489,6 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
         for (int g = 0; g < 4; ++g) zr[g] = *reinterpret_cast<const u32x2*>(zrow + 8 * g);
       };
       // rows (loaded above), then z, then stores: the order of every later iteration
-      if constexpr (kSummary) {
-        for (int i = c0; i < c1; ++i) {
-          rotary(rows, i);
-          rows = load_rows(i + 1);
-          lds_barrier();
-          lds_barrier();
-        }
-        return;
-      }
       __builtin_amdgcn_sched_barrier(0);
       u32x2 zr[4];
       load_z(c0, zr);
@@ -589,7 +622,7 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
       for (int q = 0; q < 4; ++q) {
         S[4 * q] = seed[q].x, S[4 * q + 1] = seed[q].y, S[4 * q + 2] = seed[q].z, S[4 * q + 3] = seed[q].w;
       }
-      if constexpr (!kSummary) {
+      {
         u32x4 lo, hi;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -599,16 +632,15 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
         sh.sb[c0 % 3][s_idx][0][lane] = lo;  // bf16 S_c0 (read by the outputs of chunk c0)
         sh.sb[c0 % 3][s_idx][1][lane] = hi;
       }
-      float seg_log2 = 0.f;  // summary: the segment's log2 decay, summed chunk by chunk
-      for (int i = c0; i < (kSummary ? c1 : c1 + 1); ++i) {
+      for (int i = c0; i <= c1; ++i) {
         // ---------------- interval A(i) ----------------
         if (i < c1) rotary(rows, i);
         rows = load_rows(i + 1);
         lds_barrier();
 
         // ---------------- interval B(i) ----------------
-        // the walk needs S_{i+1} for a later chunk; the summary, every chunk's
-        if (kSummary || i + 1 < c1) {
+        // the walk needs S_{i+1} for a later chunk
+        if (i + 1 < c1) {
           // S_{i+1} = S_i 2^tot + kr^T . bf16(v 2^(tot - cs)) of chunk i (mamba_fused.py:150-152)
           const int cb = i & 1;
           u32x4 kx[4], vy[4];
@@ -617,9 +649,7 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
             kx[s] = tr_operand(sh.kr[cb], nt, s, lane);
             vy[s] = tr_operand(sh.vs[cb], spt, s, lane);
           }
-          const float tot_i = sh.tot[i % 3][0];
-          const float dec = fast_exp2(tot_i);
-          seg_log2 += tot_i;
+          const float dec = fast_exp2(sh.tot[i % 3][0]);
           f32x16 d = zero16();
 #pragma unroll
           for (int s = 0; s < 4; ++s) d = mfma(kx[s], vy[s], d);
@@ -631,17 +661,10 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
             lo[q] = pack2(S[2 * q], S[2 * q + 1]);
             hi[q] = pack2(S[8 + 2 * q], S[8 + 2 * q + 1]);
           }
-          if constexpr (!kSummary) {
-            sh.sb[(i + 1) % 3][s_idx][0][lane] = lo;
-            sh.sb[(i + 1) % 3][s_idx][1][lane] = hi;
-          }
+          sh.sb[(i + 1) % 3][s_idx][0][lane] = lo;
+          sh.sb[(i + 1) % 3][s_idx][1][lane] = hi;
         }
         lds_barrier();
-      }
-      if constexpr (kSummary) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) rec_state[64 * q] = make_float4(S[4 * q], S[4 * q + 1], S[4 * q + 2], S[4 * q + 3]);
-        if (s_idx == 0 && lane == 0) P.seg_decay[rec] = seg_log2;
       }
     } else {
       // The prologue waves carry each interval's longest chain (the score
@@ -649,11 +672,11 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
       // youngest waves, so oldest-first issue would serve them last: raise
       // their issue priority over the output and state waves on their SIMD.
       __builtin_amdgcn_s_setprio(2);
-      for (int i = c0; i < (kSummary ? c1 : c1 + 1); ++i) {
+      for (int i = c0; i <= c1; ++i) {
         // ---------------- interval A(i) ----------------
         // angles of chunk i + 1, for the phase at B(i)
         load_pipe_angles<RPW, ANG16>(P, th, gbase, pair, (i + 1) * kChunk + sg * RPW, L);
-        if (!kSummary && p_idx < 3 && i > c0) {
+        if (p_idx < 3 && i > c0) {
           // scores of chunk i - 1: tile (th, uh) = (0,0), (1,0), (1,1)
           const int c = i - 1;
           const int cb = c & 1;
@@ -685,15 +708,7 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
     }
   }
 
-  if constexpr (kSummary) {
-    // a segment past the valid prefix leaves no state and no decay
-    if (c1 <= c0 && state_wave) {
-      float4* rec_state = P.seg_state + static_cast<size_t>(rec) * 1024 + s_idx * 256 + lane;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) rec_state[64 * q] = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (s_idx == 0 && lane == 0) P.seg_decay[rec] = 0.f;
-    }
-  } else {
+  {
     // rows in [L, T) of the segment's time range (the whole range with one
     // segment), the same rows in either direction: unreversed base and stride
     constexpr int PD = 64;
@@ -757,10 +772,8 @@ __global__ __launch_bounds__(1024) void pipe_phase_sums_kernel(const MfmaParams 
       for (int j = 0; j < kBatch; ++j) {
         float step = dt[j];
         if (P.ctl_raw) step = control_step(step, step_bias);
-        float om = tanh_fast(th[j]) * step * 0.5f;
-        om -= rintf(om);
-        const float x = fminf(om * 4294967296.f, 2147483520.f);
-        if (t0 + j * kLanes < t_end) acc += static_cast<uint32_t>(static_cast<int>(x));
+        const uint32_t x = phase_inc(th[j], step);
+        if (t0 + j * kLanes < t_end) acc += x;
       }
     }
   }
@@ -773,6 +786,228 @@ __global__ __launch_bounds__(1024) void pipe_phase_sums_kernel(const MfmaParams 
       for (int g = 0; g < kLanes; ++g) sum += part[g][threadIdx.x];
     P.phase_fx[static_cast<size_t>(blockIdx.x) * 32 + threadIdx.x] = sum;
   }
+}
+
+// LDS of the summary pass: a batch of four chunks (256 rows).
+template <int PAIRS>
+struct SummarySmem {
+  union {
+    float trig[256 * kTrigStride];  // [row][pair] (cos, sin)
+    float4 dstate[4][1024];         // dS of each chunk, in record layout
+  } a;
+  union {
+    uint32_t inc[PAIRS][260];  // fixed-point phase increments [pair][row]
+    struct {
+      uint16_t kr[4][64 * 64];  // bf16(rot(k + kb) * s), row buffers
+      uint16_t vs[4][64 * 64];  // bf16(v * 2^(tot - cs))
+    } t;
+  } b;
+  float sc[256];
+  float wv[256];
+  float tot[2][4];  // the chunks' total log2 decays, by batch parity
+};
+
+// Summary pass of the chunk-parallel form, parallel over the chunks of the
+// segment: the state the segment leaves from zero state, S <- S 2^tot_c + dS_c
+// over its chunks c (mamba_fused.py:150-152), where dS_c = bf16(v_c 2^(tot_c -
+// cs))^T . kr_c needs only chunk c's rows and the phase entering it. Chunks go
+// in batches of four (1024 threads, 16 waves):
+//   - every thread forms the fixed-point phase increments of rows x pairs of
+//     the batch (lane = pair, so a wave's angle loads are whole rows), and the
+//     first waves the controls of one chunk each (lane = row);
+//   - wave j scans pair j's increments over the batch's rows, from the phase
+//     entering the batch, into the cos/sin table;
+//   - every thread rotates and scales the keys of one channel group and
+//     scales the values, for two rows (8 lanes per row);
+//   - wave w computes the 32 x 32 tile w mod 4 of dS for chunk w / 4;
+//   - thread f folds float4 f of the four dS_c into the state, in chunk order.
+// These are the serial walk's operations, in its order (its shared helpers,
+// with the multiply-adds spelled out), so the record is the one a serial walk
+// of the segment from zero state leaves.
+template <bool CTL16, bool TRAP16, bool ANG16, int PAIRS>
+__global__ __launch_bounds__(1024) void pipe_summary_kernel(const MfmaParams P) {
+  constexpr int kBatch = 4;                      // chunks per batch
+  constexpr int kRowLanes = 1024 / PAIRS;        // phase row lanes per pair
+  constexpr int kRowsPer = 256 / kRowLanes;      // phase rows per thread
+  constexpr int kSlots = PAIRS / 16;             // pairs per scanning wave
+  __shared__ SummarySmem<PAIRS> sh;
+  const int tid = static_cast<int>(threadIdx.x);
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const PipeItem it = pipe_item(P);
+  const int b = it.b, h = it.h;
+  const int qh = h / P.group;
+  const int T = P.T;
+  const int R = P.R;
+  int L = T;
+  if (P.lengths != nullptr) {
+    const int64_t l = P.lengths[b];
+    L = l < 0 ? 0 : (l > T ? T : static_cast<int>(l));
+  }
+  const int nvalid = (L + kChunk - 1) / kChunk;
+  const int c0 = min(it.seg * P.SC, nvalid);
+  const int c1 = min(c0 + P.SC, nvalid);
+  const int tlim = P.rev ? L : T;
+  const int roff = P.rev ? max(L - 1, 0) : 0;
+  const uint16_t* kbase = P.k + b * P.k_sb + qh * P.k_sh - roff * P.k_st;
+  const uint16_t* vbase = P.v + b * P.v_sb + h * P.v_sh - roff * P.v_st;
+  const int dto = b * P.d_sb + h * P.d_sh - roff * P.d_st;
+  const int ado = b * P.a_sb + h * P.a_sh - roff * P.a_st;
+  const int trb = b * P.r_sb + h * P.r_sh - roff * P.r_st;
+  const int gbase = b * P.g_sb + h * P.g_sh - roff * P.g_st;
+  const float step_bias = P.ctl_raw ? P.dt_bias[h] : 0.f;
+
+  // phase entering the segment for the wave's scan pairs: the wrapping sum
+  // of the earlier segments' sums
+  uint32_t carry[kSlots];
+#pragma unroll
+  for (int k = 0; k < kSlots; ++k) {
+    const int j = w + 16 * k;
+    uint32_t part = 0;
+    if (j < R)
+      for (int g = lane; g < it.seg; g += 64) part += P.phase_fx[(static_cast<size_t>(it.unit) * P.G + g) * 32 + j];
+    carry[k] = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(wave_scan_u32(part)), 63));
+  }
+  const int pj = tid % PAIRS;   // phase lanes: pair
+  const int prl = tid / PAIRS;  // and row lane
+  // key rotation tasks: channel group ng of batch rows rsub and rsub + 128
+  // (8 lanes per row, so a wave's row loads are 8 whole 128-byte rows)
+  const int ng = lane & 7;
+  const int rsub = w * 8 + (lane >> 3);
+  float kbv[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) kbv[j] = P.kb[h * 64 + 8 * ng + j];
+
+  float4 S = make_float4(0.f, 0.f, 0.f, 0.f);
+  float seg_log2 = 0.f;
+  int parity = 0;
+  for (int cb0 = c0; cb0 < c1; cb0 += kBatch, parity ^= 1) {
+    const int nb = min(kBatch, c1 - cb0);
+    const int t_lo = cb0 * kChunk;
+    // the batch's loads, all issued before the first use
+    float th[kRowsPer], dts[kRowsPer];
+    if (pj < R) {
+#pragma unroll
+      for (int i = 0; i < kRowsPer; ++i) {
+        const int tc = min(t_lo + prl + kRowLanes * i, L - 1);
+        dts[i] = load_elem<CTL16>(P.dt, dto + tc * P.d_st);
+        th[i] = load_elem<ANG16>(P.angles, gbase + pj * P.g_sr + tc * P.g_st);
+      }
+    }
+    PipeCtl raw = {};
+    if (w < nb) raw = load_pipe_ctl<CTL16, TRAP16>(P, dto, ado, trb, (cb0 + w) * kChunk + lane, L, tlim);
+    u32x4 kin[2], vin[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int tc = min(t_lo + rsub + 128 * i, L - 1);
+      kin[i] = *reinterpret_cast<const u32x4*>(kbase + tc * P.k_st + 8 * ng);
+      vin[i] = *reinterpret_cast<const u32x4*>(vbase + tc * P.v_st + 8 * ng);
+    }
+
+    // phase increments (rows past the length have no step and add 0)
+    if (pj < R) {
+#pragma unroll
+      for (int i = 0; i < kRowsPer; ++i) {
+        const int r = prl + kRowLanes * i;
+        float d = dts[i];
+        if (P.ctl_raw) d = control_step(d, step_bias);
+        sh.b.inc[pj][r] = phase_inc(th[i], t_lo + r < L ? d : 0.f);
+      }
+    }
+    // controls of chunk cb0 + w
+    if (w < nb) {
+      const int t = (cb0 + w) * kChunk + lane;
+      const RowControls rc = row_controls(P, raw, t < L, t + 1 < tlim, step_bias);
+      sh.sc[w * kChunk + lane] = rc.sc;
+      sh.wv[w * kChunk + lane] = rc.wv;
+      if (lane == 0) sh.tot[parity][w] = rc.tot;
+    }
+    lds_barrier();
+
+    // per pair: phase of every row of the batch, then cos/sin
+#pragma unroll
+    for (int k = 0; k < kSlots; ++k) {
+      const int j = w + 16 * k;
+      if (j < R) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = lane + 64 * i;
+          const uint32_t incl = wave_scan_u32(sh.b.inc[j][r]);
+          *reinterpret_cast<float2*>(&sh.a.trig[r * kTrigStride + 2 * j]) = phase_trig(carry[k] + incl);
+          carry[k] += static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(incl), 63));
+        }
+      }
+    }
+    lds_barrier();
+
+    // keys: bias, rotation, scale; values: decay scale (mamba_fused.py:112-131, 151)
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r = rsub + 128 * i;
+      const int cc = r >> 6;
+      if (cc < nb) {
+        const bool valid = t_lo + r < L;
+        const float scl = sh.sc[r];
+        const float wvt = sh.wv[r];
+        u32x4 ko, vso;
+        if (4 * ng < R) {
+          // pairs 4 ng + j >= R turn by the identity
+          const float4* tg = reinterpret_cast<const float4*>(&sh.a.trig[r * kTrigStride + 8 * ng]);
+          const float4 a = tg[0], bq = tg[1];
+          const float cosv[4] = {a.x, a.z, bq.x, bq.z}, sinv[4] = {a.y, a.w, bq.y, bq.w};
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const bool on = 4 * ng + j < R;
+            const float k0 = lo_f(kin[i][j]) + kbv[2 * j], k1 = hi_f(kin[i][j]) + kbv[2 * j + 1];
+            ko[j] = key_pair(k0, k1, on ? cosv[j] : 1.f, on ? sinv[j] : 0.f, scl);
+          }
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float k0 = lo_f(kin[i][j]) + kbv[2 * j], k1 = hi_f(kin[i][j]) + kbv[2 * j + 1];
+            ko[j] = pack2(k0 * scl, k1 * scl);
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) vso[j] = scaled_pair(valid ? vin[i][j] : 0u, wvt);
+        rb_write16(sh.b.t.kr[cc], r & 63, 2 * ng, ko);
+        rb_write16(sh.b.t.vs[cc], r & 63, 2 * ng, vso);
+      }
+    }
+    lds_barrier();
+
+    // dS_c = kr^T . vs tile (nt, pt) of S^T[n][p], in the walk's tile layout
+    {
+      const int cc = w >> 2, st = w & 3;
+      if (cc < nb) {
+        const int nt = st >> 1, spt = st & 1;
+        u32x4 kx[4], vy[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          kx[s] = tr_operand(sh.b.t.kr[cc], nt, s, lane);
+          vy[s] = tr_operand(sh.b.t.vs[cc], spt, s, lane);
+        }
+        f32x16 d = zero16();
+#pragma unroll
+        for (int s = 0; s < 4; ++s) d = mfma(kx[s], vy[s], d);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          sh.a.dstate[cc][st * 256 + q * 64 + lane] = make_float4(d[4 * q], d[4 * q + 1], d[4 * q + 2], d[4 * q + 3]);
+      }
+    }
+    lds_barrier();
+
+    // S <- S 2^tot_c + dS_c, chunk by chunk
+    for (int cc = 0; cc < nb; ++cc) {
+      const float tot = sh.tot[parity][cc];
+      const float dec = fast_exp2(tot);
+      const float4 x = sh.a.dstate[cc][tid];
+      S = make_float4(S.x * dec + x.x, S.y * dec + x.y, S.z * dec + x.z, S.w * dec + x.w);
+      seg_log2 += tot;
+    }
+  }
+  P.seg_state[static_cast<size_t>(it.rec) * 1024 + tid] = S;
+  if (tid == 0) P.seg_decay[it.rec] = seg_log2;
 }
 
 // Chunk-parallel plan: with at most 128 (batch, head) units, each unit's time
@@ -853,14 +1088,17 @@ int launch_pipe_kernel(const MfmaParams& P, hipStream_t stream) {
         hipLaunchKernelGGL((pipe_phase_sums_kernel<CTL16, ANG16, 32>), grid, dim3(1024), 0, stream, P);
       if (const int rc = launch_status()) return rc;
     }
-    hipLaunchKernelGGL((mamba_pipe_kernel<RPW, CTL16, TRAP16, ANG16, false, 1>), grid, block, 0, stream, P);
+    if (P.R <= 16)
+      hipLaunchKernelGGL((pipe_summary_kernel<CTL16, TRAP16, ANG16, 16>), grid, dim3(1024), 0, stream, P);
+    else
+      hipLaunchKernelGGL((pipe_summary_kernel<CTL16, TRAP16, ANG16, 32>), grid, dim3(1024), 0, stream, P);
     if (const int rc = launch_status()) return rc;
     if (const int rc = launch_segment_scan(P.seg_state, P.seg_decay, P.units, 1024, P.G, stream)) return rc;
   }
   if (P.out_f32)
-    hipLaunchKernelGGL((mamba_pipe_kernel<RPW, CTL16, TRAP16, ANG16, true, 0>), grid, block, 0, stream, P);
+    hipLaunchKernelGGL((mamba_pipe_kernel<RPW, CTL16, TRAP16, ANG16, true>), grid, block, 0, stream, P);
   else
-    hipLaunchKernelGGL((mamba_pipe_kernel<RPW, CTL16, TRAP16, ANG16, false, 0>), grid, block, 0, stream, P);
+    hipLaunchKernelGGL((mamba_pipe_kernel<RPW, CTL16, TRAP16, ANG16, false>), grid, block, 0, stream, P);
   return launch_status();
 }
 

@@ -82,6 +82,17 @@ __device__ __forceinline__ float wave_scan_dpp(float x) {
   return x;
 }
 
+// Inclusive prefix sum over the 64 lanes of the wave on DPP, wrapping uint32.
+__device__ __forceinline__ uint32_t wave_scan_u32(uint32_t x) {
+  x += dpp_u32<kDppRowShr + 1>(x);
+  x += dpp_u32<kDppRowShr + 2>(x);
+  x += dpp_u32<kDppRowShr + 4>(x);
+  x += dpp_u32<kDppRowShr + 8>(x);
+  x += dpp_u32<kDppRowBcast15, 0xa>(x);
+  x += dpp_u32<kDppRowBcast31, 0xc>(x);
+  return x;
+}
+
 // Inclusive prefix sum within each group of G consecutive lanes (G = 8 or 16),
 // wrapping uint32 arithmetic, on DPP.
 template <int G>
@@ -232,6 +243,34 @@ struct MfmaParams {
   // pair the wrapping sum of its fixed-point phase increments ([G][32]).
   uint32_t* phase_fx;
 };
+
+// The segment scan of one unit's records, float4 f of each: record g (the
+// state segment g leaves from zero state; log2 decay dec[g]) is replaced by
+// the state entering segment g: S_0 = 0, S_{g+1} = S_g 2^dec[g] + record g.
+// Loads run ahead of the serial chain in batches of 16 records.
+__device__ __forceinline__ void scan_unit_records(float4* st, const float* dec, int kf4, int G, int f) {
+  constexpr int kBatch = 16;
+  float4 run = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int g0 = 0; g0 < G; g0 += kBatch) {
+    float4 d[kBatch];
+    float m[kBatch];
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      if (g0 + j < G) {
+        d[j] = st[static_cast<size_t>(g0 + j) * kf4 + f];
+        m[j] = fast_exp2(dec[g0 + j]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kBatch; ++j) {
+      if (g0 + j < G) {
+        st[static_cast<size_t>(g0 + j) * kf4 + f] = run;
+        run = make_float4(run.x * m[j] + d[j].x, run.y * m[j] + d[j].y, run.z * m[j] + d[j].z,
+                          run.w * m[j] + d[j].w);
+      }
+    }
+  }
+}
 
 // Element i of a control tensor (fp32, or bf16 for raw controls).
 __device__ __forceinline__ float ctl_value(const void* base, int bf16, int i) {
