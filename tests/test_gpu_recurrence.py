@@ -68,6 +68,27 @@ def test_reference_shapes(variant, batch, time, heads):
 
 
 @pytest.mark.parametrize("variant", VARIANTS)
+@pytest.mark.parametrize("case", ["clip", "varlen_reverse", "long"])
+def test_bf16_output_is_rounded_fp32_output(variant, case):
+    """The bf16 output path (its own stores) holds exactly the fp32 output
+    rounded to nearest even, row by row, including rows past the lengths."""
+    b, t, lens, rev = {"clip": (4, 400, None, False), "varlen_reverse": (3, 400, (400, 213, 0), True),
+                       "long": (1, 3000, None, False)}[case]
+    args = clip_inputs(b, t, heads=8, rotary=16, seed=23)
+    needs(variant, args)
+    dargs = to_dev(args)
+    lengths = None if lens is None else torch.tensor(lens, dtype=torch.int64, device=DEV)
+    print(f"case {case} variant={variant}", flush=True)
+    with torch.inference_mode():
+        y32 = fused_mamba(*dargs, out=torch.empty(dargs[2].shape, device=DEV), variant=variant, lengths=lengths,
+                          reverse=rev)
+        y16 = fused_mamba(*dargs, out=torch.empty(dargs[2].shape, device=DEV, dtype=torch.bfloat16), variant=variant,
+                          lengths=lengths, reverse=rev)
+    torch.cuda.synchronize()
+    assert torch.equal(y16.cpu(), y32.cpu().to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("variant", VARIANTS)
 def test_short_against_f64(variant):
     args = reference_test_inputs(1, 17, 4)
     needs(variant, args)

@@ -482,26 +482,24 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
           ((L - 1) * o_row + 64) * esz, kRawBufferWord3);
       // gate rows of chunk c (lane = row 32 th + c32 of the chunk, the tile's
       // columns), loaded at A(c) and turned into silu factors at A(c + 1)
-      auto load_z = [&](int c, u32x2 (&zr)[4]) {
+      // (lane c32 + 32 hh holds 32 contiguous bytes of its row: columns
+      // 32 opt + 16 hh .. + 15; the gate stage trades halves with lane ^ 32)
+      auto load_z = [&](int c, u32x4 (&zr)[2]) {
         const int t = min(c * kChunk + 32 * th_o + c32, L - 1);
-        const uint16_t* zrow = zbase + t * P.z_st + 32 * opt + 4 * hh;
-#pragma unroll
-        for (int g = 0; g < 4; ++g) zr[g] = *reinterpret_cast<const u32x2*>(zrow + 8 * g);
+        const uint16_t* zrow = zbase + t * P.z_st + 32 * opt + 16 * hh;
+        zr[0] = *reinterpret_cast<const u32x4*>(zrow);
+        zr[1] = *reinterpret_cast<const u32x4*>(zrow + 8);
       };
       // rows (loaded above), then z, then stores: the order of every later iteration
       __builtin_amdgcn_sched_barrier(0);
-      u32x2 zr[4];
+      u32x4 zr[2];
       load_z(c0, zr);
       __builtin_amdgcn_sched_barrier(0);
-      // four dropped stores, so the walk starts with the same outstanding
+      // dropped stores, so the walk starts with the same outstanding
       // operations (rows, z, stores) as every later iteration
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        if constexpr (OUT32)
-          __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, out_rsrc, kOutOfRange, 0, 0);
-        else
-          __builtin_amdgcn_raw_buffer_store_b64(u32x2{0u, 0u}, out_rsrc, kOutOfRange, 0, 0);
-      }
+      for (int g = 0; g < (OUT32 ? 4 : 2); ++g)
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, out_rsrc, kOutOfRange, 0, 0);
       float gate[16];           // silu(z) of the chunk being finished (mamba_fused.py:148)
       f32x16 ybase = zero16();  // skip and inter-chunk terms of the chunk being finished
 #pragma unroll
@@ -511,11 +509,31 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
         if (i < c1) rotary(rows, i);
         if (i > c0) {
           // silu factors of chunk i - 1 from its gate rows (loaded at A(i - 1))
+          // columns 8 g + 4 hh .. + 3 of the tile layout: hh = 0 keeps its
+          // g = 0, 1 pieces and takes g = 2, 3 from lane ^ 32, hh = 1 the reverse
+          u32x2 zt[4];
+          {
+            uint32_t snd[4], rcv[4];
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+              snd[2 * k] = hh ? zr[k][0] : zr[k][2];
+              snd[2 * k + 1] = hh ? zr[k][1] : zr[k][3];
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k) rcv[k] = static_cast<uint32_t>(__shfl_xor(static_cast<int>(snd[k]), 32));
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+              const u32x2 own = hh ? u32x2{zr[k][2], zr[k][3]} : u32x2{zr[k][0], zr[k][1]};
+              const u32x2 got = u32x2{rcv[2 * k], rcv[2 * k + 1]};
+              zt[k] = hh ? got : own;
+              zt[k + 2] = hh ? own : got;
+            }
+          }
 #pragma unroll
           for (int g = 0; g < 4; ++g) {
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-              const uint32_t zw = zr[g][q >> 1];
+              const uint32_t zw = zt[g][q >> 1];
               const float zz = (q & 1) ? hi_f(zw) : lo_f(zw);
               gate[4 * g + q] = zz * sigmoid_fast(zz);
             }
@@ -597,18 +615,36 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
         // no chunk to finish) take an offset past any buffer size and the
         // hardware drops them; rows in [L, T) are zero-filled after the walk.
         const int mrow = P.rev ? L - 1 - t : t;  // row in memory order
-        const int lane_off = (i > c0 && t < L) ? (mrow * o_row + 32 * opt + 4 * hh) * esz : kOutOfRange;
+        const bool live = i > c0 && t < L;
+        if constexpr (OUT32) {
+          const int lane_off = live ? (mrow * o_row + 32 * opt + 4 * hh) * esz : kOutOfRange;
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          if constexpr (OUT32) {
+          for (int g = 0; g < 4; ++g)
             __builtin_amdgcn_raw_buffer_store_b128(
                 u32x4{__builtin_bit_cast(uint32_t, yv[4 * g]), __builtin_bit_cast(uint32_t, yv[4 * g + 1]),
                       __builtin_bit_cast(uint32_t, yv[4 * g + 2]), __builtin_bit_cast(uint32_t, yv[4 * g + 3])},
                 out_rsrc, lane_off + 32 * g, 0, 0);
-          } else {
-            __builtin_amdgcn_raw_buffer_store_b64(
-                u32x2{pack2(yv[4 * g], yv[4 * g + 1]), pack2(yv[4 * g + 2], yv[4 * g + 3])}, out_rsrc,
-                lane_off + 16 * g, 0, 0);
+        } else {
+          // bf16 pieces g (columns 8 g + 4 hh .. + 3) traded with lane ^ 32 into
+          // 32 contiguous bytes per lane: columns 16 hh .. 16 hh + 15
+          u32x2 pw[4];
+#pragma unroll
+          for (int g = 0; g < 4; ++g) pw[g] = u32x2{pack2(yv[4 * g], yv[4 * g + 1]), pack2(yv[4 * g + 2], yv[4 * g + 3])};
+          uint32_t snd[4], rcv[4];
+#pragma unroll
+          for (int k = 0; k < 2; ++k) {
+            snd[2 * k] = hh ? pw[k][0] : pw[k + 2][0];
+            snd[2 * k + 1] = hh ? pw[k][1] : pw[k + 2][1];
+          }
+#pragma unroll
+          for (int k = 0; k < 4; ++k) rcv[k] = static_cast<uint32_t>(__shfl_xor(static_cast<int>(snd[k]), 32));
+          const int lane_off = live ? (mrow * o_row + 32 * opt + 16 * hh) * esz : kOutOfRange;
+#pragma unroll
+          for (int k = 0; k < 2; ++k) {
+            const u32x2 own = hh ? pw[k + 2] : pw[k];
+            const u32x2 got = u32x2{rcv[2 * k], rcv[2 * k + 1]};
+            const u32x4 piece = hh ? u32x4{got[0], got[1], own[0], own[1]} : u32x4{own[0], own[1], got[0], got[1]};
+            __builtin_amdgcn_raw_buffer_store_b128(piece, out_rsrc, lane_off + 16 * k, 0, 0);
           }
         }
         lds_barrier();
