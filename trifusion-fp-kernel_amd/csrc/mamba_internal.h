@@ -24,10 +24,6 @@ int launch_mfma(const tf_mamba_args& a, hipStream_t stream);
 // (0: one workgroup per unit).
 int64_t mfma_workspace_bytes(const tf_mamba_args& a);
 
-// Exclusive scan of per-segment state records (layout-agnostic: kf4 float4
-// per record, [units][G] records), S_0 = 0, S_{g+1} = S_g 2^decay_g + dS_g.
-int launch_segment_scan(float4* state, const float* decay, int units, int kf4, int G, hipStream_t stream);
-
 // Pipelined MFMA kernel (N = P = 64): one workgroup walks each unit, or, for
 // few long units with a workspace, each (unit, time segment).
 bool pipe_supported(const tf_mamba_args& a);

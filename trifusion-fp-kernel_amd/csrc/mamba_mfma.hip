@@ -889,13 +889,6 @@ int launch_shape(const tf_mamba_args& a, hipStream_t stream) {
 
 }  // namespace
 
-int launch_segment_scan(float4* state, const float* decay, int units, int kf4, int G, hipStream_t stream) {
-  if (kf4 % kScanSlice != 0) return TF_ERR_SHAPE;
-  hipLaunchKernelGGL(segment_scan_kernel, dim3(static_cast<uint32_t>(units) * (kf4 / kScanSlice)), dim3(kScanSlice),
-                     0, stream, state, decay, kf4, G);
-  return launch_status();
-}
-
 int64_t mfma_workspace_bytes(const tf_mamba_args& a) {
   if (!mfma_supported(a)) return 0;
   const SegPlan plan = plan_segments(a, shape_cw(a), static_cast<int>((a.state / 32) * (a.head_dim / 32) * 256));

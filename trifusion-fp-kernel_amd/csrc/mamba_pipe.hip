@@ -39,7 +39,9 @@
 namespace tf {
 namespace {
 
-constexpr int kTrigStride = 68;  // floats per row of the cos/sin table: 32 pairs x 2 + 4 pad
+// Floats per row of a cos/sin table: 32 pairs x 2 + 2 pad. Rows 4 apart (the
+// walk's phase lanes) land 8 banks apart, consecutive rows (the summary's) 2.
+constexpr int kTrigStride = 66;
 
 // Fourth word of a raw (unswizzled, stride 0) buffer descriptor on gfx9-family
 // parts: 32-bit data format; loads and stores past num_records are dropped.
@@ -158,6 +160,9 @@ __device__ __forceinline__ void load_pipe_angles(const MfmaParams& P, float (&th
   for (int i = 0; i < RPW; ++i) th[i] = load_elem<ANG16>(P.angles, col + min(row0 + i, L - 1) * P.g_st);
 }
 
+// Segment summaries a thread of the seeded walk loads per round trip.
+constexpr int kSeedBatch = 8;
+
 // Raw 16-byte row pieces of the wave's eight channels (lane = row).
 struct PipeRows {
   u32x4 q, k, v;
@@ -242,9 +247,9 @@ __device__ __forceinline__ uint32_t scaled_pair(uint32_t vw, float wvt) {
   return pack2(lo_f(vw) * wvt, hi_f(vw) * wvt);
 }
 
-// Walks the unit (or, P.G > 1, one time segment of it, seeded with the state
-// and phase entering the segment) and writes the outputs.
-template <int RPW, bool CTL16, bool TRAP16, bool ANG16, bool OUT32>
+// Walks the unit (or, SEEDED with P.G > 1, one time segment of it, from the
+// state and phase entering the segment) and writes the outputs.
+template <int RPW, bool CTL16, bool TRAP16, bool ANG16, bool OUT32, bool SEEDED>
 __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
   __shared__ PipeSmem sh;
   const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
@@ -269,7 +274,6 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
   // the segment's chunks [c0, c1) of the valid prefix
   const int c0 = min(seg * P.SC, nvalid);
   const int c1 = min(c0 + P.SC, nvalid);
-  const bool seeded = P.G > 1;
   const int tlim = P.rev ? L : T;
   const int roff = P.rev ? max(L - 1, 0) : 0;
   const uint16_t* qbase = P.q + b * P.q_sb + qh * P.q_sh - roff * P.q_st;
@@ -318,7 +322,7 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
 
     // rotary phase and cos/sin of chunk c (phase waves)
     uint32_t carry = 0;  // phase entering the chunk, pair `pair`, 2^-32 revolutions
-    if (P.G > 1 && phase_wave) {
+    if (SEEDED && phase_wave) {
       // a segment's walk starts from the phase of the segments before it: the
       // wrapping sum of their fixed-point sums (the same integers the serial
       // walk adds), lanes of a pair splitting the segments
@@ -388,9 +392,9 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
       float part = 0.f;
       if (4 * ng < R) {
         // pairs 4 ng + j >= R turn by the identity: x * 1 - y * 0 is x exactly
-        const float4* tg = reinterpret_cast<const float4*>(&sh.trig[cb][rrow * kTrigStride + 8 * ng]);
-        const float4 a = tg[0], bq = tg[1];
-        const float cosv[4] = {a.x, a.z, bq.x, bq.z}, sinv[4] = {a.y, a.w, bq.y, bq.w};
+        const float2* tg = reinterpret_cast<const float2*>(&sh.trig[cb][rrow * kTrigStride + 8 * ng]);
+        const float2 t0 = tg[0], t1 = tg[1], t2 = tg[2], t3 = tg[3];
+        const float cosv[4] = {t0.x, t1.x, t2.x, t3.x}, sinv[4] = {t0.y, t1.y, t2.y, t3.y};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const bool on = 4 * ng + j < R;
@@ -437,17 +441,41 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
     for (int i = 0; i < RPW; ++i) th[i] = 0.f;
     PipeRows rows = {};
     PipeCtl ctl_next = {};
-    // output and state waves: chunk c0's rows (and a seeded segment's entering
-    // state) before the start's barriers, so that their latency overlaps the
-    // first controls and phase
+    // output and state waves: chunk c0's rows before the start's barrier, so
+    // that their latency overlaps the first controls and phase
     if (w < 8) rows = load_rows(c0);
-    float4 seed[4];  // state waves: [tile][16 / 4][lane] float4 of the segment's record
+    // A seeded segment's entering state: the segment scan of the unit's
+    // summaries of the segments before it, S <- S 2^dec_g + summary_g for
+    // g < seg, float4 f = threadIdx.x (and + 768) of the record layout, left in
+    // the second chunk's qr/kr buffers (tiles 0-1, 2-3) for the state waves.
+    [[maybe_unused]] float4* seed_lds[2] = {reinterpret_cast<float4*>(sh.qr[(c0 + 1) & 1]),
+                                            reinterpret_cast<float4*>(sh.kr[(c0 + 1) & 1])};
+    if constexpr (SEEDED) {
+      const int f0 = static_cast<int>(threadIdx.x), f1 = f0 + 768;
+      const float4* sums = P.seg_state + static_cast<size_t>(unit) * P.G * 1024;
+      const float* decs = P.seg_decay + unit * P.G;
+      float4 run0 = make_float4(0.f, 0.f, 0.f, 0.f), run1 = run0;
+      for (int g0 = 0; g0 < seg; g0 += kSeedBatch) {
+        float4 d0[kSeedBatch], d1[kSeedBatch];
+        float m[kSeedBatch];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) seed[q] = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (state_wave && seeded) {
-      const float4* rec_state = P.seg_state + static_cast<size_t>(rec) * 1024 + s_idx * 256 + lane;
+        for (int j = 0; j < kSeedBatch; ++j) {
+          if (g0 + j < seg) {
+            d0[j] = sums[static_cast<size_t>(g0 + j) * 1024 + f0];
+            if (f1 < 1024) d1[j] = sums[static_cast<size_t>(g0 + j) * 1024 + f1];
+            m[j] = fast_exp2(decs[g0 + j]);
+          }
+        }
 #pragma unroll
-      for (int q = 0; q < 4; ++q) seed[q] = rec_state[64 * q];
+        for (int j = 0; j < kSeedBatch; ++j) {
+          if (g0 + j < seg) {
+            run0 = state_step(run0, m[j], d0[j]);
+            if (f1 < 1024) run1 = state_step(run1, m[j], d1[j]);
+          }
+        }
+      }
+      seed_lds[f0 >> 9][f0 & 511] = run0;
+      if (f1 < 1024) seed_lds[f1 >> 9][f1 & 511] = run1;
     }
     if (w >= 8) {
       // every prologue wave loads the controls rows (wave 11 uses them), so
@@ -651,12 +679,16 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
       }
     } else if (state_wave) {
       const int nt = (s_idx >> 1) & 1, spt = s_idx & 1;
-      // tile (nt, pt) of S^T[n][p]; a seeded segment starts from the state the
-      // segment scan left in its record (zero otherwise)
-      f32x16 S;
+      // tile (nt, pt) of S^T[n][p]; a seeded segment starts from its entering
+      // state (zero otherwise)
+      f32x16 S = zero16();
+      if constexpr (SEEDED) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        S[4 * q] = seed[q].x, S[4 * q + 1] = seed[q].y, S[4 * q + 2] = seed[q].z, S[4 * q + 3] = seed[q].w;
+        for (int q = 0; q < 4; ++q) {
+          const int f = s_idx * 256 + q * 64 + lane;
+          const float4 x = seed_lds[f >> 9][f & 511];
+          S[4 * q] = x.x, S[4 * q + 1] = x.y, S[4 * q + 2] = x.z, S[4 * q + 3] = x.w;
+        }
       }
       {
         u32x4 lo, hi;
@@ -850,7 +882,8 @@ struct SummarySmem {
 // in batches of four (1024 threads, 16 waves):
 //   - every thread forms the fixed-point phase increments of rows x pairs of
 //     the batch (lane = pair, so a wave's angle loads are whole rows), and the
-//     first waves the controls of one chunk each (lane = row);
+//     first waves the controls of one chunk each (lane = row); the batch's
+//     loads were issued during the previous batch;
 //   - wave j scans pair j's increments over the batch's rows, from the phase
 //     entering the batch, into the cos/sin table;
 //   - every thread rotates and scales the keys of one channel group and
@@ -917,11 +950,12 @@ __global__ __launch_bounds__(1024) void pipe_summary_kernel(const MfmaParams P) 
   float4 S = make_float4(0.f, 0.f, 0.f, 0.f);
   float seg_log2 = 0.f;
   int parity = 0;
-  for (int cb0 = c0; cb0 < c1; cb0 += kBatch, parity ^= 1) {
-    const int nb = min(kBatch, c1 - cb0);
+  // a batch's loads (rows clamped to ones that exist), issued one batch ahead
+  float th[kRowsPer], dts[kRowsPer];
+  PipeCtl raw = {};
+  u32x4 kin[2], vin[2];
+  auto issue_loads = [&](int cb0) {
     const int t_lo = cb0 * kChunk;
-    // the batch's loads, all issued before the first use
-    float th[kRowsPer], dts[kRowsPer];
     if (pj < R) {
 #pragma unroll
       for (int i = 0; i < kRowsPer; ++i) {
@@ -930,15 +964,18 @@ __global__ __launch_bounds__(1024) void pipe_summary_kernel(const MfmaParams P) 
         th[i] = load_elem<ANG16>(P.angles, gbase + pj * P.g_sr + tc * P.g_st);
       }
     }
-    PipeCtl raw = {};
-    if (w < nb) raw = load_pipe_ctl<CTL16, TRAP16>(P, dto, ado, trb, (cb0 + w) * kChunk + lane, L, tlim);
-    u32x4 kin[2], vin[2];
+    raw = load_pipe_ctl<CTL16, TRAP16>(P, dto, ado, trb, (cb0 + (w & 3)) * kChunk + lane, L, tlim);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int tc = min(t_lo + rsub + 128 * i, L - 1);
       kin[i] = *reinterpret_cast<const u32x4*>(kbase + tc * P.k_st + 8 * ng);
       vin[i] = *reinterpret_cast<const u32x4*>(vbase + tc * P.v_st + 8 * ng);
     }
+  };
+  if (c0 < c1) issue_loads(c0);
+  for (int cb0 = c0; cb0 < c1; cb0 += kBatch, parity ^= 1) {
+    const int nb = min(kBatch, c1 - cb0);
+    const int t_lo = cb0 * kChunk;
 
     // phase increments (rows past the length have no step and add 0)
     if (pj < R) {
@@ -988,9 +1025,9 @@ __global__ __launch_bounds__(1024) void pipe_summary_kernel(const MfmaParams P) 
         u32x4 ko, vso;
         if (4 * ng < R) {
           // pairs 4 ng + j >= R turn by the identity
-          const float4* tg = reinterpret_cast<const float4*>(&sh.a.trig[r * kTrigStride + 8 * ng]);
-          const float4 a = tg[0], bq = tg[1];
-          const float cosv[4] = {a.x, a.z, bq.x, bq.z}, sinv[4] = {a.y, a.w, bq.y, bq.w};
+          const float2* tg = reinterpret_cast<const float2*>(&sh.a.trig[r * kTrigStride + 8 * ng]);
+          const float2 t0 = tg[0], t1 = tg[1], t2 = tg[2], t3 = tg[3];
+          const float cosv[4] = {t0.x, t1.x, t2.x, t3.x}, sinv[4] = {t0.y, t1.y, t2.y, t3.y};
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
             const bool on = 4 * ng + j < R;
@@ -1010,6 +1047,7 @@ __global__ __launch_bounds__(1024) void pipe_summary_kernel(const MfmaParams P) 
         rb_write16(sh.b.t.vs[cc], r & 63, 2 * ng, vso);
       }
     }
+    if (cb0 + kBatch < c1) issue_loads(cb0 + kBatch);
     lds_barrier();
 
     // dS_c = kr^T . vs tile (nt, pt) of S^T[n][p], in the walk's tile layout
@@ -1115,8 +1153,8 @@ template <int RPW, bool CTL16, bool TRAP16, bool ANG16>
 int launch_pipe_kernel(const MfmaParams& P, hipStream_t stream) {
   const dim3 grid(static_cast<uint32_t>(P.units) * P.G), block(768);
   if (P.G > 1) {
-    // phase sums -> segment summaries (from zero state) -> scan of the
-    // segment states -> the seeded walks that write the outputs
+    // phase sums -> segment summaries (from zero state) -> the seeded walks,
+    // which scan the summaries before their segment and write the outputs
     if (P.R > 0) {
       if (P.R <= 16)
         hipLaunchKernelGGL((pipe_phase_sums_kernel<CTL16, ANG16, 16>), grid, dim3(1024), 0, stream, P);
@@ -1129,12 +1167,17 @@ int launch_pipe_kernel(const MfmaParams& P, hipStream_t stream) {
     else
       hipLaunchKernelGGL((pipe_summary_kernel<CTL16, TRAP16, ANG16, 32>), grid, dim3(1024), 0, stream, P);
     if (const int rc = launch_status()) return rc;
-    if (const int rc = launch_segment_scan(P.seg_state, P.seg_decay, P.units, 1024, P.G, stream)) return rc;
   }
-  if (P.out_f32)
-    hipLaunchKernelGGL((mamba_pipe_kernel<RPW, CTL16, TRAP16, ANG16, true>), grid, block, 0, stream, P);
-  else
-    hipLaunchKernelGGL((mamba_pipe_kernel<RPW, CTL16, TRAP16, ANG16, false>), grid, block, 0, stream, P);
+  if (P.G > 1) {
+    if (P.out_f32)
+      hipLaunchKernelGGL((mamba_pipe_kernel<RPW, CTL16, TRAP16, ANG16, true, true>), grid, block, 0, stream, P);
+    else
+      hipLaunchKernelGGL((mamba_pipe_kernel<RPW, CTL16, TRAP16, ANG16, false, true>), grid, block, 0, stream, P);
+  } else if (P.out_f32) {
+    hipLaunchKernelGGL((mamba_pipe_kernel<RPW, CTL16, TRAP16, ANG16, true, false>), grid, block, 0, stream, P);
+  } else {
+    hipLaunchKernelGGL((mamba_pipe_kernel<RPW, CTL16, TRAP16, ANG16, false, false>), grid, block, 0, stream, P);
+  }
   return launch_status();
 }
 

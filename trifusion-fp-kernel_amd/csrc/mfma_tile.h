@@ -244,6 +244,13 @@ struct MfmaParams {
   uint32_t* phase_fx;
 };
 
+// One step of the segment scan, S 2^dec + summary, as explicit fused
+// multiply-adds (the same rounding wherever it is inlined).
+__device__ __forceinline__ float4 state_step(const float4& s, float m, const float4& d) {
+  return make_float4(__builtin_fmaf(s.x, m, d.x), __builtin_fmaf(s.y, m, d.y), __builtin_fmaf(s.z, m, d.z),
+                     __builtin_fmaf(s.w, m, d.w));
+}
+
 // The segment scan of one unit's records, float4 f of each: record g (the
 // state segment g leaves from zero state; log2 decay dec[g]) is replaced by
 // the state entering segment g: S_0 = 0, S_{g+1} = S_g 2^dec[g] + record g.
@@ -265,8 +272,7 @@ __device__ __forceinline__ void scan_unit_records(float4* st, const float* dec, 
     for (int j = 0; j < kBatch; ++j) {
       if (g0 + j < G) {
         st[static_cast<size_t>(g0 + j) * kf4 + f] = run;
-        run = make_float4(run.x * m[j] + d[j].x, run.y * m[j] + d[j].y, run.z * m[j] + d[j].z,
-                          run.w * m[j] + d[j].w);
+        run = state_step(run, m[j], d[j]);
       }
     }
   }
