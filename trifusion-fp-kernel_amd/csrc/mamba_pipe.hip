@@ -7,14 +7,14 @@
 // the workgroup barriers of consecutive iterations, so the stages of
 // neighbouring chunks overlap:
 //
-//   stage of chunk c       interval   waves                  lane layout
-//   controls               A(c-1)     prologue wave 3        lane = row
-//   phase, cos/sin         B(c-1)     state waves            lane = (pair, row segment)
-//   bias, rotation         A(c)       output + state waves   lane = row, wave = 8 channels
-//   state S_{c+1}          B(c)       state waves            one 32x32 tile of S each
-//   scores                 A(c+1)     prologue waves 0-2     one 32x32 score tile each
-//   skip, inter-chunk      A(c+1)     output waves           one 32x32 tile of y each
-//   scores . v, gate       B(c+1)     output waves           the same tile
+//   stage of chunk c       interval   waves                    lane layout
+//   controls               A(c-1)     prologue wave 3          lane = row
+//   phase, cos/sin         B(c-1)     prologue waves           lane = (pair, row segment)
+//   bias, rotation         A(c)       state + prologue waves   lane = (row, 8 channels)
+//   state S_{c+1}          B(c)       state waves              one 32x32 tile of S each
+//   scores                 A(c+1)     prologue waves 0-2       one 32x32 score tile each
+//   skip, inter-chunk      A(c+1)     output waves             one 32x32 tile of y each
+//   scores . v, gate       B(c+1)     output waves             the same tile
 //
 // Waves 0-3 are output waves (time half th = w >> 1, head-dim tile pt = w & 1),
 // waves 4-7 state waves (s = w - 4: state tile nt = s >> 1, pt = s & 1) and
@@ -294,10 +294,11 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
     const int pair = p_idx * RPW + pi;                // phase pair of a prologue wave's lane
     const bool phase_wave = w >= 8 && p_idx * RPW < R;  // wave-uniform
 
-    // rotary tasks of waves 0-7: row rrow of the chunk, channel group ng (the
-    // state waves groups 0-3, the output waves 4-7; 16 rows per wave)
+    // rotary tasks of the state and prologue waves: row rrow of the chunk,
+    // channel group ng (state waves groups 0-3, prologue waves 4-7; 16 rows
+    // per wave)
     const int rrow = 16 * (w & 3) + (lane >> 2);
-    const int ng = (w < 4 ? 4 : 0) + (lane & 3);
+    const int ng = (state_wave ? 0 : 4) + (lane & 3);
     auto load_rows = [&](int c) {
       const int t = min(c * kChunk + rrow, L - 1);
       PipeRows r;
@@ -380,9 +381,11 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
     // bias, rotation, scaling and bf16 rounding of chunk c's rows (lane = row
     // rrow, channels 8 ng .. 8 ng + 7; mamba_fused.py:112-135, 151). The state
     // waves take channel groups 0-3, which hold the rotated pairs when R <= 16,
-    // and the output waves groups 4-7, so each SIMD gets one of each; a wave's
-    // 16 rows x 4 groups make its row loads 16 pieces of 64 contiguous bytes
-    // (a row per lane would touch 64 cache lines per load).
+    // and the prologue waves groups 4-7 (first in their interval A, whose
+    // score tiles and controls are short), so the output waves' interval A
+    // holds only their own tile's work; a wave's 16 rows x 4 groups make its
+    // row loads 16 pieces of 64 contiguous bytes (a row per lane would touch
+    // 64 cache lines per load).
     auto rotary = [&](const PipeRows& in, int c) {
       const int cb = c & 1, cr = c % 3;
       const bool valid = c * kChunk + rrow < L;
@@ -441,9 +444,9 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
     for (int i = 0; i < RPW; ++i) th[i] = 0.f;
     PipeRows rows = {};
     PipeCtl ctl_next = {};
-    // output and state waves: chunk c0's rows before the start's barrier, so
+    // state and prologue waves: chunk c0's rows before the start's barrier, so
     // that their latency overlaps the first controls and phase
-    if (w < 8) rows = load_rows(c0);
+    if (w >= 4) rows = load_rows(c0);
     // A seeded segment's entering state: the segment scan of the unit's
     // summaries of the segments before it, S <- S 2^dec_g + summary_g for
     // g < seg, float4 f = threadIdx.x (and + 768) of the record layout, left in
@@ -518,13 +521,13 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
         zr[0] = *reinterpret_cast<const u32x4*>(zrow);
         zr[1] = *reinterpret_cast<const u32x4*>(zrow + 8);
       };
-      // rows (loaded above), then z, then stores: the order of every later iteration
+      // z, then stores: the order of every later iteration
       __builtin_amdgcn_sched_barrier(0);
       u32x4 zr[2];
       load_z(c0, zr);
       __builtin_amdgcn_sched_barrier(0);
       // dropped stores, so the walk starts with the same outstanding
-      // operations (rows, z, stores) as every later iteration
+      // operations (z, stores) as every later iteration
 #pragma unroll
       for (int g = 0; g < (OUT32 ? 4 : 2); ++g)
         __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, out_rsrc, kOutOfRange, 0, 0);
@@ -534,7 +537,6 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
       for (int e = 0; e < 16; ++e) gate[e] = 0.f;
       for (int i = c0; i <= c1; ++i) {
         // ---------------- interval A(i) ----------------
-        if (i < c1) rotary(rows, i);
         if (i > c0) {
           // silu factors of chunk i - 1 from its gate rows (loaded at A(i - 1))
           // columns 8 g + 4 hh .. + 3 of the tile layout: hh = 0 keeps its
@@ -572,7 +574,6 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
 #pragma unroll
           for (int e = 0; e < 16; ++e) asm volatile("" : "+v"(gate[e]));
         }
-        rows = load_rows(i + 1);
         load_z(i, zr);
         if (i > c0) {
           // chunk c = i - 1, tile (th, pt) of y^T[p][t]: (D + gamma (q + qb).(k + kb)) v
@@ -744,6 +745,8 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
         // ---------------- interval A(i) ----------------
         // angles of chunk i + 1, for the phase at B(i)
         load_pipe_angles<RPW, ANG16>(P, th, gbase, pair, (i + 1) * kChunk + sg * RPW, L);
+        if (i < c1) rotary(rows, i);
+        rows = load_rows(i + 1);
         if (p_idx < 3 && i > c0) {
           // scores of chunk i - 1: tile (th, uh) = (0,0), (1,0), (1,1)
           const int c = i - 1;
