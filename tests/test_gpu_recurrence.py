@@ -142,6 +142,24 @@ def test_variable_length_batch(variant):
         assert torch.equal(y_full[i, :n], y[i, :n])
 
 
+@pytest.mark.parametrize("variant", ["pipe"])
+def test_variable_length_batch_64_rows_with_ties(variant):
+    """B=64 x 8 heads (512 units) with many equal lengths and zero lengths: the
+    pipelined walk deals batch rows longest first; every unit must still be
+    walked exactly once (oracle parity, padded rows exactly 0)."""
+    b, t = 64, 200
+    args = clip_inputs(b, t, heads=8, seed=13)
+    needs(variant, args)
+    base = [0, 1, 64, 65, 128, 200, 137, 63]
+    lengths = torch.tensor([base[i % 8] for i in range(b)], dtype=torch.int64)
+    print(f"case b64 ties variant={variant}", flush=True)
+    ref = fused_mamba_chunked(*args, lengths=lengths)
+    y = run(args, variant, lengths=lengths)
+    assert max_rel(y, ref) <= MAX_REL
+    for i, n in enumerate(lengths.tolist()):
+        assert torch.all(y[i, n:] == 0)
+
+
 @pytest.mark.parametrize("variant", VARIANTS)
 def test_model_layout_strides(variant):
     """Operands as the Mamba block passes them: v/z/trap/ddt are column slices

@@ -793,6 +793,7 @@ MfmaParams make_params(const tf_mamba_args& a) {
   P.chunk_phase = nullptr;
   P.seg_decay = nullptr;
   P.phase_fx = nullptr;
+  P.lpt = 0;
   P.ctl_raw = a.dt_bias != nullptr;
   P.ctl_bf16 = a.dt_dtype == TF_BFLOAT16;
   P.a_floor = a.a_floor;

@@ -188,6 +188,38 @@ __device__ __forceinline__ PipeItem pipe_item(const MfmaParams& P) {
   return it;
 }
 
+// Work item of an unsegmented varlen walk with P.lpt set (B <= 64, B % 8 ==
+// 0, more units than CUs): the batch rows ranked by chunk count (more first,
+// then lower index), rank r dealt to XCD r mod 8 in snake order (r = 8 k + x,
+// or 8 k + 7 - x on odd rounds k), and each XCD's rows taken in rank order,
+// all heads of a row together. The longest units take the first CU slots and
+// the short ones fill in behind them. Every wave ranks the rows itself (lane
+// = batch row), so the result is wave-uniform with no exchange.
+__device__ __forceinline__ PipeItem pipe_item_lpt(const MfmaParams& P, int lane) {
+  const int x = static_cast<int>(blockIdx.x & 7), pos = static_cast<int>(blockIdx.x >> 3);
+  const int k = pos / P.H;
+  PipeItem it;
+  it.h = pos - k * P.H;
+  const int r = 8 * k + ((k & 1) ? 7 - x : x);
+  const int B = P.units / P.H;
+  int c = -1;  // chunk count of batch row `lane`
+  if (lane < B) {
+    const int64_t l = P.lengths[lane];
+    c = static_cast<int>(((l < 0 ? 0 : (l > P.T ? P.T : l)) + kChunk - 1) / kChunk);
+  }
+  int rank = 0;
+  for (int u = 0; u < B; ++u) {
+    const int cu = __builtin_amdgcn_readlane(c, u);
+    rank += (cu > c || (cu == c && u < lane)) ? 1 : 0;
+  }
+  const uint64_t hit = __ballot(lane < B && rank == r);
+  it.b = __builtin_amdgcn_readfirstlane(static_cast<int>(__builtin_ctzll(hit)));
+  it.seg = 0;
+  it.unit = it.b * P.H + it.h;
+  it.rec = it.unit;
+  return it;
+}
+
 // Fixed-point phase increment of one (row, pair): pi tanh(theta) dt radians
 // (mamba_fused.py:102-109) = tanh(theta) dt / 2 revolutions, reduced to
 // [-1/2, 1/2] and scaled by 2^32. A row without a step (dt = 0) adds 0.
@@ -260,7 +292,7 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
   const bool state_wave = w >= 4 && w < 8;
   const int s_idx = w - 4;  // state wave index (state waves)
   const int p_idx = w - 8;  // prologue wave index (prologue waves)
-  const PipeItem it = pipe_item(P);
+  const PipeItem it = (!SEEDED && P.lpt) ? pipe_item_lpt(P, lane) : pipe_item(P);
   const int b = it.b, h = it.h, seg = it.seg, unit = it.unit, rec = it.rec;
   const int qh = h / P.group;
   const int T = P.T;
@@ -781,19 +813,20 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
 
   {
     // rows in [L, T) of the segment's time range (the whole range with one
-    // segment), the same rows in either direction: unreversed base and stride
-    constexpr int PD = 64;
+    // segment), the same rows in either direction: unreversed base and
+    // stride; 16 pieces per row (16 bytes of fp32, 8 bytes of bf16: the
+    // alignment the output rows are checked for)
     const int o_st = P.rev ? -P.o_st : P.o_st;
     const int obase_fwd = b * P.o_sb + h * P.o_sh;
     const int r0 = max(L, seg * P.SC * kChunk);
     const int r1 = seg == P.G - 1 ? T : min(T, (seg + 1) * P.SC * kChunk);
-    for (int e = r0 * PD + static_cast<int>(threadIdx.x); e < r1 * PD; e += 768) {
-      const int tt = e / PD, p = e - tt * PD;
-      const int off = obase_fwd + tt * o_st + p;
+    for (int e = r0 * 16 + static_cast<int>(threadIdx.x); e < r1 * 16; e += 768) {
+      const int tt = e >> 4, piece = e & 15;
+      const int off = obase_fwd + tt * o_st + 4 * piece;
       if constexpr (OUT32)
-        static_cast<float*>(P.out)[off] = 0.f;
+        *reinterpret_cast<float4*>(static_cast<float*>(P.out) + off) = make_float4(0.f, 0.f, 0.f, 0.f);
       else
-        static_cast<uint16_t*>(P.out)[off] = 0;
+        *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(P.out) + off) = u32x2{0u, 0u};
     }
   }
 }
@@ -1227,6 +1260,8 @@ int launch_pipe(const tf_mamba_args& a, hipStream_t stream) {
   }
   const int64_t items = static_cast<int64_t>(P.units) * P.G;
   P.xcd_per = (items % 8 == 0 && items >= 64) ? static_cast<int>(items / 8) : 0;
+  // unsegmented varlen walks over more units than CUs: longest rows first
+  P.lpt = (a.lengths != nullptr && P.G == 1 && a.batch <= 64 && a.batch % 8 == 0 && items > 256) ? 1 : 0;
   return a.rotary <= 16 ? launch_pipe_rpw<4>(P, stream) : launch_pipe_rpw<8>(P, stream);
 }
 

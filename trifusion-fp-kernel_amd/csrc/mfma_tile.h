@@ -242,6 +242,8 @@ struct MfmaParams {
   // Pipelined kernel's chunk-parallel form: per (unit, segment) and rotary
   // pair the wrapping sum of its fixed-point phase increments ([G][32]).
   uint32_t* phase_fx;
+  // Pipelined kernel, unsegmented varlen walks: deal batch rows longest first.
+  int lpt;
 };
 
 // One step of the segment scan, S 2^dec + summary, as explicit fused
