@@ -476,8 +476,24 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
     for (int i = 0; i < RPW; ++i) th[i] = 0.f;
     PipeRows rows = {};
     PipeCtl ctl_next = {};
-    // state and prologue waves: chunk c0's rows before the start's barrier, so
-    // that their latency overlaps the first controls and phase
+    // The start's loads, all issued before any of them is used (a wave's loads
+    // complete in order): the prologue waves' controls, angles and steps of
+    // chunk c0 (every prologue wave loads the controls rows, wave 11 uses
+    // them, so their count in each wave's outstanding loads is the same on
+    // every path), then the rows of the state and prologue waves, then a
+    // seeded segment's summaries.
+    PipeCtl ctl0 = {};
+    float dts[RPW];
+    if (w >= 8) {
+      ctl0 = load_pipe_ctl<CTL16, TRAP16>(P, dto, ado, trb, c0 * kChunk + lane, L, tlim);
+      ctl_next = load_pipe_ctl<CTL16, TRAP16>(P, dto, ado, trb, (c0 + 1) * kChunk + lane, L, tlim);
+      load_pipe_angles<RPW, ANG16>(P, th, gbase, pair, c0 * kChunk + sg * RPW, L);
+      // chunk c0's steps for the phase, read here rather than from the
+      // controls' LDS rows, so that the phase does not wait for a barrier
+#pragma unroll
+      for (int i = 0; i < RPW; ++i)
+        dts[i] = load_elem<CTL16>(P.dt, dto + min(c0 * kChunk + sg * RPW + i, L - 1) * P.d_st);
+    }
     if (w >= 4) rows = load_rows(c0);
     // A seeded segment's entering state: the segment scan of the unit's
     // summaries of the segments before it, S <- S 2^dec_g + summary_g for
@@ -513,20 +529,11 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
       if (f1 < 1024) seed_lds[f1 >> 9][f1 & 511] = run1;
     }
     if (w >= 8) {
-      // every prologue wave loads the controls rows (wave 11 uses them), so
-      // their count in each wave's outstanding loads is the same on every path
-      const PipeCtl ctl0 = load_pipe_ctl<CTL16, TRAP16>(P, dto, ado, trb, c0 * kChunk + lane, L, tlim);
-      ctl_next = load_pipe_ctl<CTL16, TRAP16>(P, dto, ado, trb, (c0 + 1) * kChunk + lane, L, tlim);
-      load_pipe_angles<RPW, ANG16>(P, th, gbase, pair, c0 * kChunk + sg * RPW, L);
-      // chunk c0's steps for the phase, read here rather than from the
-      // controls' LDS rows, so that the phase does not wait for a barrier
-      float dts[RPW];
 #pragma unroll
       for (int i = 0; i < RPW; ++i) {
-        const int t = c0 * kChunk + sg * RPW + i;
-        float d = load_elem<CTL16>(P.dt, dto + min(t, L - 1) * P.d_st);
+        float d = dts[i];
         if (P.ctl_raw) d = control_step(d, step_bias);
-        dts[i] = t < L ? d : 0.f;
+        dts[i] = c0 * kChunk + sg * RPW + i < L ? d : 0.f;
       }
       if (w == 11) controls(ctl0, c0);
       if (phase_wave) phase_steps(th, dts, c0);
