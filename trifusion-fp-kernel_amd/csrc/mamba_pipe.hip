@@ -579,23 +579,17 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
         if (i > c0) {
           // silu factors of chunk i - 1 from its gate rows (loaded at A(i - 1))
           // columns 8 g + 4 hh .. + 3 of the tile layout: hh = 0 keeps its
-          // g = 0, 1 pieces and takes g = 2, 3 from lane ^ 32, hh = 1 the reverse
+          // g = 0, 1 pieces and takes g = 2, 3 from lane ^ 32, hh = 1 the
+          // reverse. v_permlane32_swap(a, b) trades a's upper 32 lanes with
+          // b's lower 32, so one swap per word pair does it in registers.
           u32x2 zt[4];
-          {
-            uint32_t snd[4], rcv[4];
 #pragma unroll
-            for (int k = 0; k < 2; ++k) {
-              snd[2 * k] = hh ? zr[k][0] : zr[k][2];
-              snd[2 * k + 1] = hh ? zr[k][1] : zr[k][3];
-            }
+          for (int k = 0; k < 2; ++k) {
 #pragma unroll
-            for (int k = 0; k < 4; ++k) rcv[k] = static_cast<uint32_t>(__shfl_xor(static_cast<int>(snd[k]), 32));
-#pragma unroll
-            for (int k = 0; k < 2; ++k) {
-              const u32x2 own = hh ? u32x2{zr[k][2], zr[k][3]} : u32x2{zr[k][0], zr[k][1]};
-              const u32x2 got = u32x2{rcv[2 * k], rcv[2 * k + 1]};
-              zt[k] = hh ? got : own;
-              zt[k + 2] = hh ? own : got;
+            for (int m = 0; m < 2; ++m) {
+              const auto x = __builtin_amdgcn_permlane32_swap(zr[k][m], zr[k][m + 2], false, false);
+              zt[k][m] = x[0];
+              zt[k + 2][m] = x[1];
             }
           }
 #pragma unroll
@@ -694,25 +688,18 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
                 out_rsrc, lane_off + 32 * g, 0, 0);
         } else {
           // bf16 pieces g (columns 8 g + 4 hh .. + 3) traded with lane ^ 32 into
-          // 32 contiguous bytes per lane: columns 16 hh .. 16 hh + 15
+          // 32 contiguous bytes per lane, columns 16 hh .. 16 hh + 15: after
+          // swapping pieces k and k + 2 (one v_permlane32_swap per word),
+          // both halves hold (first, second) piece of their 16 bytes k
           u32x2 pw[4];
 #pragma unroll
           for (int g = 0; g < 4; ++g) pw[g] = u32x2{pack2(yv[4 * g], yv[4 * g + 1]), pack2(yv[4 * g + 2], yv[4 * g + 3])};
-          uint32_t snd[4], rcv[4];
-#pragma unroll
-          for (int k = 0; k < 2; ++k) {
-            snd[2 * k] = hh ? pw[k][0] : pw[k + 2][0];
-            snd[2 * k + 1] = hh ? pw[k][1] : pw[k + 2][1];
-          }
-#pragma unroll
-          for (int k = 0; k < 4; ++k) rcv[k] = static_cast<uint32_t>(__shfl_xor(static_cast<int>(snd[k]), 32));
           const int lane_off = live ? (mrow * o_row + 32 * opt + 16 * hh) * esz : kOutOfRange;
 #pragma unroll
           for (int k = 0; k < 2; ++k) {
-            const u32x2 own = hh ? pw[k + 2] : pw[k];
-            const u32x2 got = u32x2{rcv[2 * k], rcv[2 * k + 1]};
-            const u32x4 piece = hh ? u32x4{got[0], got[1], own[0], own[1]} : u32x4{own[0], own[1], got[0], got[1]};
-            __builtin_amdgcn_raw_buffer_store_b128(piece, out_rsrc, lane_off + 16 * k, 0, 0);
+            const auto x0 = __builtin_amdgcn_permlane32_swap(pw[k][0], pw[k + 2][0], false, false);
+            const auto x1 = __builtin_amdgcn_permlane32_swap(pw[k][1], pw[k + 2][1], false, false);
+            __builtin_amdgcn_raw_buffer_store_b128(u32x4{x0[0], x1[0], x0[1], x1[1]}, out_rsrc, lane_off + 16 * k, 0, 0);
           }
         }
         lds_barrier();
