@@ -837,10 +837,10 @@ __global__ __launch_bounds__(1024) void pipe_phase_sums_kernel(const MfmaParams 
   constexpr int kLanes = 1024 / PAIRS;  // row lanes per pair
   constexpr int kBatch = 8;
   __shared__ uint32_t part[kLanes][PAIRS];
-  const int unit = blockIdx.x / P.G;
-  const int seg = blockIdx.x - unit * P.G;
-  const int b = unit / P.H;
-  const int h = unit - b * P.H;
+  // the walk's item order: the heads of one segment share an XCD, and with it
+  // the 128-byte angle lines that two neighbouring heads split
+  const PipeItem it = pipe_item(P);
+  const int seg = it.seg, b = it.b, h = it.h;
   int L = P.T;
   if (P.lengths != nullptr) {
     const int64_t l = P.lengths[b];
@@ -882,7 +882,7 @@ __global__ __launch_bounds__(1024) void pipe_phase_sums_kernel(const MfmaParams 
     if (static_cast<int>(threadIdx.x) < PAIRS)
 #pragma unroll
       for (int g = 0; g < kLanes; ++g) sum += part[g][threadIdx.x];
-    P.phase_fx[static_cast<size_t>(blockIdx.x) * 32 + threadIdx.x] = sum;
+    P.phase_fx[static_cast<size_t>(it.rec) * 32 + threadIdx.x] = sum;
   }
 }
 
