@@ -4,9 +4,10 @@ units), for the chunked kernel and, at N = P = 64, the pipelined kernel.
 With fewer (batch, head) units than half the CUs, the time axis is cut into
 segments run by separate workgroups: a phase pre-pass, a summary pass (each
 segment's state contribution and log2 decay from zero), a scan of the segment
-records, then the output pass seeded with each segment's entering state and
-phase. The tests check, on shapes that take this path (the workspace query is
-> 0):
+records (its own launch for the chunked kernel, the start of each walk for the
+pipelined one), then the output pass seeded with each segment's entering state
+and phase. The tests check, on shapes that take this path (the workspace query
+is > 0):
 
 * parity with the CPU oracle at the recurrence tolerance, for both phase-lane
   widths, N = 32/64/128 and variable lengths;
@@ -106,19 +107,23 @@ def test_segments_graph_replay_matches_eager():
             assert torch.equal(out, eager)
 
 
-def test_segments_bitwise_equal_serial_walk_b1_l1000_h4():
-    """B1 L1000 H4 (16 chunks, 4 units) runs in two segments. The second
-    segment's entering state is the first segment's summary from zero, the
-    same operations in the same order as the serial walk's state after 8
-    chunks, so the two forms agree bit for bit."""
-    args = clip_inputs(1, 1000, heads=4, head_dim=64, state=64, rotary=16, qk_heads=1, seed=11)
+@pytest.mark.parametrize("variant,batch,heads", [("mfma", 1, 4), ("pipe", 8, 16)])
+def test_segments_bitwise_equal_serial_walk_l1000(variant, batch, heads):
+    """L1000 (16 chunks) runs in two segments: B1 H4 for the chunked kernel,
+    B8 H16 (128 units) for the pipelined one. The second segment's entering
+    state is the first segment's summary from zero (for the pipelined form
+    the chunk-parallel summary, then the walk's scan step 0 * m + summary),
+    the same operations in the same order as the serial walk's state after 8
+    chunks, and the phase carry is an exact integer sum, so the two forms
+    agree bit for bit."""
+    args = clip_inputs(batch, 1000, heads=heads, head_dim=64, state=64, rotary=16, qk_heads=1, seed=11)
     dargs = tuple(x.to(DEV) for x in args)
-    print("case segments_vs_serial_bitwise_b1_l1000_h4", flush=True)
+    print(f"case segments_vs_serial_bitwise variant={variant} B={batch} H={heads} L1000", flush=True)
     with torch.inference_mode():
         out = torch.empty(dargs[2].shape, device=DEV, dtype=torch.float32)
-        assert _workspace_bytes(dargs, out, None) > 0
-        y = fused_mamba(*dargs, out=out, variant="mfma").clone()
-        ys = _serial(dargs, torch.empty_like(out), None)
+        assert _workspace_bytes(dargs, out, None, variant) > 0
+        y = fused_mamba(*dargs, out=out, variant=variant).clone()
+        ys = _serial(dargs, torch.empty_like(out), None, variant)
     torch.cuda.synchronize()
     assert torch.equal(y, ys)
 
