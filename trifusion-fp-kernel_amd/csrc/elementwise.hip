@@ -366,21 +366,23 @@ __global__ __launch_bounds__(256) void masked_mean_kernel(const T* __restrict__ 
 // Masked mean over 128-byte column slices. Workgroup (slice, b, split) sums
 // frames [split*span, (split+1)*span) of clip b, clipped to its valid prefix,
 // for the V*8 columns of the slice (V = 16 / sizeof(T) per lane): lane l of
-// wave w loads 16 bytes at column V*(l % 8) of frame 8*w + l / 8 + 128*j, four
-// frames in flight per lane. The 8 lanes of a column block meet by xor
-// shuffles, the 16 waves through LDS in wave order, so the sum's order is fixed
-// by (span, split count) alone. One split: y = sum / lengths[b]; more: the sum
+// wave w loads 16 bytes at column V*(l % 8) of frame 8*w + l / 8 + 64*j, eight
+// frames in flight per lane, and a lane issues no load past the span's end.
+// Lanes l and l^8 meet by a DPP row rotation, then l and l^16 by a swizzle;
+// lanes 0-7 and 32-39 of the 8 waves write 16 partial rows to LDS, which one
+// thread per column adds in row order, so the sum's order is fixed by
+// (span, split count) alone. One split: y = sum / lengths[b]; more: the sum
 // goes to partial[split, b, :] and masked_mean_finish_kernel adds the splits in
 // order.
 template <typename T>
-__global__ __launch_bounds__(1024) void masked_mean_slice_kernel(const T* __restrict__ x,
-                                                                 const int64_t* __restrict__ lengths,
-                                                                 float* __restrict__ y, float* __restrict__ partial,
-                                                                 int64_t time, int64_t d, int64_t span) {
+__global__ __launch_bounds__(512) void masked_mean_slice_kernel(const T* __restrict__ x,
+                                                                const int64_t* __restrict__ lengths,
+                                                                float* __restrict__ y, float* __restrict__ partial,
+                                                                int64_t time, int64_t d, int64_t span) {
   constexpr int V = 16 / sizeof(T);
-  constexpr int kWaves = 16;
+  constexpr int kWaves = 8;
   constexpr int kStep = 8 * kWaves;  // frames per pass of the workgroup
-  __shared__ float part[kWaves][8][V];
+  __shared__ float part[2 * kWaves][8][V];
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
   const int64_t b = blockIdx.y;
@@ -395,14 +397,17 @@ __global__ __launch_bounds__(1024) void masked_mean_slice_kernel(const T* __rest
   for (int e = 0; e < V; ++e) acc[e] = 0.f;
   if (col < d) {
     const T* base = x + b * time * d + col;
-    for (int64_t t = t0 + 8 * w + (lane >> 3); t < t1; t += 4 * kStep) {
-      float v[4][V];
+    for (int64_t t = t0 + 8 * w + (lane >> 3); t < t1; t += 8 * kStep) {
+      float v[8][V];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        // every lane loads from a valid frame (t < t1); frames past t1 are dropped after the load
+      for (int u = 0; u < 8; ++u) {
+        // frames past t1 add zero and issue no load
         const int64_t tu = t + u * kStep;
-        const T* src = base + (tu < t1 ? tu : t) * d;
-        if constexpr (sizeof(T) == 4) {
+        const T* src = base + tu * d;
+        if (tu >= t1) {
+#pragma unroll
+          for (int e = 0; e < V; ++e) v[u][e] = 0.f;
+        } else if constexpr (sizeof(T) == 4) {
           const float4 f = *reinterpret_cast<const float4*>(src);
           v[u][0] = f.x, v[u][1] = f.y, v[u][2] = f.z, v[u][3] = f.w;
         } else {
@@ -416,21 +421,22 @@ __global__ __launch_bounds__(1024) void masked_mean_slice_kernel(const T* __rest
         }
       }
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
-        if (t + u * kStep < t1)
+      for (int u = 0; u < 8; ++u)
 #pragma unroll
-          for (int e = 0; e < V; ++e) acc[e] += v[u][e];
+        for (int e = 0; e < V; ++e) acc[e] += v[u][e];
     }
   }
+  constexpr int kRowRor8 = 0x128;     // DPP row_ror:8: lane l reads lane l^8 of its row of 16
+  constexpr int kSwizzleXor16 = 0x401f;  // ds_swizzle bit mode, xor mask 16: lane l reads lane l^16
 #pragma unroll
   for (int e = 0; e < V; ++e) {
-    acc[e] += __shfl_xor(acc[e], 8);
-    acc[e] += __shfl_xor(acc[e], 16);
-    acc[e] += __shfl_xor(acc[e], 32);
+    const int a = __builtin_bit_cast(int, acc[e]);
+    acc[e] += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, a, kRowRor8, 0xf, 0xf, false));
+    acc[e] += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, acc[e]), kSwizzleXor16));
   }
-  if (lane < 8)
+  if ((lane & 24) == 0)
 #pragma unroll
-    for (int e = 0; e < V; ++e) part[w][lane][e] = acc[e];
+    for (int e = 0; e < V; ++e) part[2 * w + (lane >> 5)][lane & 7][e] = acc[e];
   __syncthreads();
   const int c = threadIdx.x;  // column of the slice this thread finishes
   if (c >= 8 * V) return;
@@ -438,7 +444,7 @@ __global__ __launch_bounds__(1024) void masked_mean_slice_kernel(const T* __rest
   if (out_col >= d) return;
   float sum = 0.f;
 #pragma unroll
-  for (int i = 0; i < kWaves; ++i) sum += part[i][c / V][c % V];
+  for (int i = 0; i < 2 * kWaves; ++i) sum += part[i][c / V][c % V];
   if (gridDim.z == 1)
     y[b * d + out_col] = sum / static_cast<float>(len);
   else
@@ -727,7 +733,7 @@ extern "C" int tf_masked_mean(const void* x, int32_t dtype, const int64_t* lengt
     const dim3 grid(static_cast<uint32_t>(m.slices), static_cast<uint32_t>(batch), static_cast<uint32_t>(m.splits));
     float* partial = static_cast<float*>(workspace);
     TF_DISPATCH(dtype, T,
-                hipLaunchKernelGGL(tf::masked_mean_slice_kernel<T>, grid, dim3(1024), 0, s,
+                hipLaunchKernelGGL(tf::masked_mean_slice_kernel<T>, grid, dim3(512), 0, s,
                                    static_cast<const T*>(x), lengths, y, partial, time, d, m.span);
                 if (m.splits > 1) hipLaunchKernelGGL(tf::masked_mean_finish_kernel,
                                                      dim3(tf::blocks_for(batch * d, 256)), dim3(256), 0, s,
