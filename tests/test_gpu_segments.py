@@ -2,11 +2,13 @@
 units), for the chunked kernel and, at N = P = 64, the pipelined kernel.
 
 With fewer (batch, head) units than half the CUs, the time axis is cut into
-segments run by separate workgroups: a phase pre-pass, a summary pass (each
-segment's state contribution and log2 decay from zero), a scan of the segment
-records (its own launch for the chunked kernel, the start of each walk for the
-pipelined one), then the output pass seeded with each segment's entering state
-and phase. The tests check, on shapes that take this path (the workspace query
+segments run by separate workgroups: a summary pass (each segment's state
+contribution and log2 decay from zero; the chunked kernel's after a phase
+pre-pass, the pipelined kernel's in the segment's own phase frame, with its
+phase sums), a scan of the segment records (its own launch for the chunked
+kernel, the start of each walk for the pipelined one, which turns each record
+by the phase entering its segment), then the output pass seeded with each
+segment's entering state and phase. The tests check, on shapes that take this path (the workspace query
 is > 0):
 
 * parity with the CPU oracle at the recurrence tolerance, for both phase-lane
@@ -114,8 +116,9 @@ def test_segments_bitwise_equal_serial_walk_l1000(variant, batch, heads):
     state is the first segment's summary from zero (for the pipelined form
     the chunk-parallel summary, then the walk's scan step 0 * m + summary),
     the same operations in the same order as the serial walk's state after 8
-    chunks, and the phase carry is an exact integer sum, so the two forms
-    agree bit for bit."""
+    chunks (the first segment's phase frame is the unit's, so its record is
+    used unturned), and the phase carry is an exact integer sum, so the two
+    forms agree bit for bit."""
     args = clip_inputs(batch, 1000, heads=heads, head_dim=64, state=64, rotary=16, qk_heads=1, seed=11)
     dargs = tuple(x.to(DEV) for x in args)
     print(f"case segments_vs_serial_bitwise variant={variant} B={batch} H={heads} L1000", flush=True)

@@ -236,6 +236,24 @@ __device__ __forceinline__ float2 phase_trig(uint32_t ph) {
   return make_float2(__builtin_amdgcn_cosf(rev), __builtin_amdgcn_sinf(rev));
 }
 
+// Rows (2 rp, 2 rp + 1) and (2 rp + 2, 2 rp + 3) of a state record, the rotary
+// pairs rp and rp + 1, turned by phases ph (the key rotation of key_pair,
+// applied to the rows kr contributes to); pairs >= R are left as they are.
+__device__ __forceinline__ float4 turn_rows(const float4& d, uint2 ph, int rp, int R) {
+  float4 o = d;
+  if (rp < R) {
+    const float2 a = phase_trig(ph.x);
+    o.x = __builtin_fmaf(d.x, a.x, -(d.y * a.y));
+    o.y = __builtin_fmaf(d.x, a.y, d.y * a.x);
+  }
+  if (rp + 1 < R) {
+    const float2 a = phase_trig(ph.y);
+    o.z = __builtin_fmaf(d.z, a.x, -(d.w * a.y));
+    o.w = __builtin_fmaf(d.z, a.y, d.w * a.x);
+  }
+  return o;
+}
+
 // Controls of one chunk, one wave, lane = row (mamba_fused.py:96-101, 139-142):
 // step, key scale, inclusive log2 decay, 2^(tot - cs), dt sigmoid(trap), and
 // the chunk's total log2 decay (every lane).
@@ -496,32 +514,57 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
     }
     if (w >= 4) rows = load_rows(c0);
     // A seeded segment's entering state: the segment scan of the unit's
-    // summaries of the segments before it, S <- S 2^dec_g + summary_g for
-    // g < seg, float4 f = threadIdx.x (and + 768) of the record layout, left in
-    // the second chunk's qr/kr buffers (tiles 0-1, 2-3) for the state waves.
+    // summaries of the segments before it, S <- S 2^dec_g + turn_g(summary_g)
+    // for g < seg, float4 f = threadIdx.x (and + 768) of the record layout,
+    // left in the second chunk's qr/kr buffers (tiles 0-1, 2-3) for the state
+    // waves. Summary g is formed in segment g's phase frame (phase 0 at its
+    // start); turn_g rotates its rotary row pairs by the phase entering the
+    // segment, the wrapping sum of the earlier segments' phase sums (kr of the
+    // unit's frame is that rotation of kr of the segment's frame). Segment 0
+    // starts at phase 0 and is used as it is.
     [[maybe_unused]] float4* seed_lds[2] = {reinterpret_cast<float4*>(sh.qr[(c0 + 1) & 1]),
                                             reinterpret_cast<float4*>(sh.kr[(c0 + 1) & 1])};
     if constexpr (SEEDED) {
       const int f0 = static_cast<int>(threadIdx.x), f1 = f0 + 768;
       const float4* sums = P.seg_state + static_cast<size_t>(unit) * P.G * 1024;
       const float* decs = P.seg_decay + unit * P.G;
+      const uint2* phs = reinterpret_cast<const uint2*>(P.phase_fx + static_cast<size_t>(unit) * P.G * 32);
+      // float4 f holds rows 32 (f >> 9) + 8 ((f >> 6) & 3) + 4 ((f >> 5) & 1)
+      // + 0..3 of the record's S^T (the 32 x 32 tile layout): rotary pairs
+      // rp(f) and rp(f) + 1
+      const int rp0 = 16 * (f0 >> 9) + 4 * ((f0 >> 6) & 3) + 2 * ((f0 >> 5) & 1);
+      const int rp1 = 16 * (f1 >> 9) + 4 * ((f1 >> 6) & 3) + 2 * ((f1 >> 5) & 1);
       float4 run0 = make_float4(0.f, 0.f, 0.f, 0.f), run1 = run0;
+      uint2 ph0 = make_uint2(0u, 0u), ph1 = ph0;  // phase entering segment g, pairs rp, rp + 1
       for (int g0 = 0; g0 < seg; g0 += kSeedBatch) {
         float4 d0[kSeedBatch], d1[kSeedBatch];
+        uint2 s0[kSeedBatch], s1[kSeedBatch];
         float m[kSeedBatch];
 #pragma unroll
         for (int j = 0; j < kSeedBatch; ++j) {
           if (g0 + j < seg) {
             d0[j] = sums[static_cast<size_t>(g0 + j) * 1024 + f0];
-            if (f1 < 1024) d1[j] = sums[static_cast<size_t>(g0 + j) * 1024 + f1];
+            s0[j] = phs[(g0 + j) * 16 + rp0 / 2];
+            if (f1 < 1024) {
+              d1[j] = sums[static_cast<size_t>(g0 + j) * 1024 + f1];
+              s1[j] = phs[(g0 + j) * 16 + rp1 / 2];
+            }
             m[j] = fast_exp2(decs[g0 + j]);
           }
         }
 #pragma unroll
         for (int j = 0; j < kSeedBatch; ++j) {
           if (g0 + j < seg) {
+            if (g0 + j > 0) {
+              d0[j] = turn_rows(d0[j], ph0, rp0, R);
+              if (f1 < 1024) d1[j] = turn_rows(d1[j], ph1, rp1, R);
+            }
             run0 = state_step(run0, m[j], d0[j]);
-            if (f1 < 1024) run1 = state_step(run1, m[j], d1[j]);
+            ph0 = make_uint2(ph0.x + s0[j].x, ph0.y + s0[j].y);
+            if (f1 < 1024) {
+              run1 = state_step(run1, m[j], d1[j]);
+              ph1 = make_uint2(ph1.x + s1[j].x, ph1.y + s1[j].y);
+            }
           }
         }
       }
@@ -825,67 +868,6 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
   }
 }
 
-// Fixed-point phase sums of each (unit, segment) and rotary pair for the
-// chunk-parallel form: the increments the walk's phase stage forms (tanh(theta)
-// dt / 2 revolutions, reduced to [-1/2, 1/2], times 2^32; rows past the length
-// add nothing), added as wrapping 32-bit integers, so that any order of
-// addition gives the serial walk's bits. Thread (pair, row lane) of 16 x 64
-// (R <= 16; 32 x 32 above) strides over the segment's rows, loads batched 8 at
-// a time (one batch for a 512-row segment at R <= 16); LDS adds the row lanes.
-template <bool CTL16, bool ANG16, int PAIRS>
-__global__ __launch_bounds__(1024) void pipe_phase_sums_kernel(const MfmaParams P) {
-  constexpr int kLanes = 1024 / PAIRS;  // row lanes per pair
-  constexpr int kBatch = 8;
-  __shared__ uint32_t part[kLanes][PAIRS];
-  // the walk's item order: the heads of one segment share an XCD, and with it
-  // the 128-byte angle lines that two neighbouring heads split
-  const PipeItem it = pipe_item(P);
-  const int seg = it.seg, b = it.b, h = it.h;
-  int L = P.T;
-  if (P.lengths != nullptr) {
-    const int64_t l = P.lengths[b];
-    L = l < 0 ? 0 : (l > P.T ? P.T : static_cast<int>(l));
-  }
-  const int roff = P.rev ? max(L - 1, 0) : 0;
-  const int dto = b * P.d_sb + h * P.d_sh - roff * P.d_st;
-  const int gbase = b * P.g_sb + h * P.g_sh - roff * P.g_st;
-  const float step_bias = P.ctl_raw ? P.dt_bias[h] : 0.f;
-  const int r = threadIdx.x % PAIRS;
-  const int rl = threadIdx.x / PAIRS;
-  const int t_begin = seg * P.SC * kChunk;
-  const int t_end = min(t_begin + P.SC * kChunk, L);
-  uint32_t acc = 0;
-  if (r < P.R) {
-    for (int t0 = t_begin + rl; t0 < t_end; t0 += kBatch * kLanes) {
-      float dt[kBatch], th[kBatch];
-#pragma unroll
-      for (int j = 0; j < kBatch; ++j) {
-        // rows clamped to the segment's last valid row, masked below: every
-        // load of the batch is issued before the first use
-        const int t = min(t0 + j * kLanes, t_end - 1);
-        dt[j] = load_elem<CTL16>(P.dt, dto + t * P.d_st);
-        th[j] = load_elem<ANG16>(P.angles, gbase + r * P.g_sr + t * P.g_st);
-      }
-#pragma unroll
-      for (int j = 0; j < kBatch; ++j) {
-        float step = dt[j];
-        if (P.ctl_raw) step = control_step(step, step_bias);
-        const uint32_t x = phase_inc(th[j], step);
-        if (t0 + j * kLanes < t_end) acc += x;
-      }
-    }
-  }
-  part[rl][r] = acc;
-  __syncthreads();
-  if (threadIdx.x < 32) {
-    uint32_t sum = 0;
-    if (static_cast<int>(threadIdx.x) < PAIRS)
-#pragma unroll
-      for (int g = 0; g < kLanes; ++g) sum += part[g][threadIdx.x];
-    P.phase_fx[static_cast<size_t>(it.rec) * 32 + threadIdx.x] = sum;
-  }
-}
-
 // LDS of the summary pass: a batch of four chunks (256 rows).
 template <int PAIRS>
 struct SummarySmem {
@@ -915,14 +897,18 @@ struct SummarySmem {
 //     first waves the controls of one chunk each (lane = row); the batch's
 //     loads were issued during the previous batch;
 //   - wave j scans pair j's increments over the batch's rows, from the phase
-//     entering the batch, into the cos/sin table;
+//     entering the batch (0 at the segment's start), into the cos/sin table;
 //   - every thread rotates and scales the keys of one channel group and
 //     scales the values, for two rows (8 lanes per row);
 //   - wave w computes the 32 x 32 tile w mod 4 of dS for chunk w / 4;
 //   - thread f folds float4 f of the four dS_c into the state, in chunk order.
 // These are the serial walk's operations, in its order (its shared helpers,
 // with the multiply-adds spelled out), so the record is the one a serial walk
-// of the segment from zero state leaves.
+// of the segment from zero state and phase leaves: for the first segment, the
+// serial walk's own state after it. The record of a later segment is in that
+// segment's phase frame, and the walks turn it by the phase entering the
+// segment, which they form from the wrapping phase sums this pass also
+// writes (the same integers the serial walk adds).
 template <bool CTL16, bool TRAP16, bool ANG16, int PAIRS>
 __global__ __launch_bounds__(1024) void pipe_summary_kernel(const MfmaParams P) {
   constexpr int kBatch = 4;                      // chunks per batch
@@ -956,17 +942,10 @@ __global__ __launch_bounds__(1024) void pipe_summary_kernel(const MfmaParams P) 
   const int gbase = b * P.g_sb + h * P.g_sh - roff * P.g_st;
   const float step_bias = P.ctl_raw ? P.dt_bias[h] : 0.f;
 
-  // phase entering the segment for the wave's scan pairs: the wrapping sum
-  // of the earlier segments' sums
-  uint32_t carry[kSlots];
-#pragma unroll
-  for (int k = 0; k < kSlots; ++k) {
-    const int j = w + 16 * k;
-    uint32_t part = 0;
-    if (j < R)
-      for (int g = lane; g < it.seg; g += 64) part += P.phase_fx[(static_cast<size_t>(it.unit) * P.G + g) * 32 + j];
-    carry[k] = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(wave_scan_u32(part)), 63));
-  }
+  // phase of the wave's scan pairs from the segment's start (the segment's
+  // own frame; the walks turn the record into the unit's frame)
+  uint32_t carry[kSlots] = {};
+  const int t_stop = min(L, c1 * kChunk);  // rows past the segment add no phase
   const int pj = tid % PAIRS;   // phase lanes: pair
   const int prl = tid / PAIRS;  // and row lane
   // key rotation tasks: channel group ng of batch rows rsub and rsub + 128
@@ -1014,7 +993,7 @@ __global__ __launch_bounds__(1024) void pipe_summary_kernel(const MfmaParams P) 
         const int r = prl + kRowLanes * i;
         float d = dts[i];
         if (P.ctl_raw) d = control_step(d, step_bias);
-        sh.b.inc[pj][r] = phase_inc(th[i], t_lo + r < L ? d : 0.f);
+        sh.b.inc[pj][r] = phase_inc(th[i], t_lo + r < t_stop ? d : 0.f);
       }
     }
     // controls of chunk cb0 + w
@@ -1112,6 +1091,12 @@ __global__ __launch_bounds__(1024) void pipe_summary_kernel(const MfmaParams P) 
   }
   P.seg_state[static_cast<size_t>(it.rec) * 1024 + tid] = S;
   if (tid == 0) P.seg_decay[it.rec] = seg_log2;
+  // the segment's phase sum per pair (0 for pairs >= R)
+  if (lane == 0) {
+#pragma unroll
+    for (int k = 0; k < kSlots; ++k) P.phase_fx[static_cast<size_t>(it.rec) * 32 + w + 16 * k] = carry[k];
+    if constexpr (PAIRS == 16) P.phase_fx[static_cast<size_t>(it.rec) * 32 + w + 16] = 0u;
+  }
 }
 
 // Chunk-parallel plan: with at most 128 (batch, head) units, each unit's time
@@ -1134,7 +1119,7 @@ PipePlan pipe_plan(const tf_mamba_args& a) {
   if (units <= 0 || chunks <= 0 || units > 128) return p;
   int64_t g = 256 / units;
   // at least kMinSegmentChunks per segment: shorter walks gain less from the
-  // extra workgroups than the three extra passes cost
+  // extra workgroups than the two extra passes cost
   const int64_t sc = std::max<int64_t>((chunks + g - 1) / g, kMinSegmentChunks);
   g = (chunks + sc - 1) / sc;
   if (g < 2) return p;
@@ -1183,15 +1168,9 @@ template <int RPW, bool CTL16, bool TRAP16, bool ANG16>
 int launch_pipe_kernel(const MfmaParams& P, hipStream_t stream) {
   const dim3 grid(static_cast<uint32_t>(P.units) * P.G), block(768);
   if (P.G > 1) {
-    // phase sums -> segment summaries (from zero state) -> the seeded walks,
-    // which scan the summaries before their segment and write the outputs
-    if (P.R > 0) {
-      if (P.R <= 16)
-        hipLaunchKernelGGL((pipe_phase_sums_kernel<CTL16, ANG16, 16>), grid, dim3(1024), 0, stream, P);
-      else
-        hipLaunchKernelGGL((pipe_phase_sums_kernel<CTL16, ANG16, 32>), grid, dim3(1024), 0, stream, P);
-      if (const int rc = launch_status()) return rc;
-    }
+    // segment summaries (from zero state, each in its segment's phase frame,
+    // with the segment's phase sums) -> the seeded walks, which scan the
+    // summaries before their segment and write the outputs
     if (P.R <= 16)
       hipLaunchKernelGGL((pipe_summary_kernel<CTL16, TRAP16, ANG16, 16>), grid, dim3(1024), 0, stream, P);
     else
