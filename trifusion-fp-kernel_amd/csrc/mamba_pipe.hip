@@ -515,17 +515,18 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
     if (w >= 4) rows = load_rows(c0);
     // A seeded segment's entering state: the segment scan of the unit's
     // summaries of the segments before it, S <- S 2^dec_g + turn_g(summary_g)
-    // for g < seg, float4 f = threadIdx.x (and + 768) of the record layout,
-    // left in the second chunk's qr/kr buffers (tiles 0-1, 2-3) for the state
-    // waves. Summary g is formed in segment g's phase frame (phase 0 at its
-    // start); turn_g rotates its rotary row pairs by the phase entering the
-    // segment, the wrapping sum of the earlier segments' phase sums (kr of the
-    // unit's frame is that rotation of kr of the segment's frame). Segment 0
-    // starts at phase 0 and is used as it is.
+    // for g < seg, float4 f = threadIdx.x and threadIdx.x + 512 of the record
+    // layout on waves 0-7 (the prologue waves go straight to the chunk-0
+    // controls and phase), left in the second chunk's qr/kr buffers (tiles
+    // 0-1, 2-3) for the state waves. Summary g is formed in segment g's phase
+    // frame (phase 0 at its start); turn_g rotates its rotary row pairs by the
+    // phase entering the segment, the wrapping sum of the earlier segments'
+    // phase sums (kr of the unit's frame is that rotation of kr of the
+    // segment's frame). Segment 0 starts at phase 0 and is used as it is.
     [[maybe_unused]] float4* seed_lds[2] = {reinterpret_cast<float4*>(sh.qr[(c0 + 1) & 1]),
                                             reinterpret_cast<float4*>(sh.kr[(c0 + 1) & 1])};
-    if constexpr (SEEDED) {
-      const int f0 = static_cast<int>(threadIdx.x), f1 = f0 + 768;
+    if (SEEDED && w < 8) {
+      const int f0 = static_cast<int>(threadIdx.x), f1 = f0 + 512;
       const float4* sums = P.seg_state + static_cast<size_t>(unit) * P.G * 1024;
       const float* decs = P.seg_decay + unit * P.G;
       const uint2* phs = reinterpret_cast<const uint2*>(P.phase_fx + static_cast<size_t>(unit) * P.G * 32);
@@ -534,6 +535,10 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
       // rp(f) and rp(f) + 1
       const int rp0 = 16 * (f0 >> 9) + 4 * ((f0 >> 6) & 3) + 2 * ((f0 >> 5) & 1);
       const int rp1 = 16 * (f1 >> 9) + 4 * ((f1 >> 6) & 3) + 2 * ((f1 >> 5) & 1);
+      // only pairs < R turn: the second float4 (rows >= 32, pairs >= 16) never
+      // does when R <= 16 (RPW 4)
+      const bool turn0 = rp0 < R;
+      const bool turn1 = RPW > 4 && rp1 < R;
       float4 run0 = make_float4(0.f, 0.f, 0.f, 0.f), run1 = run0;
       uint2 ph0 = make_uint2(0u, 0u), ph1 = ph0;  // phase entering segment g, pairs rp, rp + 1
       for (int g0 = 0; g0 < seg; g0 += kSeedBatch) {
@@ -544,32 +549,30 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
         for (int j = 0; j < kSeedBatch; ++j) {
           if (g0 + j < seg) {
             d0[j] = sums[static_cast<size_t>(g0 + j) * 1024 + f0];
-            s0[j] = phs[(g0 + j) * 16 + rp0 / 2];
-            if (f1 < 1024) {
-              d1[j] = sums[static_cast<size_t>(g0 + j) * 1024 + f1];
-              s1[j] = phs[(g0 + j) * 16 + rp1 / 2];
-            }
+            if (turn0) s0[j] = phs[(g0 + j) * 16 + rp0 / 2];
+            d1[j] = sums[static_cast<size_t>(g0 + j) * 1024 + f1];
+            if (turn1) s1[j] = phs[(g0 + j) * 16 + rp1 / 2];
             m[j] = fast_exp2(decs[g0 + j]);
           }
         }
 #pragma unroll
         for (int j = 0; j < kSeedBatch; ++j) {
           if (g0 + j < seg) {
-            if (g0 + j > 0) {
-              d0[j] = turn_rows(d0[j], ph0, rp0, R);
-              if (f1 < 1024) d1[j] = turn_rows(d1[j], ph1, rp1, R);
+            if (turn0) {
+              if (g0 + j > 0) d0[j] = turn_rows(d0[j], ph0, rp0, R);
+              ph0 = make_uint2(ph0.x + s0[j].x, ph0.y + s0[j].y);
             }
-            run0 = state_step(run0, m[j], d0[j]);
-            ph0 = make_uint2(ph0.x + s0[j].x, ph0.y + s0[j].y);
-            if (f1 < 1024) {
-              run1 = state_step(run1, m[j], d1[j]);
+            if (turn1) {
+              if (g0 + j > 0) d1[j] = turn_rows(d1[j], ph1, rp1, R);
               ph1 = make_uint2(ph1.x + s1[j].x, ph1.y + s1[j].y);
             }
+            run0 = state_step(run0, m[j], d0[j]);
+            run1 = state_step(run1, m[j], d1[j]);
           }
         }
       }
-      seed_lds[f0 >> 9][f0 & 511] = run0;
-      if (f1 < 1024) seed_lds[f1 >> 9][f1 & 511] = run1;
+      seed_lds[0][f0] = run0;
+      seed_lds[1][f0] = run1;
     }
     if (w >= 8) {
 #pragma unroll
