@@ -63,13 +63,36 @@ __device__ __forceinline__ float sigmoidf(float x) { return 1.0f / (1.0f + __exp
 // adt = min(-(relu(a) + 1/(1 - min(a, 0))), -floor) * dt. Shared by the
 // controls kernel and the recurrence's raw-controls prologue, so both give
 // the same bits.
+__device__ __forceinline__ float softplus_le20(float v);
+
 __device__ __forceinline__ float control_step(float ddt, float bias) {
   const float v = ddt + bias;
-  return v > 20.f ? v : log1pf(expf(v));
+  return v > 20.f ? v : softplus_le20(v);
 }
 
 __device__ __forceinline__ float control_decay(float a, float step, float floor_) {
-  return fminf(-(fmaxf(a, 0.f) + 1.f / (1.f - fminf(a, 0.f))), -floor_) * step;
+  return fminf(-(fmaxf(a, 0.f) + __builtin_amdgcn_rcpf(1.f - fminf(a, 0.f))), -floor_) * step;
+}
+
+// softplus(v) = log(1 + e^v) for v <= 20 from the hardware exp2, log2 and
+// reciprocal (each within about 1 ulp), a few ulp in all:
+//   e^v = 2^h (1 + l ln 2) with h + l = v log2(e): h = v L1 rounded, l its
+//   rounding error (one fma) plus v L2, where L1 + L2 = log2(e) to 2^-48;
+//   log(1 + x) = x log(u) / (u - 1) with u = 1 + x rounded, and x itself when
+//   u == 1 (W. Kahan's identity: D. Goldberg, "What every computer scientist
+//   should know about floating-point arithmetic", ACM Computing Surveys 23(1),
+//   1991, Theorem 4).
+__device__ __forceinline__ float softplus_le20(float v) {
+  constexpr float kL1 = 1.4426950216293335f;     // log2(e) rounded to float
+  constexpr float kL2 = 1.925963033500011e-08f;  // log2(e) - kL1
+  constexpr float kLn2 = 0.6931471824645996f;
+  const float h = v * kL1;
+  const float l = __builtin_fmaf(v, kL1, -h) + v * kL2;
+  const float e0 = __builtin_amdgcn_exp2f(h);
+  const float x = __builtin_fmaf(e0, l * kLn2, e0);
+  const float u = 1.f + x;
+  const float r = (__builtin_amdgcn_logf(u) * kLn2) * (x * __builtin_amdgcn_rcpf(u - 1.f));
+  return u == 1.f ? x : r;
 }
 
 // x - 2pi*floor(x/2pi), the reduction the reference applies to phases.
