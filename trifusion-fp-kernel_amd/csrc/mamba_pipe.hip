@@ -302,7 +302,13 @@ __device__ __forceinline__ uint32_t scaled_pair(uint32_t vw, float wvt) {
 template <int RPW, bool CTL16, bool TRAP16, bool ANG16, bool OUT32, bool SEEDED>
 __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
   __shared__ PipeSmem sh;
-  const int w = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  // Role index w of hardware wave hw. Unseeded, the prologue role (w 8-11)
+  // carries the start's longest chain (chunk c0's controls and phase, behind
+  // its loads), so it runs on the first waves dispatched (hw 0-3), which
+  // start ~1.7 k cycles before the last. Seeded, the segment scan on w 0-7 is
+  // the longer chain, and w = hw. Either way w % 4 == hw % 4 (same SIMD).
+  const int hw = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
+  const int w = SEEDED ? hw : (hw < 4 ? hw + 8 : hw - 4);
   const int lane = static_cast<int>(threadIdx.x & 63);
   const int c32 = lane & 31;
   const int hh = lane >> 5;
@@ -501,10 +507,15 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
     // every path), then the rows of the state and prologue waves, then a
     // seeded segment's summaries.
     PipeCtl ctl0 = {};
+    // controls are formed by prologue wave 3 (lane = row); the other prologue
+    // waves issue the same loads (so every wave of the role counts the same
+    // outstanding operations) at one row for all lanes: one cache line per
+    // load instead of 32
+    const int ctl_lane = p_idx == 3 ? lane : 0;
     float dts[RPW];
     if (w >= 8) {
-      ctl0 = load_pipe_ctl<CTL16, TRAP16>(P, dto, ado, trb, c0 * kChunk + lane, L, tlim);
-      ctl_next = load_pipe_ctl<CTL16, TRAP16>(P, dto, ado, trb, (c0 + 1) * kChunk + lane, L, tlim);
+      ctl0 = load_pipe_ctl<CTL16, TRAP16>(P, dto, ado, trb, c0 * kChunk + ctl_lane, L, tlim);
+      ctl_next = load_pipe_ctl<CTL16, TRAP16>(P, dto, ado, trb, (c0 + 1) * kChunk + ctl_lane, L, tlim);
       load_pipe_angles<RPW, ANG16>(P, th, gbase, pair, c0 * kChunk + sg * RPW, L);
       // chunk c0's steps for the phase, read here rather than from the
       // controls' LDS rows, so that the phase does not wait for a barrier
@@ -515,7 +526,7 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
     if (w >= 4) rows = load_rows(c0);
     // A seeded segment's entering state: the segment scan of the unit's
     // summaries of the segments before it, S <- S 2^dec_g + turn_g(summary_g)
-    // for g < seg, float4 f = threadIdx.x and threadIdx.x + 512 of the record
+    // for g < seg, float4 f = 64 w + lane and 64 w + lane + 512 of the record
     // layout on waves 0-7 (the prologue waves go straight to the chunk-0
     // controls and phase), left in the second chunk's qr/kr buffers (tiles
     // 0-1, 2-3) for the state waves. Summary g is formed in segment g's phase
@@ -526,7 +537,7 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
     [[maybe_unused]] float4* seed_lds[2] = {reinterpret_cast<float4*>(sh.qr[(c0 + 1) & 1]),
                                             reinterpret_cast<float4*>(sh.kr[(c0 + 1) & 1])};
     if (SEEDED && w < 8) {
-      const int f0 = static_cast<int>(threadIdx.x), f1 = f0 + 512;
+      const int f0 = 64 * w + lane, f1 = f0 + 512;
       const float4* sums = P.seg_state + static_cast<size_t>(unit) * P.G * 1024;
       const float* decs = P.seg_decay + unit * P.G;
       const uint2* phs = reinterpret_cast<const uint2*>(P.phase_fx + static_cast<size_t>(unit) * P.G * 32);
@@ -841,7 +852,7 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
           sh.score[cb][p_idx][1][lane] = sc[1];
         }
         if (p_idx == 3 && i + 1 < c1) controls(ctl_next, i + 1);
-        ctl_next = load_pipe_ctl<CTL16, TRAP16>(P, dto, ado, trb, (i + 2) * kChunk + lane, L, tlim);
+        ctl_next = load_pipe_ctl<CTL16, TRAP16>(P, dto, ado, trb, (i + 2) * kChunk + ctl_lane, L, tlim);
         lds_barrier();
 
         // ---------------- interval B(i) ----------------
@@ -976,7 +987,9 @@ __global__ __launch_bounds__(1024) void pipe_summary_kernel(const MfmaParams P) 
         th[i] = load_elem<ANG16>(P.angles, gbase + pj * P.g_sr + tc * P.g_st);
       }
     }
-    raw = load_pipe_ctl<CTL16, TRAP16>(P, dto, ado, trb, (cb0 + (w & 3)) * kChunk + lane, L, tlim);
+    // waves 4-15 do not form controls: one row for all lanes (one cache line
+    // per load instead of 32)
+    raw = load_pipe_ctl<CTL16, TRAP16>(P, dto, ado, trb, (cb0 + (w & 3)) * kChunk + (w < kBatch ? lane : 0), L, tlim);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int tc = min(t_lo + rsub + 128 * i, L - 1);
