@@ -111,6 +111,41 @@ def test_mamba_controls(dtype):
     torch.testing.assert_close(adt.cpu(), adt_ref, rtol=2e-6, atol=1e-7)
 
 
+def test_control_step_softplus_range():
+    """The step dt = softplus(ddt + bias), formed from the hardware exp2, log2
+    and reciprocal with Kahan's log1p identity, over ddt + bias in [-100, 25]
+    (plus points around e^v = 2^-24, where u = 1 + e^v rounds to 1, and
+    around the linear threshold 20): within 8 float32 ulp of float64
+    softplus where the result is a normal float, exactly v above 20; and the
+    decay adt = min(-(relu(a) + 1/(1 - min(a, 0))), -floor) * dt within 8 ulp
+    of its float64 value on the kernel's own dt."""
+    v = torch.cat([torch.linspace(-100.0, 25.0, 8001),
+                   torch.tensor([-17.5, -16.7, -16.6, -16.0, -1e-6, 0.0, 1e-6, 19.999, 20.0, 20.001])])
+    t = v.numel()
+    a = torch.linspace(-3.0, 3.0, t)
+    proj = torch.stack([v, a], dim=1).view(1, t, 2)  # columns ddt | a, head dim unit-strided
+    dproj = proj.to(DEV)
+    floor = 1e-4
+    adt, dt = mamba_controls(dproj[..., 1:2], dproj[..., 0:1], torch.zeros(1, device=DEV), floor)
+    dt = dt.cpu().view(-1).double()
+    adt = adt.cpu().view(-1).double()
+    vd = v.double()
+    ref = torch.where(vd > 20, vd, torch.log1p(torch.exp(vd)))
+    ulp = 2.0 ** -23
+    normal = ref > torch.finfo(torch.float32).tiny
+    rel = ((dt - ref).abs() / ref.clamp_min(1e-300))[normal]
+    print(f"softplus: max error {rel.max().item() / ulp:.2f} ulp over {int(normal.sum())} normal results", flush=True)
+    assert rel.max().item() <= 8 * ulp
+    assert (dt[~normal] - ref[~normal]).abs().max().item() <= torch.finfo(torch.float32).tiny
+    assert torch.equal(dt[vd > 20], vd[vd > 20])
+    ad = a.double()
+    adt_ref = torch.minimum(-(ad.clamp_min(0) + 1.0 / (1.0 - ad.clamp_max(0))), torch.tensor(-floor, dtype=torch.float64)) * dt
+    nz = adt_ref.abs() > torch.finfo(torch.float32).tiny
+    rel_a = ((adt - adt_ref).abs() / adt_ref.abs().clamp_min(1e-300))[nz]
+    print(f"decay: max error {rel_a.max().item() / ulp:.2f} ulp", flush=True)
+    assert rel_a.max().item() <= 8 * ulp
+
+
 MEAN_SHAPES = [
     # batch, time, d: the encoder pool (one split in fp32, two in bf16), a long
     # single clip (16 time splits), few frames (no split), d that is not a whole
