@@ -700,7 +700,6 @@ __global__ __launch_bounds__(256) void chunk_phase_kernel(const MfmaParams P) {
   if (r < P.R) {
     const int g0 = b * P.g_sb + h * P.g_sh + r * P.g_sr - roff * P.g_st;
     // unrolled so that several rows' loads are in flight before the first use
-#pragma unroll 4
     for (int t = t_begin + grp; t < t_end; t += ngrp) {
       const float th = P.angles_dtype == TF_FLOAT32 ? static_cast<const float*>(P.angles)[g0 + t * P.g_st]
                                                     : to_f32(static_cast<const bf16_t*>(P.angles)[g0 + t * P.g_st]);
