@@ -16,9 +16,11 @@
 //   skip, inter-chunk      A(c+1)     output waves             one 32x32 tile of y each
 //   scores . v, gate       B(c+1)     output waves             the same tile
 //
-// Waves 0-3 are output waves (time half th = w >> 1, head-dim tile pt = w & 1),
-// waves 4-7 state waves (s = w - 4: state tile nt = s >> 1, pt = s & 1) and
-// waves 8-11 prologue waves, so each SIMD holds one of each. The fp32 state S
+// By role index w: waves 0-3 are output waves (time half th = w >> 1, head-dim
+// tile pt = w & 1), waves 4-7 state waves (s = w - 4: state tile nt = s >> 1,
+// pt = s & 1) and waves 8-11 prologue waves, so each SIMD holds one of each
+// (the unseeded walk runs the prologue role on the first-dispatched hardware
+// waves; w and the hardware wave share their SIMD). The fp32 state S
 // (64 x 64) lives in the state waves' registers for the whole walk: each holds
 // one 32 x 32 tile in MFMA accumulator layout and applies S <- S 2^tot + dS
 // once per chunk; there is no scan and no state in LDS other than the bf16

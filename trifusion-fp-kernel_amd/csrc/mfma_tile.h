@@ -240,7 +240,8 @@ struct MfmaParams {
   float* seg_decay;
   int units, G, SC, NC;
   // Pipelined kernel's chunk-parallel form: per (unit, segment) and rotary
-  // pair the wrapping sum of its fixed-point phase increments ([G][32]).
+  // pair the wrapping sum of its fixed-point phase increments ([G][32]),
+  // written by the summary pass beside the segment's record.
   uint32_t* phase_fx;
   // Pipelined kernel, unsegmented varlen walks: deal batch rows longest first.
   int lpt;
