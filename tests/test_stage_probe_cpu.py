@@ -1,8 +1,9 @@
 """The stage-probe report (trifusion_amd/stage_probe.py) on synthetic
 timestamps: every stage a role records appears with its offset from the third
 iteration's start, stages a role does not have read -1, iteration lengths are
-B-barrier end minus A start, and workgroup durations are grouped by the
-kernel's XCD dealing (workgroup i runs unit (i % 8) * 32 + i / 8)."""
+B-barrier end minus A start, and workgroup durations are grouped by the unit
+and chunk count each workgroup recorded, with a least-squares fixed +
+per-chunk cost."""
 
 from trifusion_amd import build, stage_probe
 
@@ -23,11 +24,14 @@ def _synthetic():
     for j in range(3):  # 0 marks an event that was not recorded
         ts[0][24 + j] = 500 + 1000 * j
         ts[0][40 + j] = 500 + 1000 * j + 700 + j
-    blk = [0] * (4096 * 2)
+    blk = [0] * (4096 * 3)
     for i in range(256):
         unit = (i % 8) * 32 + i // 8
-        blk[2 * i] = 5
-        blk[2 * i + 1] = 5 + 1000 + (100 if unit % 16 == 3 else 0)  # head 3 slower by 1 us
+        chunks = 1 + unit % 7
+        blk[3 * i] = 5
+        # 2 us + 1 us per chunk, head 3 slower by 1 us (100 MHz ticks)
+        blk[3 * i + 1] = 5 + 200 + 100 * chunks + (100 if unit % 16 == 3 else 0)
+        blk[3 * i + 2] = unit * 256 + chunks
     return ts, blk
 
 
@@ -43,8 +47,13 @@ def test_report_tables():
     assert [int(v) for v in before_ctl] == [-1] * 11 + [300 - 1000]
     iters = [line for line in lines if line.strip().startswith("iteration ")]
     assert [int(line.split()[-1]) for line in iters] == [700, 701, 702]
-    by_head = next(line for line in lines if "median by head" in line).split(":")[1].split()
-    assert [int(v) for v in by_head] == [10000] * 3 + [11000] + [10000] * 12
+    by_chunks = next(line for line in lines if "by chunk count" in line)
+    assert "7: " in by_chunks and "1: " in by_chunks
+    fit = next(line for line in lines if "fit over walked units" in line)
+    rhs = fit.split("=")[1]  # " <fixed> ns + <per chunk> ns per chunk"
+    fixed = float(rhs.split("ns")[0])
+    per_chunk = float(rhs.split("+")[1].split("ns")[0])
+    assert abs(per_chunk - 1000) < 30 and abs(fixed - 2000) < 150
 
 
 def test_probe_library_is_separate():

@@ -47,12 +47,13 @@ namespace tf {
 // workgroup 0 stores them once at the end, so the walk issues no extra memory
 // operation (the compiler may not move code across a marker, so the probe
 // library's schedule can differ slightly); every workgroup also stores its
-// start and end s_memrealtime (100 MHz). Events: 20 kernel start, 16 start loads issued, 17 before the
+// start and end s_memrealtime (100 MHz) and its unit and chunk count
+// (unit * 256 + chunks). Events: 20 kernel start, 16 start loads issued, 17 before the
 // chunk-0 controls, 14/15 before/after the start barrier, 24 + j / 40 + j
 // interval A start / interval B barrier end of iteration j (output waves),
 // 0-13 the stages of iteration 2 (per role), 21 walk end.
 __device__ long long g_stage_ts[12 * 64];
-__device__ long long g_stage_blk[4096 * 2];
+__device__ long long g_stage_blk[4096 * 3];
 #define TF_STAGE(k)                                                  \
   do {                                                               \
     __builtin_amdgcn_sched_barrier(0);                               \
@@ -938,8 +939,9 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
     g_stage_ts[w * 64 + lane] =
         (static_cast<long long>(static_cast<unsigned>(stage_hi)) << 32) | static_cast<unsigned>(stage_lo);
   if (threadIdx.x == 0 && blockIdx.x < 4096) {
-    g_stage_blk[2 * blockIdx.x] = stage_blk_t0;
-    g_stage_blk[2 * blockIdx.x + 1] = __builtin_amdgcn_s_memrealtime();
+    g_stage_blk[3 * blockIdx.x] = stage_blk_t0;
+    g_stage_blk[3 * blockIdx.x + 1] = __builtin_amdgcn_s_memrealtime();
+    g_stage_blk[3 * blockIdx.x + 2] = static_cast<long long>(unit) * 256 + (c1 - c0);
   }
 #endif
   {
@@ -1338,11 +1340,12 @@ int launch_pipe(const tf_mamba_args& a, hipStream_t stream) {
 
 #ifdef TF_STAGE_PROBE
 // Stage timestamps of the last walk (workgroup 0, [12 waves][64 events],
-// s_memtime) and every workgroup's start/end ([4096][2], s_memrealtime) of
-// the library built with -DTF_STAGE_PROBE. Not part of the product interface.
+// s_memtime) and every workgroup's start, end (s_memrealtime) and unit *
+// 256 + chunk count ([4096][3]) of the library built with -DTF_STAGE_PROBE.
+// Not part of the product interface.
 extern "C" int tf_stage_probe_read(long long* ts, long long* blocks) {
   if (!ts || !blocks) return TF_ERR_NULL;
   if (hipMemcpyFromSymbol(ts, HIP_SYMBOL(tf::g_stage_ts), sizeof(long long) * 12 * 64) != hipSuccess) return 1;
-  return hipMemcpyFromSymbol(blocks, HIP_SYMBOL(tf::g_stage_blk), sizeof(long long) * 4096 * 2) == hipSuccess ? 0 : 1;
+  return hipMemcpyFromSymbol(blocks, HIP_SYMBOL(tf::g_stage_blk), sizeof(long long) * 4096 * 3) == hipSuccess ? 0 : 1;
 }
 #endif
