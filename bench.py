@@ -5,8 +5,9 @@ N=64 (R=16, Hq=1; bf16 x/B/C/z, fp32 dt/adt/trap/angles), synthetic seeded
 inputs resident in HBM. A step is one call over the batch; the timed region
 replays a HIP graph holding ``--steps`` back-to-back calls so host dispatch does
 not stall the GPU between calls, bracketed by device synchronisation and timed
-with HIP events on the launch stream, after ``--warmup`` eager calls and five
-untimed replays of the same graph. The calls cycle through copies of the
+with HIP events on the launch stream, after ``--warmup`` eager calls and
+untimed replays of the same graph that add up to at least 50 ms of GPU time
+(so the GPU's clocks have settled whatever ``--steps`` is). The calls cycle through copies of the
 inputs (each with its own output) whose total exceeds twice the 256 MB
 last-level cache, so every call reads its operands from HBM; the single-set,
 cache-warm time is reported beside it.
@@ -155,10 +156,27 @@ def utilisation_counters():
     return out
 
 
-# Untimed replays of a captured graph before its timed replay. One replay of
-# the clip's 200 calls (~5 ms) leaves the GPU's clocks still rising: the timed
-# replay then reads ~2 us per call slower than after five.
-WARM_REPLAYS = 5
+# Untimed GPU work before a graph's timed replay: the captured graph is
+# replayed until at least this many milliseconds of it have run, whatever
+# --steps is. After ~5 ms the GPU's clocks are still rising (the timed replay
+# read ~2 us per call slower than after ~25 ms of replays).
+WARM_GPU_MS = 50.0
+
+
+def warm_graph(torch, graph, stream, min_ms=WARM_GPU_MS):
+    """Replay ``graph`` (untimed) until ``min_ms`` of its GPU time has run."""
+    spent = 0.0
+    replays = 0
+    while spent < min_ms or replays < 2:
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        graph.replay()
+        b.record(stream)
+        b.synchronize()
+        spent += a.elapsed_time(b)
+        replays += 1
+    return replays
 
 
 def time_fused_mamba(args, torch, fused_mamba, sets, steps, warmup, variant, eager, lengths=None):
@@ -192,8 +210,7 @@ def time_fused_mamba(args, torch, fused_mamba, sets, steps, warmup, variant, eag
                 for i in range(steps):
                     call(i)
         stream.wait_stream(side)
-        for _ in range(WARM_REPLAYS):
-            graph.replay()
+        warm_graph(torch, graph, stream)
         torch.cuda.synchronize()
         start.record(stream)
         graph.replay()
@@ -273,8 +290,7 @@ def graph_us(torch, fn, steps=100):
                 for i in range(steps):
                     fn(i)
         stream.wait_stream(side)
-        for _ in range(WARM_REPLAYS):
-            graph.replay()
+        warm_graph(torch, graph, stream)
         torch.cuda.synchronize()
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)

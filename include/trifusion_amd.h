@@ -132,7 +132,10 @@ int tf_fused_mamba_variant(const tf_mamba_args *args);
  * tf_fused_mamba_static_scratch_bytes() (16 MiB) that every device holds until
  * the process ends. Arguments whose tf_fused_mamba_workspace_size exceeds it
  * return TF_ERR_WORKSPACE and launch nothing. Calls allocate nothing; the
- * first call on a device looks up that device's copy of the array. Every call
+ * first call on a device that needs scratch looks up that device's copy of the
+ * array (hipGetSymbolAddress, which may load the library's code object): make
+ * that first call outside graph capture. A failed lookup returns TF_ERR_LAUNCH
+ * and is tried again on the next call. Every call
  * on one device shares that device's array, and the kernels rewrite all of the
  * scratch they read within the call (nothing needs to start at zero), so calls
  * that overlap on one device (different streams, no ordering) race: serialise

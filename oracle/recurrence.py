@@ -251,18 +251,28 @@ def fused_mamba_f64(q, k, v, adt, dt, trap, qb, kb, angles, d, z):
     return torch.stack(outputs, 1)
 
 
-def fused_mamba_attention_f64(q, k, v, adt, dt, trap, qb, kb, angles, d, z):
+def fused_mamba_attention_f64(q, k, v, adt, dt, trap, qb, kb, angles, d, z, clamp_chunk=None):
     """Quadratic (attention-form) FP64 closed form of the same recurrence.
 
     ``y = silu(z) * (sum_{u<t} exp(A_t - A_u) (qr_t . kr_u) s_u v_u + (D + delta_t) v_t)``
     with ``A = cumsum(adt)``. Unrolls the state recursion of
     ``tests/test_recurrence.py:64-84`` into an explicit lower-triangular kernel.
+
+    ``clamp_chunk=C`` caps the weight at 1 for u and t in the same C-step
+    chunk, ``exp(min(A_t - A_u, 0))``: the reference's intra-chunk score decay
+    (``mamba_fused.py:144``). Pairs in different chunks meet through the carried
+    state, which has no clamp (``:143, 150-152``). With ``adt <= 0`` the clamp
+    changes nothing.
     """
     bsz, t, h, p = v.shape
     qt, kt, qr, kr = _rotated_f64(q, k, qb, kb, angles, dt, h)
     gamma, scale = step_controls(dt.double(), trap.double())
     a = adt.double().cumsum(-1)
     diff = a[..., :, None] - a[..., None, :]
+    if clamp_chunk is not None:
+        chunk_of = torch.arange(t) // clamp_chunk
+        same = chunk_of[:, None] == chunk_of[None, :]
+        diff = torch.where(same, diff.clamp_max(0.0), diff)
     strict = torch.ones(t, t, dtype=torch.bool).tril(-1)
     decay = diff.masked_fill(~strict, -torch.inf).exp()
     qr = qr.permute(0, 2, 1, 3)

@@ -116,11 +116,13 @@ def test_control_step_softplus_range():
     and reciprocal with Kahan's log1p identity, over ddt + bias in [-100, 25]
     (plus points around e^v = 2^-24, where u = 1 + e^v rounds to 1, and
     around the linear threshold 20): within 8 float32 ulp of float64
-    softplus where the result is a normal float, exactly v above 20; and the
+    softplus where the result is a normal float, exactly v above 20, and 0
+    (not NaN) from -104 down to -inf, where e^v is below the least subnormal; and the
     decay adt = min(-(relu(a) + 1/(1 - min(a, 0))), -floor) * dt within 8 ulp
     of its float64 value on the kernel's own dt."""
     v = torch.cat([torch.linspace(-100.0, 25.0, 8001),
-                   torch.tensor([-17.5, -16.7, -16.6, -16.0, -1e-6, 0.0, 1e-6, 19.999, 20.0, 20.001])])
+                   torch.tensor([-17.5, -16.7, -16.6, -16.0, -1e-6, 0.0, 1e-6, 19.999, 20.0, 20.001]),
+                   torch.tensor([-103.9, -104.0, -104.1, -150.0, -1e30, -float("inf")])])
     t = v.numel()
     a = torch.linspace(-3.0, 3.0, t)
     proj = torch.stack([v, a], dim=1).view(1, t, 2)  # columns ddt | a, head dim unit-strided
@@ -138,6 +140,8 @@ def test_control_step_softplus_range():
     assert rel.max().item() <= 8 * ulp
     assert (dt[~normal] - ref[~normal]).abs().max().item() <= torch.finfo(torch.float32).tiny
     assert torch.equal(dt[vd > 20], vd[vd > 20])
+    assert torch.isfinite(dt).all()
+    assert torch.equal(dt[vd <= -104], torch.zeros_like(dt[vd <= -104]))
     ad = a.double()
     adt_ref = torch.minimum(-(ad.clamp_min(0) + 1.0 / (1.0 - ad.clamp_max(0))), torch.tensor(-floor, dtype=torch.float64)) * dt
     nz = adt_ref.abs() > torch.finfo(torch.float32).tiny

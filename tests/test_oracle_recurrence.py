@@ -46,6 +46,28 @@ def test_chunked_fp32_matches_f64_loop_clip_distributions(b, t, h, p, n, r, hq):
     assert R.max_rel(out, ref) < 2e-5
 
 
+@pytest.mark.parametrize("t", [50, 150])
+def test_chunked_clamps_positive_decay_within_chunks(t):
+    """Steps with adt > 0: the chunked form equals the FP64 attention form whose
+    weights are capped at 1 inside a 64-step chunk and uncapped across chunks
+    (mamba_fused.py:143-152). The unclamped closed form (the true recurrence)
+    is far away on the same inputs, so a form without the clamp fails here."""
+    args = list(clip_inputs(2, t, heads=4, head_dim=32, state=32, rotary=8, dtype=torch.float32, seed=9))
+    g = torch.Generator().manual_seed(19)
+    flip = torch.rand(args[3].shape, generator=g) < 0.3
+    args[3] = torch.where(flip, -0.5 * args[3], args[3])
+    assert (args[3] > 0).sum() > 10
+    out = R.fused_mamba_chunked(*args)
+    clamped = R.fused_mamba_attention_f64(*args, clamp_chunk=R.CHUNK)
+    assert R.max_rel(out, clamped) < 2e-5
+    unclamped = R.fused_mamba_attention_f64(*args)
+    assert R.max_rel(unclamped, clamped) > 1e-2
+    # with adt <= 0 the clamp is the identity
+    neg = list(args)
+    neg[3] = -args[3].abs()
+    assert R.max_rel(R.fused_mamba_attention_f64(*neg, clamp_chunk=R.CHUNK), R.fused_mamba_attention_f64(*neg)) < 1e-12
+
+
 @pytest.mark.parametrize("b,t,h,n,r,hq", [(1, 17, 4, 128, 32, 1), (2, 40, 4, 16, 4, 2), (1, 90, 3, 64, 16, 3)])
 def test_f64_loop_matches_attention_form(b, t, h, n, r, hq):
     args = clip_inputs(b, t, heads=h, head_dim=32, state=n, rotary=r, qk_heads=hq, dtype=torch.float64, seed=5)

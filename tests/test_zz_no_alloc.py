@@ -5,7 +5,8 @@ Two calls in a row on the library's static scratch, the second smaller, each
 compared bit for bit with tf_fused_mamba on a torch-allocated workspace (both
 run the same kernels with the same segment plan). Also a shape that needs no
 scratch, and one whose scratch exceeds the static array, which must be
-rejected with TF_ERR_WORKSPACE before anything is launched.
+rejected with TF_ERR_WORKSPACE before anything is launched; and the entry
+captured into a HIP graph, whose replays must equal the eager result.
 """
 
 import ctypes
@@ -62,6 +63,41 @@ def test_static_scratch_matches_workspace_entry():
         assert rc_ref == 0 and rc == 0
         assert torch.isfinite(got).all()
         assert torch.equal(got, ref), f"{name}: max diff {(got - ref).abs().max().item():.3e}"
+
+
+def test_static_entry_under_graph_capture():
+    """tf_fused_mamba_static captured into a HIP graph (the callers it is for):
+    after one eager call on the device (which looks up the scratch address),
+    the capture launches the chunk-parallel kernels on the static scratch, and
+    every replay, with eager work on the same buffers between replays, equals
+    the eager tf_fused_mamba result bit for bit."""
+    lib = _lib.load()
+    args = clip_inputs(1, 7200, seed=24)
+    dargs = tuple(a.to(DEV) for a in args)
+    print("case graph long_b1_l7200_h16", flush=True)
+    rc_ref, ref = call("tf_fused_mamba", dargs)
+    rc, first = call("tf_fused_mamba_static", dargs)
+    assert rc_ref == 0 and rc == 0 and torch.equal(first, ref)
+    out = torch.full(dargs[2].shape, float("nan"), device=DEV, dtype=torch.float32)
+    cargs = build_args(*dargs, out, None, "auto", False, None, 1e-4)
+    codes = []
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            codes.append(lib.tf_fused_mamba_static(ctypes.byref(cargs), _lib.stream_of(out)))
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    assert codes == [0]
+    for replay in range(3):
+        out.fill_(float("nan"))
+        # eager work between replays on the same device and buffers
+        _, again = call("tf_fused_mamba_static", dargs)
+        assert torch.equal(again, ref)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"replay {replay}: max diff {(out - ref).abs().max().item():.3e}"
 
 
 @pytest.mark.parametrize("variant,t,h", [("mfma", 16384, 128)])

@@ -82,6 +82,8 @@ __device__ __forceinline__ float control_decay(float a, float step, float floor_
 //   u == 1 (W. Kahan's identity: D. Goldberg, "What every computer scientist
 //   should know about floating-point arithmetic", ACM Computing Surveys 23(1),
 //   1991, Theorem 4).
+// Below -104, e^v is under half the least fp32 subnormal, so the result is 0
+// (also at v = -inf, where the split of v log2(e) would form -inf + inf).
 __device__ __forceinline__ float softplus_le20(float v) {
   constexpr float kL1 = 1.4426950216293335f;     // log2(e) rounded to float
   constexpr float kL2 = 1.925963033500011e-08f;  // log2(e) - kL1
@@ -92,7 +94,7 @@ __device__ __forceinline__ float softplus_le20(float v) {
   const float x = __builtin_fmaf(e0, l * kLn2, e0);
   const float u = 1.f + x;
   const float r = (__builtin_amdgcn_logf(u) * kLn2) * (x * __builtin_amdgcn_rcpf(u - 1.f));
-  return u == 1.f ? x : r;
+  return v < -104.f ? 0.f : (u == 1.f ? x : r);
 }
 
 // x - 2pi*floor(x/2pi), the reduction the reference applies to phases.

@@ -19,23 +19,24 @@ constexpr int64_t kStaticScratchBytes = int64_t(16) << 20;
 __device__ __align__(256) char scratch[kStaticScratchBytes];
 
 constexpr int kMaxDevices = 64;
-std::once_flag g_scratch_once[kMaxDevices];
+std::mutex g_scratch_mutex;
 void* g_scratch_ptr[kMaxDevices] = {};
 
-// Device address of `scratch` on `device`, looked up once per device with that
-// device current (the previous current device is restored). NULL on failure.
+// Device address of `scratch` on `device`, looked up with that device current
+// (the previous current device is restored). A successful lookup is kept; a
+// failed one returns NULL and is tried again on the next call.
 void* static_scratch(int device) {
   if (device < 0 || device >= kMaxDevices) return nullptr;
-  std::call_once(g_scratch_once[device], [device] {
-    int prev = -1;
-    hipError_t rc = hipGetDevice(&prev);
-    if (rc == hipSuccess && prev != device) rc = hipSetDevice(device);
-    void* ptr = nullptr;
-    if (rc == hipSuccess) rc = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
-    if (prev >= 0 && prev != device) (void)hipSetDevice(prev);
-    g_scratch_ptr[device] = rc == hipSuccess ? ptr : nullptr;
-  });
-  return g_scratch_ptr[device];
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[device] != nullptr) return g_scratch_ptr[device];
+  int prev = -1;
+  hipError_t rc = hipGetDevice(&prev);
+  if (rc == hipSuccess && prev != device) rc = hipSetDevice(device);
+  void* ptr = nullptr;
+  if (rc == hipSuccess) rc = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+  if (prev >= 0 && prev != device) (void)hipSetDevice(prev);
+  if (rc == hipSuccess) g_scratch_ptr[device] = ptr;
+  return rc == hipSuccess ? ptr : nullptr;
 }
 
 bool empty(const tf_mamba_args* a) { return a->batch == 0 || a->time == 0; }

@@ -287,9 +287,10 @@ __device__ __forceinline__ float ctl_value(const void* base, int bf16, int i) {
 }
 
 // Scores^T[u][t] = kr_u . qr_t of one 32x32 tile times the decay
-// 2^(cs_t - cs_u), strictly causal on a diagonal tile (an off-diagonal tile
-// must have every t > u), rounded to bf16 as the Y operand of the score . v
-// product (rows t, K = u; mamba_fused.py:144-146).
+// 2^min(cs_t - cs_u, 0), strictly causal on a diagonal tile (an off-diagonal
+// tile must have every t > u), rounded to bf16 as the Y operand of the
+// score . v product (rows t, K = u; mamba_fused.py:144-146). The clamp caps a
+// weight at 1 where the signed decay is positive somewhere between u and t.
 __device__ __forceinline__ void score_tile(const f32x16& acc, float cst, const float* csu_base, bool diag, int c32,
                                            int hh, u32x4 (&out)[2]) {
 #pragma unroll
@@ -301,7 +302,7 @@ __device__ __forceinline__ void score_tile(const f32x16& acc, float cst, const f
     for (int q = 0; q < 4; ++q) {
       const int e = 4 * g + q;
       // masked elements (t <= u) may overflow here; the select below drops them
-      const float x = acc[e] * fast_exp2(cst - cu[q]);
+      const float x = acc[e] * fast_exp2(fminf(cst - cu[q], 0.f));
       vals[q] = (!diag || c32 > drow(e, hh)) ? x : 0.f;
     }
     out[g >> 1][2 * (g & 1)] = pack2(vals[0], vals[1]);

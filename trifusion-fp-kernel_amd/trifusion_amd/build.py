@@ -5,12 +5,6 @@ every ``csrc/*.hip`` file becomes an object under ``_build/`` and the objects
 are linked into ``trifusion_amd/libtrifusion_amd.so``, which ``_lib.py`` loads
 with ctypes. The library exports only the ``extern "C"`` entry points declared
 in ``include/trifusion_amd.h``.
-
-``build_library(stage_probe=True)`` (``python -m trifusion_amd.build
---stage-probe``) builds a second library, ``libtrifusion_amd_stage_probe.so``,
-with ``-DTF_STAGE_PROBE``: the pipelined recurrence kernel then records stage
-timestamps for ``python -m trifusion_amd.stage_probe``. It is a measurement
-aid and never loaded by the package.
 """
 
 import os
@@ -26,7 +20,6 @@ CSRC_DIR = PROJECT_DIR / "csrc"
 INCLUDE_DIR = REPO_DIR / "include"
 BUILD_DIR = PROJECT_DIR / "_build"
 LIB_PATH = PACKAGE_DIR / "libtrifusion_amd.so"
-STAGE_PROBE_LIB_PATH = PACKAGE_DIR / "libtrifusion_amd_stage_probe.so"
 ARCH = "gfx950"
 
 # Packed-fp32 VALU forms are disabled for all device code; hipcc -O3 would
@@ -47,8 +40,8 @@ def sources():
     return sorted(CSRC_DIR.glob("*.hip"))
 
 
-def _compile(hipcc, src, obj, defines=()):
-    cmd = [hipcc, *COMMON_FLAGS, *DEVICE_FLAGS, *defines, "-I", str(INCLUDE_DIR), "-I", str(CSRC_DIR), "-c", str(src),
+def _compile(hipcc, src, obj):
+    cmd = [hipcc, *COMMON_FLAGS, *DEVICE_FLAGS, "-I", str(INCLUDE_DIR), "-I", str(CSRC_DIR), "-c", str(src),
            "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     lines = [
@@ -61,33 +54,27 @@ def _compile(hipcc, src, obj, defines=()):
     return lines
 
 
-def build_library(verbose=False, jobs=None, stage_probe=False):
-    """Compile every ``csrc/*.hip`` for gfx950 and link the shared library
-    (the stage-probe library with ``stage_probe``)."""
+def build_library(verbose=False, jobs=None):
+    """Compile every ``csrc/*.hip`` for gfx950 and link the shared library."""
     hipcc = hipcc_path()
-    build_dir = BUILD_DIR / "stage_probe" if stage_probe else BUILD_DIR
-    lib_path = STAGE_PROBE_LIB_PATH if stage_probe else LIB_PATH
-    defines = ("-DTF_STAGE_PROBE",) if stage_probe else ()
-    build_dir.mkdir(parents=True, exist_ok=True)
+    BUILD_DIR.mkdir(parents=True, exist_ok=True)
     srcs = sources()
-    objs = [build_dir / (s.stem + ".o") for s in srcs]
+    objs = [BUILD_DIR / (s.stem + ".o") for s in srcs]
     jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 2)))
     with ThreadPoolExecutor(max_workers=jobs) as pool:
-        logs = list(pool.map(lambda so: _compile(hipcc, *so, defines), zip(srcs, objs)))
+        logs = list(pool.map(lambda so: _compile(hipcc, *so), zip(srcs, objs)))
     if verbose:
         for src, lines in zip(srcs, logs):
             for line in lines:
                 print(f"[{src.name}] {line}")
-    tmp = lib_path.with_suffix(".so.tmp")
+    tmp = LIB_PATH.with_suffix(".so.tmp")
     cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError("link failed:\n" + proc.stdout + proc.stderr)
-    os.replace(tmp, lib_path)
-    return lib_path
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
 
 
 if __name__ == "__main__":
-    import sys
-
-    print(build_library(verbose=True, stage_probe="--stage-probe" in sys.argv[1:]))
+    print(build_library(verbose=True))

@@ -71,11 +71,18 @@ def save_student(model, path):
     torch.save({"model_config": config, "model": model.state_dict()}, path)
 
 
+# Layers whose weights feed a GEMM (or an implicit-GEMM convolution).
+_MATMUL_LAYERS = (torch.nn.Linear, torch.nn.Conv1d, torch.nn.Conv2d)
+
+
 def prepare_static_weights(model):
-    """Cast frozen GEMM/conv parameters once; normalization and controls stay fp32."""
-    for module in model.modules():
-        if isinstance(module, (torch.nn.Linear, torch.nn.Conv1d, torch.nn.Conv2d)):
-            module.to(dtype=torch.bfloat16)
+    """Store the weights of every matrix-product layer (linear, 1-d and 2-d
+    convolution) in bf16 once, the dtype the autocast forward feeds its GEMMs,
+    instead of casting them on every call. Norm weights and the recurrence's
+    control parameters are not matrix-product layers and keep fp32."""
+    for layer in model.modules():
+        if isinstance(layer, _MATMUL_LAYERS):
+            layer.to(dtype=torch.bfloat16)
 
 
 def device_arch(index=0):
@@ -83,17 +90,58 @@ def device_arch(index=0):
 
 
 def configure_runtime(threads=2, enforce_gfx950=True):
+    """Process settings for inference: a ROCm GPU is required (a gfx950 one
+    unless ``enforce_gfx950`` is False), ``threads`` host threads, fp32 GEMMs
+    and convolutions without TF32, and no convolution autotuning (the same
+    algorithms run in every call, so a captured graph matches the eager
+    forward)."""
     if not torch.cuda.is_available():
         raise RuntimeError("A ROCm GPU is required")
-    if enforce_gfx950 and device_arch() != "gfx950":
-        raise RuntimeError("This runtime is built for MI355X (gfx950)")
+    arch = device_arch()
+    if enforce_gfx950 and arch != "gfx950":
+        raise RuntimeError(f"This runtime is built for MI355X (gfx950), not {arch}")
     torch.set_num_threads(threads)
-    torch.backends.cuda.matmul.allow_tf32 = False
-    torch.backends.cudnn.allow_tf32 = False
-    torch.backends.cudnn.benchmark = False
+    flags = torch.backends
+    flags.cuda.matmul.allow_tf32 = False
+    flags.cudnn.allow_tf32 = False
+    flags.cudnn.benchmark = False
+
+
+def _release_cached_memory():
+    gc.collect()
+    torch.cuda.empty_cache()
+
+
+class _Replay:
+    """A captured forward: its graph, the static input tensors the graph reads
+    and the logits buffer it writes."""
+
+    __slots__ = ("graph", "static_inputs", "logits")
+
+    def __init__(self, graph, static_inputs, logits):
+        self.graph = graph
+        self.static_inputs = static_inputs
+        self.logits = logits
+
+    def run(self, *inputs):
+        for dst, src in zip(self.static_inputs, inputs):
+            dst.copy_(src)
+        self.graph.replay()
+        # the caller owns its result: the next replay rewrites the buffer
+        return self.logits.clone()
 
 
 class InferenceEngine:
+    """Runs a frozen model's forward, replaying captured graphs when ``graphs``.
+
+    Graphs are cached per (audio shape, audio dtype), at most ``max_graphs`` of
+    them, the least recently used one dropped first. A shape whose capture
+    runs out of memory, or after whose capture torch's reserved pool exceeds
+    ``max_reserved_gib``, is marked in ``disabled_shapes`` and runs eagerly from
+    then on. ``graph_hits`` counts replays and ``graph_build_seconds`` the time
+    spent building graphs. Calls are not thread-safe: serialise them.
+    """
+
     def __init__(self, model, graphs=False, max_graphs=2, max_reserved_gib=19.5):
         self.model = model
         self.graphs = graphs
@@ -106,62 +154,69 @@ class InferenceEngine:
 
     @torch.inference_mode()
     def eager(self, audio, lengths, channels):
+        """One forward without a graph under bf16 autocast; the logits."""
         with torch.autocast("cuda", dtype=torch.bfloat16):
-            return self.model(audio, lengths, channels)["logits"]
+            result = self.model(audio, lengths, channels)
+        return result["logits"]
 
     def clear(self):
+        """Drop every cached graph and return the memory to the device."""
         self.cache.clear()
-        gc.collect()
-        torch.cuda.empty_cache()
+        _release_cached_memory()
 
-    def _capture(self, x, lengths, channels):
-        """Warm up on a side stream, then record one forward into a graph."""
-        stream = torch.cuda.Stream()
-        stream.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(stream):
-            for _ in range(2):
-                self.eager(x, lengths, channels)
-        torch.cuda.current_stream().wait_stream(stream)
+    def _capture(self, audio, lengths, channels):
+        """Record one forward reading ``audio``/``lengths``/``channels`` into a
+        graph. Two eager forwards on a side stream come first, so kernels are
+        loaded and library handles and workspaces exist before capture."""
+        caller = torch.cuda.current_stream()
+        side = torch.cuda.Stream()
+        side.wait_stream(caller)
+        with torch.cuda.stream(side):
+            self.eager(audio, lengths, channels)
+            self.eager(audio, lengths, channels)
+        caller.wait_stream(side)
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            out = self.eager(x, lengths, channels)
-        return graph, out
+            logits = self.eager(audio, lengths, channels)
+        return graph, logits
+
+    def _disable(self, shape_key):
+        self.disabled_shapes.add(shape_key)
+        self.clear()
+
+    def _build(self, shape_key, inputs):
+        """Capture a graph for ``shape_key`` on copies of ``inputs``; None when
+        the shape has to run eagerly instead."""
+        while len(self.cache) >= self.max_graphs:
+            self.cache.popitem(last=False)
+        _release_cached_memory()
+        began = time.perf_counter()
+        static_inputs = tuple(t.clone() for t in inputs)
+        try:
+            graph, logits = self._capture(*static_inputs)
+        except torch.cuda.OutOfMemoryError:
+            static_inputs = None
+            self._disable(shape_key)
+            return None
+        self.graph_build_seconds += time.perf_counter() - began
+        if torch.cuda.memory_reserved() > self.limit:
+            graph = logits = static_inputs = None
+            self._disable(shape_key)
+            return None
+        replay = _Replay(graph, static_inputs, logits)
+        self.cache[shape_key] = replay
+        return replay
 
     @torch.inference_mode()
     def __call__(self, audio, lengths, channels):
-        key = (tuple(audio.shape), audio.dtype)
-        if not self.graphs or key in self.disabled_shapes:
-            return self.eager(audio, lengths, channels)
-        if key not in self.cache:
-            while len(self.cache) >= self.max_graphs:
-                self.cache.popitem(last=False)
-            gc.collect()
-            torch.cuda.empty_cache()
-            start = time.perf_counter()
-            x = audio.clone()
-            l = lengths.clone()
-            c = channels.clone()
-            try:
-                graph, out = self._capture(x, l, c)
-            except torch.cuda.OutOfMemoryError:
-                del x, l, c
-                self.clear()
-                self.disabled_shapes.add(key)
-                return self.eager(audio, lengths, channels)
-            self.graph_build_seconds += time.perf_counter() - start
-            if torch.cuda.memory_reserved() > self.limit:
-                del graph, out, x, l, c
-                self.clear()
-                self.disabled_shapes.add(key)
-                return self.eager(audio, lengths, channels)
-            self.cache[key] = (graph, x, l, c, out)
-        graph, x, l, c, out = self.cache[key]
-        self.cache.move_to_end(key)
-        x.copy_(audio)
-        l.copy_(lengths)
-        c.copy_(channels)
-        graph.replay()
-        self.graph_hits += 1
-        # a later replay overwrites the graph's output buffer
-        return out.clone()
+        shape_key = (tuple(audio.shape), audio.dtype)
+        if self.graphs and shape_key not in self.disabled_shapes:
+            replay = self.cache.get(shape_key)
+            if replay is None:
+                replay = self._build(shape_key, (audio, lengths, channels))
+            if replay is not None:
+                self.cache.move_to_end(shape_key)
+                self.graph_hits += 1
+                return replay.run(audio, lengths, channels)
+        return self.eager(audio, lengths, channels)
