@@ -83,6 +83,15 @@ typedef enum tf_mamba_variant {
  *                 reference's reverse_valid(fused_mamba(reverse_valid(...)))
  *                 of the backward direction (src/trifusion_l4/model.py:174-179,
  *                 kernels/__init__.py:44-55) with no reversed copies.
+ *   q_norm, k_norm [N] fp32, contiguous, or both NULL (extension). Non-NULL:
+ *                 q and k are the raw C and B columns of the in-projection, and
+ *                 the block's C/B RMSNorm (src/trifusion_l4/mamba.py:56-57,
+ *                 kernels/__init__.py:10-12) is applied to each row as it is
+ *                 loaded, rounded to the operand dtype as the separate norm's
+ *                 output is:
+ *                   x <- round(x * rsqrt(mean_n(x^2) + norm_eps) * w)
+ *                 so no normalised [B, T, Hq, N] copies are written or read.
+ *   norm_eps      epsilon of those norms (the reference uses 1e-5).
  * Stride arrays follow the dimension order above.
  */
 typedef struct tf_mamba_args {
@@ -102,6 +111,8 @@ typedef struct tf_mamba_args {
   const float *dt_bias;
   float a_floor;
   int32_t reverse;
+  const float *q_norm, *k_norm;
+  float norm_eps;
 } tf_mamba_args;
 
 /*

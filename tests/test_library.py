@@ -38,8 +38,9 @@ def test_struct_layout_matches_header():
     from trifusion_amd._lib import MambaArgs
 
     # 13 pointers, 10 int32, 33 int64 strides, 7 int64 dims, workspace pointer + bytes,
-    # dt_bias pointer, a_floor float, reverse int32
-    assert ctypes.sizeof(MambaArgs) == 13 * 8 + 10 * 4 + 33 * 8 + 7 * 8 + 8 + 8 + 8 + 4 + 4
+    # dt_bias pointer, a_floor float, reverse int32, two norm-weight pointers,
+    # norm_eps float and the tail padding to 8 bytes
+    assert ctypes.sizeof(MambaArgs) == 13 * 8 + 10 * 4 + 33 * 8 + 7 * 8 + 8 + 8 + 8 + 4 + 4 + 8 + 8 + 4 + 4
     text = HEADER.read_text()
     body = text[text.index("typedef struct tf_mamba_args") : text.index("} tf_mamba_args;")]
     names_in_header = re.findall(r"\*?(\w+)(?:\[\d\])?[,;]", body)
@@ -97,6 +98,22 @@ def test_workspace_size_query():
     bad = _host_args(1, 100, 16)
     bad.heads = 0
     assert size(bad) < 0
+
+
+def test_fused_norm_weights_come_as_a_pair():
+    """The B/C norm weights are both given or both NULL; one alone is
+    TF_ERR_NULL from the host checks, before any kernel is chosen."""
+    from trifusion_amd import _lib
+
+    lib = _lib.load()
+    a = _host_args(16, 400, 16)
+    assert lib.tf_fused_mamba_variant(ctypes.byref(a)) == 3
+    a.q_norm, a.norm_eps = 1 << 20, 1e-5
+    assert lib.tf_fused_mamba_variant(ctypes.byref(a)) == -1
+    a.k_norm = 1 << 20
+    assert lib.tf_fused_mamba_variant(ctypes.byref(a)) == 3
+    a.q_norm = None
+    assert lib.tf_fused_mamba_variant(ctypes.byref(a)) == -1
 
 
 def test_version_string():

@@ -54,6 +54,8 @@ int validate(const tf_mamba_args* a) {
   if (a->batch > 65535 || a->heads > 65535 || a->time > (int64_t(1) << 30)) return TF_ERR_SHAPE;
   if (a->variant < TF_MAMBA_AUTO || a->variant > TF_MAMBA_PIPE) return TF_ERR_VARIANT;
   if (a->reverse != 0 && a->reverse != 1) return TF_ERR_SHAPE;
+  // the fused B/C norms come as a pair
+  if ((a->q_norm == nullptr) != (a->k_norm == nullptr)) return TF_ERR_NULL;
   // empty tensors may carry NULL data pointers
   if (!empty(a) && (!a->q || !a->k || !a->v || !a->adt || !a->dt || !a->trap || !a->angles ||
                     !a->z || !a->qb || !a->kb || !a->d || !a->out))

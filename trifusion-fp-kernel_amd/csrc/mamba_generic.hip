@@ -41,6 +41,7 @@ struct GenericShared {
   float scale[kChunk];
   float qk[kChunk];
   float dt[kChunk];
+  float rn[2][kChunk];  // B/C norm scales of the chunk's q and k rows
 };
 
 __global__ __launch_bounds__(kThreads) void mamba_generic_kernel(const tf_mamba_args a) {
@@ -59,6 +60,7 @@ __global__ __launch_bounds__(kThreads) void mamba_generic_kernel(const tf_mamba_
   const int tlim = rev ? L : T;
   auto row = [&](int t) -> int64_t { return rev ? L - 1 - t : t; };
   const bool raw = a.dt_bias != nullptr;
+  const bool norm = a.q_norm != nullptr;
   const float step_bias = raw ? a.dt_bias[h] : 0.f;
 
   const int64_t qo = b * a.q_stride[0] + qh * a.q_stride[2];
@@ -108,15 +110,37 @@ __global__ __launch_bounds__(kThreads) void mamba_generic_kernel(const tf_mamba_
       const int r = e / n_state, n = e - r * n_state;
       const int t = t0 + r;
       const bool valid = t < L;
-      const float qv = valid ? load_f32(a.q, a.q_dtype, qo + row(t) * a.q_stride[1] + n * a.q_stride[3]) : 0.f;
-      const float kv = valid ? load_f32(a.k, a.k_dtype, ko + row(t) * a.k_stride[1] + n * a.k_stride[3]) : 0.f;
-      sh.qr[r][n] = qv + a.qb[h * n_state + n];
-      sh.kr[r][n] = kv + a.kb[h * n_state + n];
+      sh.qr[r][n] = valid ? load_f32(a.q, a.q_dtype, qo + row(t) * a.q_stride[1] + n * a.q_stride[3]) : 0.f;
+      sh.kr[r][n] = valid ? load_f32(a.k, a.k_dtype, ko + row(t) * a.k_stride[1] + n * a.k_stride[3]) : 0.f;
     }
     for (int e = tid; e < kChunk * p_dim; e += kThreads) {
       const int r = e / p_dim, p = e - r * p_dim;
       const int t = t0 + r;
       sh.v[r][p] = t < L ? load_f32(a.v, a.v_dtype, vo + row(t) * a.v_stride[1] + p * a.v_stride[3]) : 0.f;
+    }
+    __syncthreads();
+    if (norm) {
+      // B/C RMSNorm of the raw rows (mamba.py:56-57, kernels/__init__.py:10-12):
+      // one thread per row of q (tid < 64) and of k
+      if (tid < 2 * kChunk) {
+        const int r = tid & (kChunk - 1);
+        const float* x = tid < kChunk ? sh.qr[r] : sh.kr[r];
+        float ss = 0.f;
+        for (int n = 0; n < n_state; ++n) ss += x[n] * x[n];
+        sh.rn[tid >> 6][r] = rsqrtf(ss / static_cast<float>(n_state) + a.norm_eps);
+      }
+      __syncthreads();
+    }
+    // biases, after the norm rounded to the operand dtype as the norm's output is
+    for (int e = tid; e < kChunk * n_state; e += kThreads) {
+      const int r = e / n_state, n = e - r * n_state;
+      float qv = sh.qr[r][n], kv = sh.kr[r][n];
+      if (norm) {
+        qv = round_to(qv * sh.rn[0][r] * a.q_norm[n], a.q_dtype);
+        kv = round_to(kv * sh.rn[1][r] * a.k_norm[n], a.k_dtype);
+      }
+      sh.qr[r][n] = qv + a.qb[h * n_state + n];
+      sh.kr[r][n] = kv + a.kb[h * n_state + n];
     }
     __syncthreads();
     // skip term from the unrotated biased vectors (mamba_fused.py:124)

@@ -59,6 +59,8 @@ struct Smem {
   double carry[64];         // phase carry entering the super-chunk
   float qb[32 * NT];
   float kb[32 * NT];
+  float qw[32 * NT];  // B/C norm weights (fused norms only)
+  float kw[32 * NT];
 };
 
 // Global inputs of one wave's 32 rows, in two parts loaded at different
@@ -218,6 +220,10 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
   for (int i = threadIdx.x; i < N; i += W * 64) {
     sh.qb[i] = P.qb[h * N + i];
     sh.kb[i] = P.kb[h * N + i];
+    if (P.qk_norm) {
+      sh.qw[i] = P.qn_w[i];
+      sh.kw[i] = P.kn_w[i];
+    }
   }
   float4 run[SPT];
 #pragma unroll
@@ -374,6 +380,25 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
       int bias_off = 0;
       asm volatile("" : "+v"(bias_off));
       const float* prow = stg + (32 * hf + c32) * rs;
+      // Fused B/C RMSNorm (mamba.py:56-57): the row's sum of squares over this
+      // lane's half of the state dim and the other half's (lane ^ 32), then
+      // each element x -> bf16(x * rsqrt(mean(x^2) + eps) * w) before its bias
+      float rq = 0.f, rk = 0.f;
+      if (P.qk_norm) {
+        float sq = 0.f, sk = 0.f;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4) {
+            if constexpr (MODE == 0) sq += lo_f(q[s][q4]) * lo_f(q[s][q4]) + hi_f(q[s][q4]) * hi_f(q[s][q4]);
+            sk += lo_f(k[s][q4]) * lo_f(k[s][q4]) + hi_f(k[s][q4]) * hi_f(k[s][q4]);
+          }
+        }
+        if constexpr (MODE == 0) sq += __shfl_xor(sq, 32);
+        sk += __shfl_xor(sk, 32);
+        rq = rsqrtf(sq / static_cast<float>(N) + P.norm_eps);
+        rk = rsqrtf(sk / static_cast<float>(N) + P.norm_eps);
+      }
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
         float co[4] = {1.f, 1.f, 1.f, 1.f}, si[4] = {0.f, 0.f, 0.f, 0.f};
@@ -400,12 +425,28 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
         const float4 kbh = *reinterpret_cast<const float4*>(&sh.kb[kidx(s, hh, 4) + bias_off]);
         const float qbs[8] = {qbl.x, qbl.y, qbl.z, qbl.w, qbh.x, qbh.y, qbh.z, qbh.w};
         const float kbs[8] = {kbl.x, kbl.y, kbl.z, kbl.w, kbh.x, kbh.y, kbh.z, kbh.w};
+        float qns[8] = {}, kns[8] = {};
+        if (P.qk_norm) {
+          const float4 ql = *reinterpret_cast<const float4*>(&sh.qw[kidx(s, hh, 0) + bias_off]);
+          const float4 qh4 = *reinterpret_cast<const float4*>(&sh.qw[kidx(s, hh, 4) + bias_off]);
+          const float4 kl = *reinterpret_cast<const float4*>(&sh.kw[kidx(s, hh, 0) + bias_off]);
+          const float4 kh4 = *reinterpret_cast<const float4*>(&sh.kw[kidx(s, hh, 4) + bias_off]);
+          const float qa[8] = {ql.x, ql.y, ql.z, ql.w, qh4.x, qh4.y, qh4.z, qh4.w};
+          const float ka[8] = {kl.x, kl.y, kl.z, kl.w, kh4.x, kh4.y, kh4.z, kh4.w};
+#pragma unroll
+          for (int j = 0; j < 8; ++j) qns[j] = qa[j], kns[j] = ka[j];
+        }
 #pragma unroll
         for (int q4 = 0; q4 < 4; ++q4) {
           const float qb0 = qbs[2 * q4], qb1 = qbs[2 * q4 + 1];
           const float kb0 = kbs[2 * q4], kb1 = kbs[2 * q4 + 1];
-          const uint32_t qw = q[s][q4];
-          const uint32_t kw = k[s][q4];
+          uint32_t qw = q[s][q4];
+          uint32_t kw = k[s][q4];
+          if (P.qk_norm) {
+            if constexpr (MODE == 0)
+              qw = pack2(lo_f(qw) * rq * qns[2 * q4], hi_f(qw) * rq * qns[2 * q4 + 1]);
+            kw = pack2(lo_f(kw) * rk * kns[2 * q4], hi_f(kw) * rk * kns[2 * q4 + 1]);
+          }
           const float q0 = lo_f(qw) + qb0, q1 = hi_f(qw) + qb1;
           const float k0 = lo_f(kw) + kb0, k1 = hi_f(kw) + kb1;
           if constexpr (MODE == 0) part += q0 * k0 + q1 * k1;
@@ -797,6 +838,10 @@ MfmaParams make_params(const tf_mamba_args& a) {
   P.ctl_bf16 = a.dt_dtype == TF_BFLOAT16;
   P.a_floor = a.a_floor;
   P.dt_bias = a.dt_bias;
+  P.qk_norm = a.q_norm != nullptr;
+  P.norm_eps = a.norm_eps;
+  P.qn_w = a.q_norm;
+  P.kn_w = a.k_norm;
   P.rev = a.reverse != 0;
   if (P.rev) {
     P.q_st = -P.q_st, P.k_st = -P.k_st, P.v_st = -P.v_st, P.z_st = -P.z_st, P.o_st = -P.o_st;

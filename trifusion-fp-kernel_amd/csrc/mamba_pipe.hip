@@ -88,14 +88,20 @@ typedef __attribute__((ext_vector_type(4))) short s16x4;
 typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 
 // Element offset of 8-byte unit u (0..15) of row t (0..63) in a [64][64] bf16
-// row buffer. Units are XOR-swizzled by the row, so that the three access
-// patterns each touch 16 distinct units (all 32 banks once) per 16 lanes:
-// row-form reads (16 rows, one unit), transposing reads (4 rows x 4 units) and
-// row writes (16 rows, one unit).
+// row buffer. Units are XOR-swizzled by the row, so that the access patterns
+// each touch 16 distinct units (all 32 banks once) per 16 lanes: row-form
+// reads (16 rows, one unit), transposing reads (4 rows x 4 units) and the
+// rotary's row writes (rows t and t + 4, units 2 ng (+1) of ng = 0..7: bit 0
+// of the swizzle differs between the two rows, so one writes even units and
+// the other odd ones).
 __device__ __forceinline__ int rb_off(int t, int u) {
   const int swz = ((t & 3) << 2) | ((t >> 2) & 3);
   return t * 64 + ((u ^ swz) << 2);
 }
+
+// Row (0..7) of an eight-row block held by lanes 8 j .. 8 j + 7: j / 2 + 4 (j % 2),
+// so the two rows of each 16 lanes are four apart (conflict-free row writes).
+__device__ __forceinline__ int row8_of_lane(int lane) { return (lane >> 4) + 4 * ((lane >> 3) & 1); }
 
 __device__ __forceinline__ u32x2 rb_read(const uint16_t* buf, int t, int u) {
   return *reinterpret_cast<const u32x2*>(buf + rb_off(t, u));
@@ -151,13 +157,35 @@ struct PipeSmem {
   float cs[3][64];   // inclusive log2 decay within the chunk
   float wv[3][64];   // 2^(tot - cs_t)
   float gam[3][64];  // dt_t sigmoid(trap_t)
-  float skip[3][8][64];  // partial (q + qb).(k + kb) of each wave's 8 channels
-  float tot[3][4];       // [0]: the chunk's total log2 decay
+  float skip[3][64];  // (q + qb).(k + kb) of each row
+  float tot[3][4];    // [0]: the chunk's total log2 decay
+  float nw[2][64];    // fused B/C norm weights of q and k
 };
 
 struct PipeCtl {
   float dt, dn, adt, tr, tn;
 };
+
+// Fused B/C RMSNorm (mamba.py:56-57, kernels/__init__.py:10-12) of a row of 64
+// bf16 channels held as 8 channels by each of 8 neighbouring lanes:
+// x -> bf16(x rsqrt(mean(x^2) + eps) w), the rounding of the separate norm's
+// bf16 output. w8: the lane's 8 weights (LDS). The walk and the summary pass
+// both call this, so a row is normalised to the same bits in either.
+__device__ __forceinline__ u32x4 norm_row8(const u32x4& x, const float* w8, float eps) {
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    ss = __builtin_fmaf(lo_f(x[j]), lo_f(x[j]), ss);
+    ss = __builtin_fmaf(hi_f(x[j]), hi_f(x[j]), ss);
+  }
+  const float r = rsqrtf(group8_sum(ss) / 64.f + eps);
+  const float4 wa = reinterpret_cast<const float4*>(w8)[0], wb = reinterpret_cast<const float4*>(w8)[1];
+  const float w[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+  u32x4 y;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) y[j] = pack2(lo_f(x[j]) * r * w[2 * j], hi_f(x[j]) * r * w[2 * j + 1]);
+  return y;
+}
 
 template <bool BF16>
 __device__ __forceinline__ float load_elem(const void* base, int i) {
@@ -392,10 +420,12 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
     const bool phase_wave = w >= 8 && p_idx * RPW < R;  // wave-uniform
 
     // rotary tasks of the state and prologue waves: row rrow of the chunk,
-    // channel group ng (state waves groups 0-3, prologue waves 4-7; 16 rows
-    // per wave)
-    const int rrow = 16 * (w & 3) + (lane >> 2);
-    const int ng = (state_wave ? 0 : 4) + (lane & 3);
+    // channel group ng; eight rows per wave (prologue waves rows 0-31, state
+    // waves rows 32-63), a row's eight channel groups on eight neighbouring
+    // lanes, so a wave's row load is eight whole 128-byte rows and a row's
+    // reductions (the B/C norms, the skip term) stay within its lanes
+    const int rrow = 8 * (state_wave ? 4 + s_idx : p_idx) + row8_of_lane(lane);
+    const int ng = lane & 7;
     auto load_rows = [&](int c) {
       const int t = min(c * kChunk + rrow, L - 1);
       PipeRows r;
@@ -476,44 +506,35 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
     }
 
     // bias, rotation, scaling and bf16 rounding of chunk c's rows (lane = row
-    // rrow, channels 8 ng .. 8 ng + 7; mamba_fused.py:112-135, 151). The state
-    // waves take channel groups 0-3, which hold the rotated pairs when R <= 16,
-    // and the prologue waves groups 4-7 (first in their interval A, whose
-    // score tiles and controls are short), so the output waves' interval A
-    // holds only their own tile's work; a wave's 16 rows x 4 groups make its
-    // row loads 16 pieces of 64 contiguous bytes (a row per lane would touch
-    // 64 cache lines per load).
+    // rrow, channels 8 ng .. 8 ng + 7; mamba_fused.py:112-135, 151), after the
+    // fused B/C RMSNorm when P.qk_norm (mamba.py:56-57: x -> bf16(x rsqrt(
+    // mean(x^2) + eps) w), the separate norm's output rounding). One
+    // branch-free form for every lane: pairs 4 ng + j >= R turn by the
+    // identity, x * 1 - y * 0 being x exactly.
     auto rotary = [&](const PipeRows& in, int c) {
       const int cb = c & 1, cr = c % 3;
       const bool valid = c * kChunk + rrow < L;
       const float scl = sh.sc[cr][rrow];
       const float wvt = sh.wv[cr][rrow];
+      u32x4 qin = in.q, kin = in.k;
+      if (P.qk_norm) {
+        qin = norm_row8(qin, &sh.nw[0][8 * ng], P.norm_eps);
+        kin = norm_row8(kin, &sh.nw[1][8 * ng], P.norm_eps);
+      }
       u32x4 qo, ko, vo, vso;
       float part = 0.f;
-      if (4 * ng < R) {
-        // pairs 4 ng + j >= R turn by the identity: x * 1 - y * 0 is x exactly
-        const float2* tg = reinterpret_cast<const float2*>(&sh.trig[cb][rrow * kTrigStride + 8 * ng]);
-        const float2 t0 = tg[0], t1 = tg[1], t2 = tg[2], t3 = tg[3];
-        const float cosv[4] = {t0.x, t1.x, t2.x, t3.x}, sinv[4] = {t0.y, t1.y, t2.y, t3.y};
+      const float2* tg = reinterpret_cast<const float2*>(&sh.trig[cb][rrow * kTrigStride + 8 * ng]);
+      const float2 t0 = tg[0], t1 = tg[1], t2 = tg[2], t3 = tg[3];
+      const float cosv[4] = {t0.x, t1.x, t2.x, t3.x}, sinv[4] = {t0.y, t1.y, t2.y, t3.y};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const bool on = 4 * ng + j < R;
-          const float cv = on ? cosv[j] : 1.f, sv = on ? sinv[j] : 0.f;
-          const float q0 = lo_f(in.q[j]) + qbv[2 * j], q1 = hi_f(in.q[j]) + qbv[2 * j + 1];
-          const float k0 = lo_f(in.k[j]) + kbv[2 * j], k1 = hi_f(in.k[j]) + kbv[2 * j + 1];
-          part += q0 * k0 + q1 * k1;
-          qo[j] = pack2(q0 * cv - q1 * sv, q0 * sv + q1 * cv);
-          ko[j] = key_pair(k0, k1, cv, sv, scl);
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float q0 = lo_f(in.q[j]) + qbv[2 * j], q1 = hi_f(in.q[j]) + qbv[2 * j + 1];
-          const float k0 = lo_f(in.k[j]) + kbv[2 * j], k1 = hi_f(in.k[j]) + kbv[2 * j + 1];
-          part += q0 * k0 + q1 * k1;
-          qo[j] = pack2(q0, q1);
-          ko[j] = pack2(k0 * scl, k1 * scl);
-        }
+      for (int j = 0; j < 4; ++j) {
+        const bool on = 4 * ng + j < R;
+        const float cv = on ? cosv[j] : 1.f, sv = on ? sinv[j] : 0.f;
+        const float q0 = lo_f(qin[j]) + qbv[2 * j], q1 = hi_f(qin[j]) + qbv[2 * j + 1];
+        const float k0 = lo_f(kin[j]) + kbv[2 * j], k1 = hi_f(kin[j]) + kbv[2 * j + 1];
+        part += q0 * k0 + q1 * k1;
+        qo[j] = pack2(q0 * cv - q1 * sv, q0 * sv + q1 * cv);
+        ko[j] = key_pair(k0, k1, cv, sv, scl);
       }
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -525,7 +546,8 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
       rb_write16(sh.kr[cb], rrow, 2 * ng, ko);
       rb_write16(sh.v[cb], rrow, 2 * ng, vo);
       rb_write16(sh.vs[cb], rrow, 2 * ng, vso);
-      sh.skip[cr][ng][rrow] = part;
+      part = group8_sum(part);
+      if (ng == 0) sh.skip[cr][rrow] = part;
     };
 
     // Each role runs its own copy of the walk, with the same two barriers per
@@ -565,6 +587,8 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
         dts[i] = load_elem<CTL16>(P.dt, dto + min(c0 * kChunk + sg * RPW + i, L - 1) * P.d_st);
     }
     if (w >= 4) rows = load_rows(c0);
+    // fused B/C norm weights, read by the rotary from the first chunk on
+    if (w < 2 && P.qk_norm) sh.nw[w][lane] = (w == 0 ? P.qn_w : P.kn_w)[lane];
     TF_STAGE(16);
     // A seeded segment's entering state: the segment scan of the unit's
     // summaries of the segments before it, S <- S 2^dec_g + turn_g(summary_g)
@@ -728,10 +752,7 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
           }
 #pragma unroll
           for (int g = 0; g < 4; ++g) vv[g] = rb_read(sh.v[cb], tl, 8 * opt + 2 * g + hh);
-          float part = 0.f;
-#pragma unroll
-          for (int j = 0; j < 8; ++j) part += sh.skip[cr][j][tl];
-          const float coef = skip_d + sh.gam[cr][tl] * part;
+          const float coef = skip_d + sh.gam[cr][tl] * sh.skip[cr][tl];
           const float decay = fast_exp2(sh.cs[cr][tl]);
           f32x16 yi = zero16();
 #pragma unroll
@@ -981,6 +1002,7 @@ struct SummarySmem {
   float sc[256];
   float wv[256];
   float tot[2][4];  // the chunks' total log2 decays, by batch parity
+  float kw[64];     // fused B norm weights
 };
 
 // Summary pass of the chunk-parallel form, parallel over the chunks of the
@@ -1047,7 +1069,7 @@ __global__ __launch_bounds__(1024) void pipe_summary_kernel(const MfmaParams P) 
   // key rotation tasks: channel group ng of batch rows rsub and rsub + 128
   // (8 lanes per row, so a wave's row loads are 8 whole 128-byte rows)
   const int ng = lane & 7;
-  const int rsub = w * 8 + (lane >> 3);
+  const int rsub = w * 8 + row8_of_lane(lane);
   float kbv[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) kbv[j] = P.kb[h * 64 + 8 * ng + j];
@@ -1080,6 +1102,8 @@ __global__ __launch_bounds__(1024) void pipe_summary_kernel(const MfmaParams P) 
     }
   };
   if (c0 < c1) issue_loads(c0);
+  // fused B norm weights, read by the key rotation (after two barriers)
+  if (w == 0 && P.qk_norm) sh.kw[lane] = P.kn_w[lane];
   for (int cb0 = c0; cb0 < c1; cb0 += kBatch, parity ^= 1) {
     const int nb = min(kBatch, c1 - cb0);
     const int t_lo = cb0 * kChunk;
@@ -1130,6 +1154,9 @@ __global__ __launch_bounds__(1024) void pipe_summary_kernel(const MfmaParams P) 
         const float scl = sh.sc[r];
         const float wvt = sh.wv[r];
         u32x4 ko, vso;
+        // the walk's norm of the raw key row (cc is wave-uniform: a wave's
+        // rows lie in one chunk)
+        if (P.qk_norm) kin[i] = norm_row8(kin[i], &sh.kw[8 * ng], P.norm_eps);
         if (4 * ng < R) {
           // pairs 4 ng + j >= R turn by the identity
           const float2* tg = reinterpret_cast<const float2*>(&sh.a.trig[r * kTrigStride + 8 * ng]);

@@ -68,6 +68,17 @@ __device__ __forceinline__ float dpp_f32(float x) {
   return __builtin_bit_cast(float, dpp_u32<CTRL, ROW_MASK>(__builtin_bit_cast(uint32_t, x)));
 }
 constexpr int kDppRowShr = 0x110;  // + n: row_shr:n
+
+// Sum over each aligned group of 8 lanes, in every lane of the group:
+// quad_perm [1,0,3,2] and [2,3,0,1] sum the quads, row_half_mirror (lane i of
+// an 8-lane half-row reads lane 7 - i) adds the other quad. Each step adds the
+// same two values in every lane, so all 8 lanes hold the same bits.
+__device__ __forceinline__ float group8_sum(float x) {
+  x += dpp_f32<0xB1>(x);
+  x += dpp_f32<0x4E>(x);
+  x += dpp_f32<0x141>(x);
+  return x;
+}
 constexpr int kDppRowBcast15 = 0x142;
 constexpr int kDppRowBcast31 = 0x143;
 
@@ -245,6 +256,12 @@ struct MfmaParams {
   uint32_t* phase_fx;
   // Pipelined kernel, unsegmented varlen walks: deal batch rows longest first.
   int lpt;
+  // Fused B/C RMSNorm: q and k are raw rows, each normalised as it is loaded,
+  // round(x * rsqrt(mean(x^2) + norm_eps) * w), with w = qn_w / kn_w ([N]).
+  int qk_norm;
+  float norm_eps;
+  const float* qn_w;
+  const float* kn_w;
 };
 
 // One step of the segment scan, S 2^dec + summary, as explicit fused

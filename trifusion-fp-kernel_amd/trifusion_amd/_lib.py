@@ -69,6 +69,9 @@ class MambaArgs(ctypes.Structure):
         ("dt_bias", c_ptr),
         ("a_floor", c_f32),
         ("reverse", c_i32),
+        ("q_norm", c_ptr),
+        ("k_norm", c_ptr),
+        ("norm_eps", c_f32),
     ]
 
 

@@ -12,6 +12,9 @@ recurrence are gfx950 HIP kernels; the two projections are torch GEMMs
 By default the controls (``:58-65``) are computed inside the recurrence from
 the raw ``a``/``ddt`` columns (``fuse_controls``; the same per-step formula as
 the separate ``mamba_controls`` kernel, which ``fuse_controls = False``
+restores), and so are the B/C norms (``:56-57``): the recurrence reads the raw
+B/C columns and normalises each row as it loads it (``fuse_norms``; the same
+rounding as the separate ``rms_pair`` launch, which ``fuse_norms = False``
 restores). ``forward(u, lengths, reverse=True)`` is the backward direction of
 the reference's bidirectional block, ``reverse_valid(backward_mamba(
 reverse_valid(u)))`` (``src/trifusion_l4/model.py:174-179``): every step of the
@@ -69,6 +72,7 @@ class Mamba3Inference(nn.Module):
         # "pipe" (pipelined MFMA walk), "mfma" (chunked MFMA scan), "generic" (fp32-FMA kernel) or "auto"
         self.variant = "auto"
         self.fuse_controls = True
+        self.fuse_norms = True
         self._padded = None
         self._padded_key = None
 
@@ -117,7 +121,13 @@ class Mamba3Inference(nn.Module):
         ``[B, T, H, P]`` buffer, when given)."""
         b, t, _ = p.shape
         z, v, k, q, ddt, a, trap, angles = self.split(p)
-        if self.B_norm.eps == self.C_norm.eps:
+        norms = {}
+        if self._fusable_norms():
+            # raw B/C columns; the recurrence applies both norms as it loads a row
+            q = q.reshape(b, t, 1, self.d_state)
+            k = k.reshape(b, t, 1, self.d_state)
+            norms = {"q_norm": self.C_norm.weight, "k_norm": self.B_norm.weight, "norm_eps": self.B_norm.eps}
+        elif self.B_norm.eps == self.C_norm.eps:
             # B and C sit side by side in the projection: both norms, one launch
             n = self.d_state
             kq = p[..., 2 * self.d_inner : 2 * self.d_inner + 2 * n]
@@ -150,5 +160,14 @@ class Mamba3Inference(nn.Module):
             reverse=reverse,
             out=out,
             **raw,
+            **norms,
         )
         return y.reshape(b, t, self.d_inner)
+
+    def _fusable_norms(self):
+        weights = (self.B_norm.weight, self.C_norm.weight)
+        return (
+            self.fuse_norms
+            and self.B_norm.eps == self.C_norm.eps
+            and all(w.dtype == torch.float32 and w.is_contiguous() for w in weights)
+        )

@@ -19,7 +19,13 @@ does. Keyword-only extensions:
   the raw ``a`` and ``ddt`` in-projection columns viewed as ``[B, H, T]``, and
   the recurrence computes ``mamba_controls`` (``src/trifusion_l4/kernels/
   buffers.py:82-101``) per step itself, so the ``[B, H, T]`` control tensors
-  and their launch disappear.
+  and their launch disappear;
+* ``q_norm=``, ``k_norm=`` (with ``norm_eps=``): the Mamba block's C and B
+  RMSNorm weights (``src/trifusion_l4/mamba.py:56-57``). ``q`` and ``k`` are
+  then the raw in-projection columns, and each row is normalised as it is
+  loaded, ``round(x * rsqrt(mean(x^2) + eps) * w)`` to q's dtype
+  (``src/trifusion_l4/kernels/__init__.py:10-12``), so the normalised copies
+  and the norm launch disappear.
 """
 
 import ctypes
@@ -38,7 +44,7 @@ def _shape_error(message):
 
 
 def build_args(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths=None, variant="auto", reverse=False,
-               dt_bias=None, a_floor=1e-4):
+               dt_bias=None, a_floor=1e-4, q_norm=None, k_norm=None, norm_eps=1e-5):
     """Validate the operands and pack them into a ``tf_mamba_args`` struct."""
     what = "fused_mamba"
     for name, t in (("q", q), ("k", k), ("v", v), ("z", z), ("angles", angles)):
@@ -79,7 +85,12 @@ def build_args(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths=None, 
             raise _shape_error(f"dt_bias must be a contiguous float32 tensor of shape {(h,)}")
         if adt.dtype != dt.dtype:
             raise TypeError("fused_mamba: raw controls a and ddt must share one dtype")
-    _lib.require_cuda(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths, dt_bias, what=what)
+    if (q_norm is None) != (k_norm is None):
+        raise _shape_error("q_norm and k_norm must be given together")
+    for name, ten in (("q_norm", q_norm), ("k_norm", k_norm)):
+        if ten is not None and (tuple(ten.shape) != (n,) or ten.dtype != torch.float32 or not ten.is_contiguous()):
+            raise _shape_error(f"{name} must be a contiguous float32 tensor of shape {(n,)}")
+    _lib.require_cuda(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths, dt_bias, q_norm, k_norm, what=what)
 
     a = _lib.MambaArgs()
     for name, ten in (
@@ -101,6 +112,9 @@ def build_args(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths=None, 
     a.dt_bias = dt_bias.data_ptr() if dt_bias is not None else None
     a.a_floor = float(a_floor)
     a.reverse = 1 if reverse else 0
+    a.q_norm = q_norm.data_ptr() if q_norm is not None else None
+    a.k_norm = k_norm.data_ptr() if k_norm is not None else None
+    a.norm_eps = float(norm_eps)
     for name, ten in (
         ("q", q),
         ("k", k),
@@ -127,11 +141,12 @@ def build_args(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths=None, 
 
 
 def launch(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths=None, variant="auto", reverse=False,
-           dt_bias=None, a_floor=1e-4):
+           dt_bias=None, a_floor=1e-4, q_norm=None, k_norm=None, norm_eps=1e-5):
     """Validate, then enqueue ``tf_fused_mamba`` on the current stream (the CUDA
     kernel of the ``trifusion_amd::fused_mamba`` operator); returns ``out``."""
     lib = _lib.load()
-    args = build_args(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths, variant, reverse, dt_bias, a_floor)
+    args = build_args(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths, variant, reverse, dt_bias, a_floor,
+                      q_norm, k_norm, norm_eps)
     # Long sequences over few (batch, head) units run chunk-parallel on scratch
     # the library sizes; it comes from torch's caching allocator (the graph's
     # private pool under capture), the C side never allocates.
@@ -167,32 +182,38 @@ def fused_mamba(
     reverse=False,
     dt_bias=None,
     a_floor=1e-4,
+    q_norm=None,
+    k_norm=None,
+    norm_eps=1e-5,
 ):
     """Fused Mamba-3 recurrence forward; returns ``out`` ``[B, T, H, P]``.
 
     ``warps`` is accepted for signature compatibility; gfx950 launch shapes are
     chosen by the library. ``variant`` selects ``"auto"`` (an MFMA kernel
     where supported), ``"pipe"`` (pipelined walk, N = P = 64), ``"mfma"``
-    (chunked scan) or ``"generic"``. ``reverse``, ``dt_bias`` and
-    ``a_floor`` are the extensions described in the module docstring.
+    (chunked scan) or ``"generic"``. ``reverse``, ``dt_bias``, ``a_floor``,
+    ``q_norm``, ``k_norm`` and ``norm_eps`` are the extensions described in the
+    module docstring.
     Dispatches through the ``trifusion_amd::fused_mamba`` operator
     (``fused_mamba.out`` with ``out=``).
     """
     del warps
-    ext = (lengths, variant, bool(reverse), dt_bias, float(a_floor))
+    ext = (lengths, variant, bool(reverse), dt_bias, float(a_floor), q_norm, k_norm, float(norm_eps))
     if out is None:
         return ops.fused_mamba(q, k, v, adt, dt, trap, qb, kb, angles, d, z, *ext)
     return ops.fused_mamba.out(q, k, v, adt, dt, trap, qb, kb, angles, d, z, *ext, out=out)
 
 
 def selected_variant(
-    q, k, v, adt, dt, trap, qb, kb, angles, d, z, out=None, lengths=None, variant="auto", reverse=False, dt_bias=None
+    q, k, v, adt, dt, trap, qb, kb, angles, d, z, out=None, lengths=None, variant="auto", reverse=False, dt_bias=None,
+    q_norm=None, k_norm=None,
 ):
     """Name of the kernel ``fused_mamba`` would launch for these operands."""
     lib = _lib.load()
     if out is None:
         out = torch.empty_like(v, memory_format=torch.contiguous_format)
-    args = build_args(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths, variant, reverse, dt_bias)
+    args = build_args(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths, variant, reverse, dt_bias,
+                      q_norm=q_norm, k_norm=k_norm)
     code = lib.tf_fused_mamba_variant(ctypes.byref(args))
     if code < 0:
         _lib.check(-code, "fused_mamba")

@@ -21,8 +21,12 @@ import torch
 NAMESPACE = "trifusion_amd"
 
 # keyword extensions of fused_mamba: valid lengths, kernel choice, reversed
-# walk of the valid prefix, raw controls (dt_bias) and their decay floor
-_EXT = "Tensor? lengths=None, str variant='auto', bool reverse=False, Tensor? dt_bias=None, float a_floor=0.0001"
+# walk of the valid prefix, raw controls (dt_bias) and their decay floor, and
+# the B/C RMSNorm weights applied to raw q/k rows (q_norm, k_norm, norm_eps)
+_EXT = (
+    "Tensor? lengths=None, str variant='auto', bool reverse=False, Tensor? dt_bias=None, float a_floor=0.0001, "
+    "Tensor? q_norm=None, Tensor? k_norm=None, float norm_eps=1e-05"
+)
 
 _SCHEMAS = {
     "fused_mamba": "fused_mamba(Tensor q, Tensor k, Tensor v, Tensor adt, Tensor dt, Tensor trap, Tensor qb, "
@@ -89,18 +93,20 @@ OPERATORS = tuple(_SCHEMAS)
 
 
 def _cuda_fused_mamba(q, k, v, adt, dt, trap, qb, kb, angles, d, z, lengths=None, variant="auto", reverse=False,
-                      dt_bias=None, a_floor=1e-4):
+                      dt_bias=None, a_floor=1e-4, q_norm=None, k_norm=None, norm_eps=1e-5):
     from .mamba_fused import launch
 
     out = torch.empty_like(v, memory_format=torch.contiguous_format)
-    return launch(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths, variant, reverse, dt_bias, a_floor)
+    return launch(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths, variant, reverse, dt_bias, a_floor,
+                  q_norm, k_norm, norm_eps)
 
 
 def _cuda_fused_mamba_out(q, k, v, adt, dt, trap, qb, kb, angles, d, z, lengths=None, variant="auto", reverse=False,
-                          dt_bias=None, a_floor=1e-4, *, out):
+                          dt_bias=None, a_floor=1e-4, q_norm=None, k_norm=None, norm_eps=1e-5, *, out):
     from .mamba_fused import launch
 
-    return launch(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths, variant, reverse, dt_bias, a_floor)
+    return launch(q, k, v, adt, dt, trap, qb, kb, angles, d, z, out, lengths, variant, reverse, dt_bias, a_floor,
+                  q_norm, k_norm, norm_eps)
 
 
 def _cuda_rms_norm(x, weight, eps=1e-5, out_dtype=None):
@@ -206,12 +212,12 @@ def _block(name):
 
 
 def _meta_fused_mamba(q, k, v, adt, dt, trap, qb, kb, angles, d, z, lengths=None, variant="auto", reverse=False,
-                      dt_bias=None, a_floor=1e-4):
+                      dt_bias=None, a_floor=1e-4, q_norm=None, k_norm=None, norm_eps=1e-5):
     return torch.empty_like(v, memory_format=torch.contiguous_format)
 
 
 def _meta_fused_mamba_out(q, k, v, adt, dt, trap, qb, kb, angles, d, z, lengths=None, variant="auto", reverse=False,
-                          dt_bias=None, a_floor=1e-4, *, out):
+                          dt_bias=None, a_floor=1e-4, q_norm=None, k_norm=None, norm_eps=1e-5, *, out):
     return out
 
 
