@@ -10,7 +10,7 @@
 //   stage of chunk c       interval   waves                    lane layout
 //   controls               A(c-1)     prologue wave 3          lane = row
 //   phase, cos/sin         B(c-1)     prologue waves           lane = (pair, row segment)
-//   bias, rotation         A(c)       state + prologue waves   lane = (row, 8 channels)
+//   [B/C norm,] bias, rot. A(c)       output + state waves     lane = (row, 8 channels)
 //   state S_{c+1}          B(c)       state waves              one 32x32 tile of S each
 //   scores                 A(c+1)     prologue waves 0-2       one 32x32 score tile each
 //   skip, inter-chunk      A(c+1)     output waves             one 32x32 tile of y each
@@ -39,39 +39,6 @@
 #include "mfma_tile.h"
 
 namespace tf {
-
-#ifdef TF_STAGE_PROBE
-// Stage timestamps of the walk, compiled in only in the library built with
-// -DTF_STAGE_PROBE (a measurement aid; the product library has none of
-// this): each wave keeps the s_memtime of event k in lane k of two VGPRs and
-// workgroup 0 stores them once at the end, so the walk issues no extra memory
-// operation (the compiler may not move code across a marker, so the probe
-// library's schedule can differ slightly); every workgroup also stores its
-// start and end s_memrealtime (100 MHz) and its unit and chunk count
-// (unit * 256 + chunks). Events: 20 kernel start, 16 start loads issued, 17 before the
-// chunk-0 controls, 14/15 before/after the start barrier, 24 + j / 40 + j
-// interval A start / interval B barrier end of iteration j (output waves),
-// 0-13 the stages of iteration 2 (per role), 21 walk end.
-__device__ long long g_stage_ts[12 * 64];
-__device__ long long g_stage_blk[4096 * 3];
-#define TF_STAGE(k)                                                  \
-  do {                                                               \
-    __builtin_amdgcn_sched_barrier(0);                               \
-    const long long stage_t_ = __builtin_amdgcn_s_memtime();         \
-    __builtin_amdgcn_sched_barrier(0);                               \
-    const bool stage_me_ = lane == (k);                              \
-    stage_lo = stage_me_ ? static_cast<int>(stage_t_) : stage_lo;    \
-    stage_hi = stage_me_ ? static_cast<int>(stage_t_ >> 32) : stage_hi; \
-  } while (0)
-#else
-#define TF_STAGE(k) \
-  do {              \
-  } while (0)
-#endif
-#define TF_STAGE2(k)               \
-  do {                             \
-    if (i - c0 == 2) TF_STAGE(k);  \
-  } while (0)
 
 namespace {
 
@@ -374,10 +341,6 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
   const int hw = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int w = SEEDED ? hw : (hw < 4 ? hw + 8 : hw - 4);
   const int lane = static_cast<int>(threadIdx.x & 63);
-#ifdef TF_STAGE_PROBE
-  int stage_lo = 0, stage_hi = 0;
-  const long long stage_blk_t0 = __builtin_amdgcn_s_memrealtime();
-#endif
   const int c32 = lane & 31;
   const int hh = lane >> 5;
   const bool out_wave = w < 4;
@@ -411,7 +374,6 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
   const float step_bias = P.ctl_raw ? P.dt_bias[h] : 0.f;
   const float skip_d = P.d[h];
 
-  TF_STAGE(20);
   if (c1 > c0) {
     constexpr int NSEG = 64 / RPW;  // row segments per pair
     const int pi = lane / NSEG;
@@ -419,12 +381,12 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
     const int pair = p_idx * RPW + pi;                // phase pair of a prologue wave's lane
     const bool phase_wave = w >= 8 && p_idx * RPW < R;  // wave-uniform
 
-    // rotary tasks of the state and prologue waves: row rrow of the chunk,
-    // channel group ng; eight rows per wave (prologue waves rows 0-31, state
+    // rotary tasks of the output and state waves: row rrow of the chunk,
+    // channel group ng; eight rows per wave (output waves rows 0-31, state
     // waves rows 32-63), a row's eight channel groups on eight neighbouring
     // lanes, so a wave's row load is eight whole 128-byte rows and a row's
     // reductions (the B/C norms, the skip term) stay within its lanes
-    const int rrow = 8 * (state_wave ? 4 + s_idx : p_idx) + row8_of_lane(lane);
+    const int rrow = 8 * (state_wave ? 4 + s_idx : w) + row8_of_lane(lane);
     const int ng = lane & 7;
     auto load_rows = [&](int c) {
       const int t = min(c * kChunk + rrow, L - 1);
@@ -567,7 +529,7 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
     // complete in order): the prologue waves' controls, angles and steps of
     // chunk c0 (every prologue wave loads the controls rows, wave 11 uses
     // them, so their count in each wave's outstanding loads is the same on
-    // every path), then the rows of the state and prologue waves, then a
+    // every path), then the rows of the output and state waves, then a
     // seeded segment's summaries.
     PipeCtl ctl0 = {};
     // controls are formed by prologue wave 3 (lane = row); the other prologue
@@ -586,10 +548,9 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
       for (int i = 0; i < RPW; ++i)
         dts[i] = load_elem<CTL16>(P.dt, dto + min(c0 * kChunk + sg * RPW + i, L - 1) * P.d_st);
     }
-    if (w >= 4) rows = load_rows(c0);
+    if (w < 8) rows = load_rows(c0);
     // fused B/C norm weights, read by the rotary from the first chunk on
     if (w < 2 && P.qk_norm) sh.nw[w][lane] = (w == 0 ? P.qn_w : P.kn_w)[lane];
-    TF_STAGE(16);
     // A seeded segment's entering state: the segment scan of the unit's
     // summaries of the segments before it, S <- S 2^dec_g + turn_g(summary_g)
     // for g < seg, float4 f = 64 w + lane and 64 w + lane + 512 of the record
@@ -658,13 +619,10 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
         if (P.ctl_raw) d = control_step(d, step_bias);
         dts[i] = c0 * kChunk + sg * RPW + i < L ? d : 0.f;
       }
-      TF_STAGE(17);
       if (w == 11) controls(ctl0, c0);
       if (phase_wave) phase_steps(th, dts, c0);
     }
-    TF_STAGE(14);
     lds_barrier();
-    TF_STAGE(15);
 
     if (out_wave) {
       const int th_o = w >> 1, opt = w & 1;
@@ -686,13 +644,13 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
         zr[0] = *reinterpret_cast<const u32x4*>(zrow);
         zr[1] = *reinterpret_cast<const u32x4*>(zrow + 8);
       };
-      // z, then stores: the order of every later iteration
+      // rows (above), z, then stores: the order of every later iteration
       __builtin_amdgcn_sched_barrier(0);
       u32x4 zr[2];
       load_z(c0, zr);
       __builtin_amdgcn_sched_barrier(0);
       // dropped stores, so the walk starts with the same outstanding
-      // operations (z, stores) as every later iteration
+      // operations (rows, z, stores) as every later iteration
 #pragma unroll
       for (int g = 0; g < (OUT32 ? 4 : 2); ++g)
         __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, out_rsrc, kOutOfRange, 0, 0);
@@ -702,8 +660,6 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
       for (int e = 0; e < 16; ++e) gate[e] = 0.f;
       for (int i = c0; i <= c1; ++i) {
         // ---------------- interval A(i) ----------------
-        if (i - c0 < 12) TF_STAGE(24 + (i - c0));
-        TF_STAGE2(0);
         if (i > c0) {
           // silu factors of chunk i - 1 from its gate rows (loaded at A(i - 1))
           // columns 8 g + 4 hh .. + 3 of the tile layout: hh = 0 keeps its
@@ -735,8 +691,10 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
 #pragma unroll
           for (int e = 0; e < 16; ++e) asm volatile("" : "+v"(gate[e]));
         }
-        TF_STAGE2(13);
         load_z(i, zr);
+        // rows 0-31 of chunk i (the state waves take rows 32-63)
+        if (i < c1) rotary(rows, i);
+        rows = load_rows(i + 1);
         if (i > c0) {
           // chunk c = i - 1, tile (th, pt) of y^T[p][t]: (D + gamma (q + qb).(k + kb)) v
           // (mamba_fused.py:124, 147) + 2^cs qr . bf16(S_c)^T (mamba_fused.py:143)
@@ -765,9 +723,7 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
             ybase[4 * g + 3] = coef * hi_f(vv[g][1]) + yi[4 * g + 3] * decay;
           }
         }
-        TF_STAGE2(4);
         lds_barrier();
-        TF_STAGE2(5);
 
         // ---------------- interval B(i) ----------------
         // chunk c = i - 1: intra-chunk scores . v (mamba_fused.py:144-146), gate, store
@@ -797,10 +753,8 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
             y = mfma(v2, s2, y);
             y = mfma(v3, s3, y);
           }
-          TF_STAGE2(8);
 #pragma unroll
           for (int e = 0; e < 16; ++e) yv[e] = y[e] * gate[e];
-          TF_STAGE2(9);
         }
         // Every lane stores in every iteration, through the unit's range-checked
         // output buffer: rows t >= L (and the whole first iteration, which has
@@ -832,10 +786,7 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
             __builtin_amdgcn_raw_buffer_store_b128(u32x4{x0[0], x1[0], x0[1], x1[1]}, out_rsrc, lane_off + 16 * k, 0, 0);
           }
         }
-        TF_STAGE2(11);
         lds_barrier();
-        TF_STAGE2(12);
-        if (i - c0 < 12) TF_STAGE(40 + (i - c0));
       }
     } else if (state_wave) {
       const int nt = (s_idx >> 1) & 1, spt = s_idx & 1;
@@ -862,13 +813,9 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
       }
       for (int i = c0; i <= c1; ++i) {
         // ---------------- interval A(i) ----------------
-        TF_STAGE2(0);
         if (i < c1) rotary(rows, i);
-        TF_STAGE2(1);
         rows = load_rows(i + 1);
-        TF_STAGE2(4);
         lds_barrier();
-        TF_STAGE2(5);
 
         // ---------------- interval B(i) ----------------
         // the walk needs S_{i+1} for a later chunk
@@ -895,11 +842,8 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
           }
           sh.sb[(i + 1) % 3][s_idx][0][lane] = lo;
           sh.sb[(i + 1) % 3][s_idx][1][lane] = hi;
-          TF_STAGE2(6);
         }
-        TF_STAGE2(11);
         lds_barrier();
-        TF_STAGE2(12);
       }
     } else {
       // The prologue waves carry each interval's longest chain (the score
@@ -910,11 +854,7 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
       for (int i = c0; i <= c1; ++i) {
         // ---------------- interval A(i) ----------------
         // angles of chunk i + 1, for the phase at B(i)
-        TF_STAGE2(0);
         load_pipe_angles<RPW, ANG16>(P, th, gbase, pair, (i + 1) * kChunk + sg * RPW, L);
-        if (i < c1) rotary(rows, i);
-        TF_STAGE2(1);
-        rows = load_rows(i + 1);
         if (p_idx < 3 && i > c0) {
           // scores of chunk i - 1: tile (th, uh) = (0,0), (1,0), (1,1)
           const int c = i - 1;
@@ -935,36 +875,18 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
           score_tile(acc, csr[32 * sth + c32], csr + 32 * suh, sth == suh, c32, hh, sc);
           sh.score[cb][p_idx][0][lane] = sc[0];
           sh.score[cb][p_idx][1][lane] = sc[1];
-          TF_STAGE2(2);
         }
         if (p_idx == 3 && i + 1 < c1) controls(ctl_next, i + 1);
-        TF_STAGE2(3);
         ctl_next = load_pipe_ctl<CTL16, TRAP16>(P, dto, ado, trb, (i + 2) * kChunk + ctl_lane, L, tlim);
-        TF_STAGE2(4);
         lds_barrier();
-        TF_STAGE2(5);
 
         // ---------------- interval B(i) ----------------
         if (phase_wave && i + 1 < c1) phase(th, i + 1);
-        TF_STAGE2(7);
-        TF_STAGE2(11);
         lds_barrier();
-        TF_STAGE2(12);
       }
     }
   }
 
-  TF_STAGE(21);
-#ifdef TF_STAGE_PROBE
-  if (blockIdx.x == 0)
-    g_stage_ts[w * 64 + lane] =
-        (static_cast<long long>(static_cast<unsigned>(stage_hi)) << 32) | static_cast<unsigned>(stage_lo);
-  if (threadIdx.x == 0 && blockIdx.x < 4096) {
-    g_stage_blk[3 * blockIdx.x] = stage_blk_t0;
-    g_stage_blk[3 * blockIdx.x + 1] = __builtin_amdgcn_s_memrealtime();
-    g_stage_blk[3 * blockIdx.x + 2] = static_cast<long long>(unit) * 256 + (c1 - c0);
-  }
-#endif
   {
     // rows in [L, T) of the segment's time range (the whole range with one
     // segment), the same rows in either direction: unreversed base and
@@ -1365,14 +1287,3 @@ int launch_pipe(const tf_mamba_args& a, hipStream_t stream) {
 
 }  // namespace tf
 
-#ifdef TF_STAGE_PROBE
-// Stage timestamps of the last walk (workgroup 0, [12 waves][64 events],
-// s_memtime) and every workgroup's start, end (s_memrealtime) and unit *
-// 256 + chunk count ([4096][3]) of the library built with -DTF_STAGE_PROBE.
-// Not part of the product interface.
-extern "C" int tf_stage_probe_read(long long* ts, long long* blocks) {
-  if (!ts || !blocks) return TF_ERR_NULL;
-  if (hipMemcpyFromSymbol(ts, HIP_SYMBOL(tf::g_stage_ts), sizeof(long long) * 12 * 64) != hipSuccess) return 1;
-  return hipMemcpyFromSymbol(blocks, HIP_SYMBOL(tf::g_stage_blk), sizeof(long long) * 4096 * 3) == hipSuccess ? 0 : 1;
-}
-#endif
