@@ -239,6 +239,7 @@ def test_empty_inputs():
         (16, 101, 32, 128, 32, "mfma"),  # the model's bidirectional shape (N = 128)
         (1, 7200, 16, 64, 16, "pipe"),  # long clip: pipelined kernel, cut into time segments
         (2, 64, 16, 64, 16, "pipe"),
+        (2, 256, 4, 16, 4, "mfma"),  # N = 16: the N = 32 kernel on zero-padded channels
     ],
 )
 def test_auto_selects_matrix_core_kernel(b, t, h, n, r, kernel):

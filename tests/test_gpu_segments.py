@@ -38,6 +38,7 @@ SEGMENT_CASES = {
     "b1_l1000_h4_p64_n64": (1, 1000, 4, 64, 64, 16, 1, None),
     "b2_l1500_h8_p32_n32_hq2": (2, 1500, 8, 32, 32, 8, 2, None),
     "b1_l900_h2_p64_n128": (1, 900, 2, 64, 128, 32, 1, None),
+    "b1_l1300_h4_p32_n16": (1, 1300, 4, 32, 16, 4, 1, None),
     "b1_l1100_h4_p64_n64_wide_rotary": (1, 1100, 4, 64, 64, 24, 1, None),
     "b2_l2000_h4_varlen": (2, 2000, 4, 64, 64, 16, 1, (1337, 327)),
     "b1_l4100_h16_p64_n64": (1, 4100, 16, 64, 64, 16, 1, None),

@@ -94,7 +94,14 @@ def test_workspace_size_query():
     assert size(forced) == up(recs * 16384) + up(chunks * 512) + up(recs * 4)
     assert size(_host_args(16, 400, 16)) == 0  # 256 units: one workgroup each
     assert size(_host_args(1, 64, 16)) == 0  # one chunk: nothing to split
-    assert size(_host_args(1, 7200, 16, state=16, head_dim=32, rotary=4)) == 0  # generic kernel
+    # N = 16 (bf16): the chunked kernel at N = 32 on zero-padded channels, per
+    # segment a 4 KB state record
+    assert size(_host_args(1, 7200, 16, state=16, head_dim=32, rotary=4)) == (
+        up(recs * 4096) + up(chunks * 512) + up(recs * 4)
+    )
+    fp32 = _host_args(1, 7200, 16, state=16, head_dim=32, rotary=4)
+    fp32.q_dtype = fp32.k_dtype = fp32.v_dtype = fp32.z_dtype = fp32.out_dtype = 0
+    assert size(fp32) == 0  # fp32 operands: the generic kernel, one workgroup per unit
     bad = _host_args(1, 100, 16)
     bad.heads = 0
     assert size(bad) < 0

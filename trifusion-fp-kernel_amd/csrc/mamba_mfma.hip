@@ -93,8 +93,14 @@ __device__ __forceinline__ void load_rows(const MfmaParams& P, HalfRows<KS, PS>&
   const uint16_t* v_row = vbase + tl * P.v_st;
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
-    if constexpr (WITH_Q) in.q[s] = load_row8(q_row, kidx(s, hh, 0));
-    in.k[s] = load_row8(k_row, kidx(s, hh, 0));
+    // k-steps past a 16-channel state are the zero padding (nothing to load)
+    if (16 * s < P.n_real) {
+      if constexpr (WITH_Q) in.q[s] = load_row8(q_row, kidx(s, hh, 0));
+      in.k[s] = load_row8(k_row, kidx(s, hh, 0));
+    } else {
+      if constexpr (WITH_Q) in.q[s] = u32x4{0u, 0u, 0u, 0u};
+      in.k[s] = u32x4{0u, 0u, 0u, 0u};
+    }
   }
 #pragma unroll
   for (int s = 0; s < PS; ++s) in.v[s] = load_row8(v_row, kidx(s, hh, 0));
@@ -217,12 +223,15 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
     }
     sh.carry[i] = acc;
   }
+  // biases and norm weights; a 16-channel state's padding channels get 0, so
+  // they stay 0 through bias, norm, rotation and scale
   for (int i = threadIdx.x; i < N; i += W * 64) {
-    sh.qb[i] = P.qb[h * N + i];
-    sh.kb[i] = P.kb[h * N + i];
+    const bool real = i < P.n_real;
+    sh.qb[i] = real ? P.qb[h * P.n_real + i] : 0.f;
+    sh.kb[i] = real ? P.kb[h * P.n_real + i] : 0.f;
     if (P.qk_norm) {
-      sh.qw[i] = P.qn_w[i];
-      sh.kw[i] = P.kn_w[i];
+      sh.qw[i] = real ? P.qn_w[i] : 0.f;
+      sh.kw[i] = real ? P.kn_w[i] : 0.f;
     }
   }
   float4 run[SPT];
@@ -396,8 +405,8 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
         }
         if constexpr (MODE == 0) sq += __shfl_xor(sq, 32);
         sk += __shfl_xor(sk, 32);
-        rq = rsqrtf(sq / static_cast<float>(N) + P.norm_eps);
-        rk = rsqrtf(sk / static_cast<float>(N) + P.norm_eps);
+        rq = rsqrtf(sq / static_cast<float>(P.n_real) + P.norm_eps);
+        rk = rsqrtf(sk / static_cast<float>(P.n_real) + P.norm_eps);
       }
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
@@ -822,6 +831,7 @@ MfmaParams make_params(const tf_mamba_args& a) {
   P.H = static_cast<int>(a.heads);
   P.group = static_cast<int>(a.heads / a.qk_heads);
   P.R = static_cast<int>(a.rotary);
+  P.n_real = static_cast<int>(a.state);
   P.out_f32 = a.out_dtype == TF_FLOAT32;
   P.trap_bf16 = a.trap_dtype == TF_BFLOAT16;
   P.angles_dtype = a.angles_dtype;
@@ -890,6 +900,10 @@ SegPlan plan_segments(const tf_mamba_args& a, int cw, int kf4) {
 
 int shape_cw(const tf_mamba_args& a) { return a.state == 128 ? 2 : 4; }
 
+// State dim the kernel runs at: N = 16 runs the N = 32 kernel, its upper 16
+// channels zero.
+int64_t padded_state(const tf_mamba_args& a) { return a.state < 32 ? 32 : a.state; }
+
 template <int NT, int PT, int CW, bool WIDE>
 int launch_modes(MfmaParams P, hipStream_t stream) {
   constexpr int kF4 = NT * PT * 256;
@@ -928,7 +942,8 @@ int launch_shape(const tf_mamba_args& a, hipStream_t stream) {
     P.chunk_phase = reinterpret_cast<double*>(ws + plan.phase_off);
     P.seg_decay = reinterpret_cast<float*>(ws + plan.decay_off);
   }
-  if (a.rotary > a.state / 4) return launch_modes<NT, PT, CW, true>(P, stream);
+  // WIDE: R above a quarter of the kernel's state dim (8 NT)
+  if (a.rotary > 8 * NT) return launch_modes<NT, PT, CW, true>(P, stream);
   return launch_modes<NT, PT, CW, false>(P, stream);
 }
 
@@ -936,7 +951,7 @@ int launch_shape(const tf_mamba_args& a, hipStream_t stream) {
 
 int64_t mfma_workspace_bytes(const tf_mamba_args& a) {
   if (!mfma_supported(a)) return 0;
-  const SegPlan plan = plan_segments(a, shape_cw(a), static_cast<int>((a.state / 32) * (a.head_dim / 32) * 256));
+  const SegPlan plan = plan_segments(a, shape_cw(a), static_cast<int>((padded_state(a) / 32) * (a.head_dim / 32) * 256));
   return plan.G > 1 ? plan.bytes : 0;
 }
 
@@ -951,11 +966,11 @@ bool mfma_supported(const tf_mamba_args& a) {
   if (a.trap_dtype != TF_FLOAT32 && a.trap_dtype != TF_BFLOAT16) return false;
   if (a.angles_dtype != TF_FLOAT32 && a.angles_dtype != TF_BFLOAT16) return false;
   if (a.out_dtype != TF_BFLOAT16 && a.out_dtype != TF_FLOAT32) return false;
-  if (!(a.state == 32 || a.state == 64 || a.state == 128)) return false;
+  if (!(a.state == 16 || a.state == 32 || a.state == 64 || a.state == 128)) return false;
   if (!(a.head_dim == 32 || a.head_dim == 64)) return false;
   if (a.rotary < 0 || a.rotary > a.state / 2) return false;
   // the phase staging area [64 rows][R rounded up to even] lives in a state slot
-  if (64 * ((a.rotary + 1) & ~int64_t(1)) > (a.state / 32) * (a.head_dim / 32) * 1024) return false;
+  if (64 * ((a.rotary + 1) & ~int64_t(1)) > (padded_state(a) / 32) * (a.head_dim / 32) * 1024) return false;
   if (a.batch * a.heads > 0x7fffffff) return false;
   if (!rows_vectorisable(a.q, a.q_stride, 2, 8) || !rows_vectorisable(a.k, a.k_stride, 2, 8) ||
       !rows_vectorisable(a.v, a.v_stride, 2, 8) || !rows_vectorisable(a.z, a.z_stride, 2, 8))
@@ -972,7 +987,7 @@ bool mfma_supported(const tf_mamba_args& a) {
 // super-chunk: its 69 KB of LDS lets two workgroups share a CU, so every unit
 // runs in one round instead of two (the model's 16 x 32 units: 37.8 -> 34.2 us).
 int launch_mfma(const tf_mamba_args& a, hipStream_t stream) {
-  const int nt = static_cast<int>(a.state / 32);
+  const int nt = static_cast<int>(padded_state(a) / 32);
   const int pt = static_cast<int>(a.head_dim / 32);
   if (nt == 1 && pt == 1) return launch_shape<1, 1, 4>(a, stream);
   if (nt == 1 && pt == 2) return launch_shape<1, 2, 4>(a, stream);

@@ -230,6 +230,8 @@ struct MfmaParams {
   int d_sb, d_sh, d_st;
   int r_sb, r_sh, r_st;
   int T, H, group, R, xcd_per;
+  // State dim of q/k (16 runs the N = 32 kernel on zero-padded channels)
+  int n_real;
   int out_f32, trap_bf16, angles_dtype;
   // Raw controls: adt/dt hold the in-projection's a/ddt columns (bf16 when
   // ctl_bf16), turned into the step and decay in the prologue.
