@@ -24,11 +24,12 @@ DEV = "cuda"
 TF_ERR_WORKSPACE = 7
 
 
-def call(entry, dargs, lengths=None, reverse=False):
+def call(entry, dargs, lengths=None, reverse=False, norms=None):
     lib = _lib.load()
     v = dargs[2]
     out = torch.full(v.shape, float("nan"), device=DEV, dtype=torch.float32)
-    args = build_args(*dargs, out, lengths, "auto", reverse, None, 1e-4)
+    q_norm, k_norm = norms if norms is not None else (None, None)
+    args = build_args(*dargs, out, lengths, "auto", reverse, None, 1e-4, q_norm, k_norm, 1e-5)
     workspace = None
     if entry == "tf_fused_mamba":
         need = lib.tf_fused_mamba_workspace_size(ctypes.byref(args))
@@ -63,6 +64,25 @@ def test_static_scratch_matches_workspace_entry():
         assert rc_ref == 0 and rc == 0
         assert torch.isfinite(got).all()
         assert torch.equal(got, ref), f"{name}: max diff {(got - ref).abs().max().item():.3e}"
+
+
+def test_static_entry_with_fused_norms():
+    """The B/C norms fused into the recurrence (raw q/k rows and norm
+    weights) through the static entry: the long clip's chunk-parallel
+    kernels (summary pass and seeded walks both normalise the keys) equal
+    tf_fused_mamba on a workspace bit for bit."""
+    args = clip_inputs(1, 7200, seed=25)
+    dargs = tuple(a.to(DEV) for a in args)
+    g = torch.Generator().manual_seed(26)
+    norms = tuple((0.5 + torch.rand(64, generator=g)).to(DEV) for _ in range(2))
+    print("case fused norms long_b1_l7200_h16", flush=True)
+    rc_ref, ref = call("tf_fused_mamba", dargs, norms=norms)
+    rc, got = call("tf_fused_mamba_static", dargs, norms=norms)
+    assert rc_ref == 0 and rc == 0
+    assert torch.isfinite(got).all()
+    assert torch.equal(got, ref)
+    _, plain = call("tf_fused_mamba", dargs)
+    assert not torch.equal(plain, ref), "the norm weights must change the result"
 
 
 def test_static_entry_under_graph_capture():
