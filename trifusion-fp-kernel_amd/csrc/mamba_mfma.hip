@@ -391,7 +391,9 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
       const float* prow = stg + (32 * hf + c32) * rs;
       // Fused B/C RMSNorm (mamba.py:56-57): the row's sum of squares over this
       // lane's half of the state dim and the other half's (lane ^ 32), then
-      // each element x -> bf16(x * rsqrt(mean(x^2) + eps) * w) before its bias
+      // each element x -> bf16(x * rsqrt(mean(x^2) + eps) * w) before its bias.
+      // The multiply-adds are spelled out, so the summary pass (MODE 1) and
+      // the output pass normalise a key row to the same bits.
       float rq = 0.f, rk = 0.f;
       if (P.qk_norm) {
         float sq = 0.f, sk = 0.f;
@@ -399,8 +401,12 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
         for (int s = 0; s < KS; ++s) {
 #pragma unroll
           for (int q4 = 0; q4 < 4; ++q4) {
-            if constexpr (MODE == 0) sq += lo_f(q[s][q4]) * lo_f(q[s][q4]) + hi_f(q[s][q4]) * hi_f(q[s][q4]);
-            sk += lo_f(k[s][q4]) * lo_f(k[s][q4]) + hi_f(k[s][q4]) * hi_f(k[s][q4]);
+            if constexpr (MODE == 0) {
+              sq = __builtin_fmaf(lo_f(q[s][q4]), lo_f(q[s][q4]), sq);
+              sq = __builtin_fmaf(hi_f(q[s][q4]), hi_f(q[s][q4]), sq);
+            }
+            sk = __builtin_fmaf(lo_f(k[s][q4]), lo_f(k[s][q4]), sk);
+            sk = __builtin_fmaf(hi_f(k[s][q4]), hi_f(k[s][q4]), sk);
           }
         }
         if constexpr (MODE == 0) sq += __shfl_xor(sq, 32);
