@@ -476,6 +476,15 @@ int tf_merge_gate(const void *cn, const void *mf, const void *mb, const void *an
                   void *stream);
 
 /*
+ * Evidence down-projection: z = bf16(silu(bf16(cat(cn, an) w^T + bias))), cn, an
+ * bf16 [rows, d] (contiguous, 16-byte aligned), w bf16 [r, 2d] (the Linear's
+ * weight), bias bf16 [r], z bf16 [rows, r]; d a multiple of 128, r one of 16, 32, 48, 64.
+ * Replaces torch.cat + e_down + F.silu (src/trifusion_l4/model.py:161).
+ */
+int tf_evidence_down(const void *cn, const void *an, const void *w, const void *bias, void *z, int64_t rows,
+                     int64_t d, int64_t r, void *stream);
+
+/*
  * Gated concatenation, masked depthwise merge and residual add: v = cat(cn, mn, an)
  * * 2 sigmoid(g) (fp32), c = masked depthwise conv (kernel k = 3; w bf16 [3d, k],
  * bias bf16 [3d]) of bf16(v), rounded to bf16, zero at t >= L_b; y = bf16(v + c)

@@ -18,6 +18,9 @@ replace:
 * ``evidence_norm``: ``masked(u_norm(x + value * 2 sigmoid(gate)))``
   (``src/trifusion_l4/model.py:166-167``);
 * ``gated_concat``: the reference branch (``kernels/__init__.py:59-63``);
+* ``evidence_down``: ``silu(e_down(cat(cn, an)))`` (``src/trifusion_l4/model.py:161``)
+  under bf16 autocast: bf16 operands, fp32 sums, the linear's bf16 result, SiLU
+  in fp32 rounded to bf16;
 * ``front_stage``: a whole CNN stage (``front.py:19-43``) under bf16 autocast:
   ``F.conv2d`` on bf16-rounded operands with bf16 outputs, ``front_norm``, the
   1x1 skip, the bf16 residual sum and SiLU, rows past the length cleared;
@@ -164,6 +167,13 @@ def pooled_attention(qkv, cos, sin, low_lengths, heads):
     mask = time_mask(low_lengths, t)[:, None, None, :]
     y = F.scaled_dot_product_attention(q, k, v, attn_mask=mask)
     return y.transpose(1, 2).reshape(b, t, -1).to(BF16)
+
+
+def evidence_down(cn, an, weight, bias):
+    """``silu(e_down(cat(cn, an)))`` under autocast: ``bf16(silu(bf16(cat w^T + b)))``."""
+    s = torch.cat((cn.to(BF16).float(), an.to(BF16).float()), -1)
+    z = (s @ weight.to(BF16).float().t() + bias.to(BF16).float()).to(BF16)
+    return F.silu(z.float()).to(BF16)
 
 
 def merge_gate(cn, mf, mb, an, weight, gate_w, gate_b, eps=1e-5):

@@ -21,6 +21,7 @@ from trifusion_amd.kernels.block import (
     Pool4,
     block_pre,
     depthwise_masked,
+    evidence_down,
     evidence_norm,
     glu_depthwise,
     merge_conv,
@@ -135,6 +136,48 @@ def test_merge_gate_and_conv():
     with torch.autocast("cuda", dtype=BF):
         conv = depthwise_masked(v, layer, lengths)
     assert torch.equal(y, add(v, conv, bf16=True))
+
+
+@pytest.mark.parametrize("rows, d, r", [(3 * 101, 1024, 64), (101, 128, 16), (37, 256, 48), (1, 384, 32), (0, 128, 64)])
+def test_evidence_down(rows, d, r):
+    """silu(e_down(cat(cn, an))) in one launch: the oracle's composition, and the
+    unfused GPU composition under autocast, within two bf16 steps (the linear's
+    output and the SiLU are each rounded; the sums run in another order)."""
+    g = gen(5)
+    cn = (torch.randn(rows, d, generator=g) * 1.5).to(BF)
+    an = (torch.randn(rows, d, generator=g) * 0.5).to(BF)
+    layer = torch.nn.Linear(2 * d, r)
+    with torch.no_grad():
+        layer.bias.uniform_(-0.5, 0.5, generator=g)
+    print(f"case evidence_down rows={rows} d={d} r={r}", flush=True)
+    dl = torch.nn.Linear(2 * d, r).to(DEV)
+    dl.load_state_dict(layer.state_dict())
+    with torch.inference_mode():
+        z = evidence_down(cn.to(DEV), an.to(DEV), dl)
+        with torch.autocast("cuda", torch.bfloat16):
+            unfused = F.silu(dl(torch.cat((cn.to(DEV), an.to(DEV)), -1)))
+    torch.cuda.synchronize()
+    assert z.shape == (rows, r) and z.dtype == BF
+    if rows == 0:
+        return
+    ref = O.evidence_down(cn, an, layer.weight.detach(), layer.bias.detach())
+    close_bf16(z, ref, steps=2)
+    close_bf16(z, unfused, steps=2)
+
+
+def test_evidence_down_3d_rows():
+    """[B, T, d] inputs: one row per (b, t), the output [B, T, r]."""
+    g = gen(6)
+    cn, an = (torch.randn(2, 70, 1024, generator=g).to(BF) for _ in range(2))
+    layer = torch.nn.Linear(2048, 64)
+    print("case evidence_down 3d", flush=True)
+    dl = torch.nn.Linear(2048, 64).to(DEV)
+    dl.load_state_dict(layer.state_dict())
+    with torch.inference_mode():
+        z = evidence_down(cn.to(DEV), an.to(DEV), dl)
+    torch.cuda.synchronize()
+    assert z.shape == (2, 70, 64)
+    close_bf16(z, O.evidence_down(cn, an, layer.weight.detach(), layer.bias.detach()), steps=2)
 
 
 def test_evidence_norm_bf16_out():

@@ -175,3 +175,23 @@ def test_front_stage_matches_direct_loops(s):
                 skip = ws[:, :, 0, 0].double() @ xd[i, :, tt * s, ff * 2]
                 want = F.silu(main + skip)
                 assert torch.allclose(y[i, tt, ff], want, rtol=0.03, atol=0.03), (i, tt, ff)
+
+
+def test_evidence_down_matches_loop():
+    """``evidence_down`` against an explicit float64 loop over rows and output
+    columns of the concatenated bf16 row, with the bf16 roundings of the
+    linear's result and of the SiLU; and the concatenation order matters."""
+    g = torch.Generator().manual_seed(31)
+    rows, d, r = 5, 12, 4
+    cn, an = torch.randn(rows, d, generator=g), torch.randn(rows, d, generator=g)
+    w, b = torch.randn(r, 2 * d, generator=g) / 4, torch.randn(r, generator=g)
+    y = O.evidence_down(cn, an, w, b).double()
+    bf = lambda t: t.to(torch.bfloat16).double()  # noqa: E731
+    ref = torch.empty(rows, r, dtype=torch.float64)
+    for i in range(rows):
+        s = torch.cat((bf(cn[i]), bf(an[i])))
+        for o in range(r):
+            z = bf(torch.tensor(sum(float(s[k]) * float(bf(w[o, k])) for k in range(2 * d)) + float(bf(b[o]))))
+            ref[i, o] = bf(z / (1 + torch.exp(-z)))
+    torch.testing.assert_close(y, ref, rtol=2 ** -7, atol=2 ** -7 * ref.abs().max().item())
+    assert not torch.allclose(O.evidence_down(an, cn, w, b).double(), ref, rtol=2 ** -6, atol=0)

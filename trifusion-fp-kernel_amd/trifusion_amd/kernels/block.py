@@ -451,6 +451,37 @@ def launch_merge_gate(cn, mf, mb, an, norm_weight, eps, gate_weight, gate_bias):
     return mn, g
 
 
+def evidence_down_fits(d, r):
+    """Widths ``tf_evidence_down`` takes: ``d`` a multiple of 128, ``r`` one of 16, 32, 48, 64."""
+    return d >= 128 and d % 128 == 0 and r in (16, 32, 48, 64)
+
+
+def evidence_down(cn, an, layer):
+    """``silu(layer(cat(cn, an)))`` for the block's ``e_down`` under autocast, with no
+    concatenated copy (``trifusion_amd::evidence_down``)."""
+    return ops.evidence_down(cn, an, layer.weight, layer.bias)
+
+
+def launch_evidence_down(cn, an, weight, bias):
+    lib = _lib.load()
+    _lib.require_cuda(cn, an, weight, bias, what="evidence_down")
+    cc, ac = _bf16(cn, "evidence_down", "cn"), _bf16(an, "evidence_down", "an")
+    d = cc.shape[-1]
+    r = weight.shape[0]
+    if ac.shape != cc.shape or weight.shape != (r, 2 * d) or bias.shape != (r,):
+        raise ValueError("evidence_down: cn and an must match and the layer be Linear(2 d, r)")
+    if not evidence_down_fits(d, r):
+        raise ValueError(f"evidence_down: needs d a multiple of 128 and r in (16, 32, 48, 64), got d={d}, r={r}")
+    w = _aligned16(weight.to(torch.bfloat16))
+    b = bias.to(torch.bfloat16).contiguous()
+    z = torch.empty((*cc.shape[:-1], r), device=cn.device, dtype=torch.bfloat16)
+    rows = cc.numel() // d
+    status = lib.tf_evidence_down(cc.data_ptr(), ac.data_ptr(), w.data_ptr(), b.data_ptr(), z.data_ptr(), rows, d, r,
+                                  _lib.stream_of(cn))
+    _lib.check(status, "evidence_down")
+    return z
+
+
 def merge_conv(cn, mn, an, g, layer, lengths):
     """``add(v, depthwise_masked(v, layer), bf16=True)`` with ``v = gated_concat(cat(cn,
     mn, an), g)`` (``trifusion_amd::merge_conv``)."""

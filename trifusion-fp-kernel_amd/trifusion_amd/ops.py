@@ -72,6 +72,7 @@ _SCHEMAS = {
         "merge_gate(Tensor cn, Tensor mf, Tensor mb, Tensor an, Tensor norm_weight, float eps, Tensor gate_weight, "
         "Tensor gate_bias) -> (Tensor, Tensor)"
     ),
+    "evidence_down": "evidence_down(Tensor cn, Tensor an, Tensor weight, Tensor bias) -> Tensor",
     "merge_conv": (
         "merge_conv(Tensor cn, Tensor mn, Tensor an, Tensor g, Tensor weight, Tensor bias, Tensor lengths) -> Tensor"
     ),
@@ -338,6 +339,10 @@ def _meta_merge_gate(cn, mf, mb, an, norm_weight, eps, gate_weight, gate_bias):
     return cn.new_empty(cn.shape, dtype=torch.float32), cn.new_empty((*cn.shape[:-1], 3), dtype=torch.bfloat16)
 
 
+def _meta_evidence_down(cn, an, weight, bias):
+    return cn.new_empty((*cn.shape[:-1], weight.shape[0]), dtype=torch.bfloat16)
+
+
 def _meta_merge_conv(cn, mn, an, g, weight, bias, lengths):
     return cn.new_empty((*cn.shape[:-1], 3 * cn.shape[-1]), dtype=torch.bfloat16)
 
@@ -414,8 +419,8 @@ _KERNELS = {
         name: (_block(name), globals()["_meta_" + name])
         for name in ("depthwise_masked", "pool4", "rotary_qkv", "front_norm", "interpolate", "bands",
                      "evidence_norm", "gated_concat", "front_conv1", "front_conv2", "block_pre", "norm_silu",
-                     "glu_depthwise", "pooled_attention", "merge_gate", "merge_conv", "query_read", "mask_audio",
-                     "log_power", "front_lengths", "grids")
+                     "glu_depthwise", "pooled_attention", "merge_gate", "evidence_down", "merge_conv", "query_read",
+                     "mask_audio", "log_power", "front_lengths", "grids")
     },
 }
 

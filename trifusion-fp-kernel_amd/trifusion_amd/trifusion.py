@@ -39,6 +39,8 @@ from .kernels.block import (
     bands,
     block_pre,
     depthwise_masked,
+    evidence_down,
+    evidence_down_fits,
     evidence_norm,
     front_norm,
     front_stage,
@@ -371,7 +373,10 @@ class TriFusionBlock(nn.Module):
         cn = self.cn(local.out(norm_silu(glu_depthwise(local.up(h), local.dw, lengths), local.norm)))
         att = self.attention
         an = self.an(grids.interpolate(att.out(pooled_attention(att.qkv(p), grids, att.heads))))
-        z = F.silu(self.e_down(torch.cat((cn, an), -1)))
+        if evidence_down_fits(d, self.e_down.out_features):
+            z = evidence_down(cn, an, self.e_down)
+        else:
+            z = F.silu(self.e_down(torch.cat((cn, an), -1)))
         ev, eg = self.e_value, self.e_gate
         wv = self._joined("evidence", (ev.weight, ev.bias, eg.weight, eg.bias),
                           lambda: (torch.cat((ev.weight, eg.weight)), torch.cat((ev.bias, eg.bias))))
