@@ -138,11 +138,13 @@ def test_merge_gate_and_conv():
     assert torch.equal(y, add(v, conv, bf16=True))
 
 
-@pytest.mark.parametrize("rows, d, r", [(3 * 101, 1024, 64), (101, 128, 16), (37, 256, 48), (1, 384, 32), (0, 128, 64)])
+@pytest.mark.parametrize("rows, d, r", [(3 * 101, 1024, 64), (101, 128, 16), (37, 256, 48), (1, 384, 32), (0, 128, 64),
+                                        (1616, 1024, 64), (70, 640, 48), (45, 1536, 64), (33, 1280, 16)])
 def test_evidence_down(rows, d, r):
     """silu(e_down(cat(cn, an))) in one launch: the oracle's composition, and the
     unfused GPU composition under autocast, within two bf16 steps (the linear's
-    output and the SiLU are each rounded; the sums run in another order)."""
+    output and the SiLU are each rounded; the sums run in another order). d up
+    to 1024 runs the LDS-staged kernel, wider d the direct-load kernel."""
     g = gen(5)
     cn = (torch.randn(rows, d, generator=g) * 1.5).to(BF)
     an = (torch.randn(rows, d, generator=g) * 0.5).to(BF)
