@@ -194,6 +194,16 @@ __device__ __forceinline__ void load_pipe_angles(const MfmaParams& P, float (&th
 // Segment summaries a thread of the seeded walk loads per round trip.
 constexpr int kSeedBatch = 8;
 
+// First chunk of segment g of a unit's time axis: the ceil(T / 64) chunks
+// split as evenly as G segments allow, the first (chunks mod G) segments one
+// chunk longer. A later segment's walk first scans the summaries of every
+// segment before it, so the segments that scan the most walk the fewest chunks.
+__device__ __forceinline__ int seg_start(const MfmaParams& P, int g) {
+  const int chunks = (P.T + kChunk - 1) / kChunk;
+  const int base = chunks / P.G, extra = chunks % P.G;
+  return g * base + min(g, extra);
+}
+
 // Raw 16-byte row pieces of the wave's eight channels (lane = row).
 struct PipeRows {
   u32x4 q, k, v;
@@ -359,8 +369,8 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
   }
   const int nvalid = (L + kChunk - 1) / kChunk;
   // the segment's chunks [c0, c1) of the valid prefix
-  const int c0 = min(seg * P.SC, nvalid);
-  const int c1 = min(c0 + P.SC, nvalid);
+  const int c0 = min(seg_start(P, seg), nvalid);
+  const int c1 = min(seg_start(P, seg + 1), nvalid);
   const int tlim = P.rev ? L : T;
   const int roff = P.rev ? max(L - 1, 0) : 0;
   const uint16_t* qbase = P.q + b * P.q_sb + qh * P.q_sh - roff * P.q_st;
@@ -894,8 +904,8 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
     // alignment the output rows are checked for)
     const int o_st = P.rev ? -P.o_st : P.o_st;
     const int obase_fwd = b * P.o_sb + h * P.o_sh;
-    const int r0 = max(L, seg * P.SC * kChunk);
-    const int r1 = seg == P.G - 1 ? T : min(T, (seg + 1) * P.SC * kChunk);
+    const int r0 = max(L, seg_start(P, seg) * kChunk);
+    const int r1 = seg == P.G - 1 ? T : min(T, seg_start(P, seg + 1) * kChunk);
     for (int e = r0 * 16 + static_cast<int>(threadIdx.x); e < r1 * 16; e += 768) {
       const int tt = e >> 4, piece = e & 15;
       const int off = obase_fwd + tt * o_st + 4 * piece;
@@ -970,8 +980,8 @@ __global__ __launch_bounds__(1024) void pipe_summary_kernel(const MfmaParams P) 
     L = l < 0 ? 0 : (l > T ? T : static_cast<int>(l));
   }
   const int nvalid = (L + kChunk - 1) / kChunk;
-  const int c0 = min(it.seg * P.SC, nvalid);
-  const int c1 = min(c0 + P.SC, nvalid);
+  const int c0 = min(seg_start(P, it.seg), nvalid);
+  const int c1 = min(seg_start(P, it.seg + 1), nvalid);
   const int tlim = P.rev ? L : T;
   const int roff = P.rev ? max(L - 1, 0) : 0;
   const uint16_t* kbase = P.k + b * P.k_sb + qh * P.k_sh - roff * P.k_st;
@@ -1147,8 +1157,8 @@ __global__ __launch_bounds__(1024) void pipe_summary_kernel(const MfmaParams P) 
 }
 
 // Chunk-parallel plan: with at most 128 (batch, head) units, each unit's time
-// axis is cut into G segments of SC chunks so that units * G is about one
-// workgroup per CU. Scratch: states [units][G][4096] fp32, phase sums
+// axis is cut into G segments of at most SC chunks (seg_start) so that
+// units * G is about one workgroup per CU. Scratch: states [units][G][4096] fp32, phase sums
 // [units][G][32] uint32, decays [units][G] fp32, each 256-byte aligned.
 constexpr int64_t kMinSegmentChunks = 4;
 
