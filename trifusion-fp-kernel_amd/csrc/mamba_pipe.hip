@@ -915,10 +915,11 @@ __global__ __launch_bounds__(768) void mamba_pipe_kernel(const MfmaParams P) {
     for (int e = r0 * 16 + static_cast<int>(threadIdx.x); e < r1 * 16; e += 768) {
       const int tt = e >> 4, piece = e & 15;
       const int off = obase_fwd + tt * o_st + 4 * piece;
+      // streaming stores, as the walk's (varlen batches: 24.4 -> 23.3 us)
       if constexpr (OUT32)
-        *reinterpret_cast<float4*>(static_cast<float*>(P.out) + off) = make_float4(0.f, 0.f, 0.f, 0.f);
+        __builtin_nontemporal_store(u32x4{0u, 0u, 0u, 0u}, reinterpret_cast<u32x4*>(static_cast<float*>(P.out) + off));
       else
-        *reinterpret_cast<u32x2*>(static_cast<uint16_t*>(P.out) + off) = u32x2{0u, 0u};
+        __builtin_nontemporal_store(u32x2{0u, 0u}, reinterpret_cast<u32x2*>(static_cast<uint16_t*>(P.out) + off));
     }
   }
 }
