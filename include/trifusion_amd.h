@@ -457,7 +457,8 @@ int tf_glu_depthwise(const void *up, const void *w, const void *bias, const int6
 
 /*
  * Attention on the pooled grid: qkv bf16 [B, T, 3, H, D] (D 32 or 64); q and k
- * rotated by interleaved pairs with cos/sin fp32 [T, D/2] and rounded to bf16;
+ * rotated by interleaved pairs with cos/sin fp32 [T, D/2] (contiguous, 16-byte
+ * aligned, as qkv and y are) and rounded to bf16;
  * softmax(q k^T / sqrt(D)) v in fp32 over keys j < low_lengths[b]; y bf16
  * [B, T, H D]. Replaces RotaryQKV + masked_attention + the head merge of
  * GlobalAttention (src/trifusion_l4/model.py:84-104, attention.py:8-18).

@@ -291,27 +291,22 @@ __global__ __launch_bounds__(256) void glu_depthwise_kernel(const uint16_t* __re
 // keys j < low_length with one online softmax, G keys at a time (independent
 // dot products). Keys (rotated and rounded to bf16 like the rotary kernel's
 // output) and values of 64 positions at a time sit in LDS as bf16.
-template <int D>
-__device__ __forceinline__ void rotate_row(const uint16_t* src, const float* cs, const float* sn, bool rot,
-                                          float (&o)[D]) {
+
+// Rotation of the 8 dims 8 c8 .. 8 c8 + 7 of a row (pairs 4 c8 .. 4 c8 + 3):
+// x1 cos - x2 sin and x1 sin + x2 cos with separate multiplies and adds, rounded
+// to bf16, as the reference's rotary forms them. cs4, sn4: the pairs' cos and
+// sin (16-byte aligned).
+__device__ __forceinline__ void rotate8(const uint16_t* src, const float* cs4, const float* sn4, float (&o)[8]) {
 #pragma clang fp contract(off)
+  float v[8];
+  ld8(src, v);
+  const float4 c = *reinterpret_cast<const float4*>(cs4), n = *reinterpret_cast<const float4*>(sn4);
+  const float co[4] = {c.x, c.y, c.z, c.w}, si[4] = {n.x, n.y, n.z, n.w};
 #pragma unroll
-  for (int c8 = 0; c8 < D / 8; ++c8) {
-    float v[8];
-    ld8(src + 8 * c8, v);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float a = v[2 * e], z = v[2 * e + 1];
-      const int c = 4 * c8 + e;
-      if (rot) {
-        const float co = cs[c], si = sn[c];
-        o[8 * c8 + 2 * e] = round_bf16(a * co - z * si);
-        o[8 * c8 + 2 * e + 1] = round_bf16(a * si + z * co);
-      } else {
-        o[8 * c8 + 2 * e] = a;
-        o[8 * c8 + 2 * e + 1] = z;
-      }
-    }
+  for (int e = 0; e < 4; ++e) {
+    const float a = v[2 * e], z = v[2 * e + 1];
+    o[2 * e] = round_bf16(a * co[e] - z * si[e]);
+    o[2 * e + 1] = round_bf16(a * si[e] + z * co[e]);
   }
 }
 
@@ -337,19 +332,20 @@ __global__ __launch_bounds__(64) void attention_kernel(const uint16_t* __restric
   const int t = blockIdx.x * kAttQueries + qi, h = blockIdx.y, b = blockIdx.z;
   const int LL = clamp_len(low_lengths, b, LT);
   const int64_t width = static_cast<int64_t>(3) * H * D;
+  constexpr int G8 = D / 8;  // 8-dim groups per row
+  // the lane's own dims of its query, rotated (groups part DP / 8 ..)
   float q[DP];
   {
     const int tq = t < LT ? t : 0;
-    float full[D];
-    rotate_row<D>(qkv + (static_cast<int64_t>(b) * LT + tq) * width + static_cast<int64_t>(h) * D,
-                  cs + static_cast<int64_t>(tq) * (D / 2), sn + static_cast<int64_t>(tq) * (D / 2), true, full);
+    const uint16_t* qrow = qkv + (static_cast<int64_t>(b) * LT + tq) * width + static_cast<int64_t>(h) * D;
 #pragma unroll
-    for (int i = 0; i < DP; ++i) {
-      float v = 0.f;
+    for (int gi = 0; gi < DP / 8; ++gi) {
+      const int c8 = part * (DP / 8) + gi;
+      float o[8];
+      rotate8(qrow + 8 * c8, cs + static_cast<int64_t>(tq) * (D / 2) + 4 * c8,
+              sn + static_cast<int64_t>(tq) * (D / 2) + 4 * c8, o);
 #pragma unroll
-      for (int pp = 0; pp < kAttSplit; ++pp)
-        if (pp == part) v = full[pp * DP + i];
-      q[i] = v;
+      for (int e = 0; e < 8; ++e) q[8 * gi + e] = o[e];
     }
   }
   float acc[DP];
@@ -357,26 +353,23 @@ __global__ __launch_bounds__(64) void attention_kernel(const uint16_t* __restric
   for (int i = 0; i < DP; ++i) acc[i] = 0.f;
   float m = -INFINITY, l = 0.f;
   for (int j0 = 0; j0 < LL; j0 += 64) {
-    const int j = j0 + lane;
-    if (j < LL) {
+    const int nk = min(64, LL - j0);
+    // stage the tile's keys (rotated) and values: task (row r, group c8) per
+    // lane, G8 lanes per row, so a load instruction reads whole 128-byte rows.
+    // Rows past the tile's keys repeat its last key (never read by the scores).
+#pragma unroll
+    for (int it = 0; it < G8; ++it) {
+      const int idx = lane + 64 * it, r = idx / G8, c8 = idx % G8;
+      const int j = j0 + min(r, nk - 1);
       const uint16_t* row = qkv + (static_cast<int64_t>(b) * LT + j) * width + static_cast<int64_t>(h) * D;
-      float kr[D];
-      rotate_row<D>(row + static_cast<int64_t>(H) * D, cs + static_cast<int64_t>(j) * (D / 2),
-                    sn + static_cast<int64_t>(j) * (D / 2), true, kr);
-#pragma unroll
-      for (int i = 0; i < D; i += 8) {
-        float o[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] = kr[i + e];
-        st8_bf16(ks + lane * RS + i, o);
-      }
-      const uint16_t* vrow = row + static_cast<int64_t>(2) * H * D;
-#pragma unroll
-      for (int i = 0; i < D; i += 8)
-        *reinterpret_cast<uint4*>(vs + lane * RS + i) = *reinterpret_cast<const uint4*>(vrow + i);
+      float o[8];
+      rotate8(row + static_cast<int64_t>(H) * D + 8 * c8, cs + static_cast<int64_t>(j) * (D / 2) + 4 * c8,
+              sn + static_cast<int64_t>(j) * (D / 2) + 4 * c8, o);
+      st8_bf16(ks + r * RS + 8 * c8, o);
+      *reinterpret_cast<uint4*>(vs + r * RS + 8 * c8) =
+          *reinterpret_cast<const uint4*>(row + static_cast<int64_t>(2) * H * D + 8 * c8);
     }
     __syncthreads();
-    const int nk = min(64, LL - j0);
     const uint16_t* kp = ks + part * DP;
     const uint16_t* vp = vs + part * DP;
     for (int jb = 0; jb < nk; jb += kAttGroup) {
@@ -677,7 +670,8 @@ extern "C" int tf_pooled_attention(const void* qkv, const float* cos_t, const fl
   if (!qkv || !cos_t || !sin_t || !low_lengths || !y) return TF_ERR_NULL;
   if (batch < 0 || low_time < 0 || heads < 1 || heads > 65535 || batch > 65535 || batch * low_time > 0x7fffffff)
     return TF_ERR_SHAPE;
-  if (!tf::a16(qkv) || !tf::a16(y)) return TF_ERR_SHAPE;
+  // the tables are read 4 pairs (16 bytes) at a time
+  if (!tf::a16(qkv) || !tf::a16(y) || !tf::a16(cos_t) || !tf::a16(sin_t)) return TF_ERR_SHAPE;
   if (batch * low_time == 0) return TF_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid(static_cast<uint32_t>((low_time + tf::kAttQueries - 1) / tf::kAttQueries),
