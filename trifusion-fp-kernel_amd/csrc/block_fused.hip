@@ -453,6 +453,9 @@ __global__ __launch_bounds__(256) void merge_gate_kernel(const uint16_t* __restr
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (row >= rows) return;
   float v[PER8][8];
+  // the row's cn and an pieces and the norm weights, requested with mf and mb
+  // so that the gate's dot products do not wait for a second round trip
+  float sc[PER8][8], sa[PER8][8], wv[PER8][8];
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < PER8; ++i) {
@@ -461,6 +464,9 @@ __global__ __launch_bounds__(256) void merge_gate_kernel(const uint16_t* __restr
       float bv[8];
       ld8(mf + row * d + i0, v[i]);
       ld8(mb + row * d + i0, bv);
+      ld8(cn + row * d + i0, sc[i]);
+      ld8(an + row * d + i0, sa[i]);
+      ld8(w + i0, wv[i]);
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[i][e] = (v[i][e] + bv[e]) * 0.5f;
     } else {
@@ -478,13 +484,10 @@ __global__ __launch_bounds__(256) void merge_gate_kernel(const uint16_t* __restr
   for (int i = 0; i < PER8; ++i) {
     const int i0 = 8 * (lane + 64 * i);
     if (i0 < d) {
-      float wv[8], o[8], sc[8], sa[8];
-      ld8(w + i0, wv);
+      float o[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = v[i][e] * r * wv[e];
+      for (int e = 0; e < 8; ++e) o[e] = v[i][e] * r * wv[i][e];
       st8_f32(mn + row * d + i0, o);
-      ld8(cn + row * d + i0, sc);
-      ld8(an + row * d + i0, sa);
 #pragma unroll
       for (int jj = 0; jj < 3; ++jj) {
         float w0[8], w1[8], w2[8];
@@ -492,7 +495,7 @@ __global__ __launch_bounds__(256) void merge_gate_kernel(const uint16_t* __restr
         ld8(gw + jj * d3 + d + i0, w1);
         ld8(gw + jj * d3 + 2 * d + i0, w2);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) dot[jj] += sc[e] * w0[e] + round_bf16(o[e]) * w1[e] + sa[e] * w2[e];
+        for (int e = 0; e < 8; ++e) dot[jj] += sc[i][e] * w0[e] + round_bf16(o[e]) * w1[e] + sa[i][e] * w2[e];
       }
     }
   }
