@@ -61,6 +61,20 @@ def test_pool4_and_interpolate(dtype):
     close(y, O.interpolate(ref_low, left, right, alpha, lengths), dtype)
 
 
+@pytest.mark.parametrize("d", [36, 1024])
+def test_interpolate_widths(d):
+    """The 8-wide vector form (d % 8 == 0) and the per-element form (d = 36)."""
+    g = gen(7)
+    lengths = torch.tensor([101, 57, 4])
+    low_lengths, left, right, alpha = O.grids(lengths, 101)
+    low = torch.randn(3, left.max().item() + 1, d, generator=g).to(BF)
+    grids = SimpleNamespace(left=left.to(DEV), right=right.to(DEV), alpha=alpha.to(DEV), lengths=lengths.to(DEV))
+    y = interpolate(low.to(DEV), grids)
+    ref = O.interpolate(low, left, right, alpha, lengths)
+    close(y, ref, BF)
+    assert not y[1, 57:].float().any() and not y[2, 4:].float().any()
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, BF])
 def test_rotary_qkv(dtype):
     g = gen(2)

@@ -135,6 +135,39 @@ __global__ __launch_bounds__(256) void front_norm_kernel(const T* __restrict__ x
   }
 }
 
+// 8 consecutive elements of a row as fp32 (16- or 32-byte aligned loads and stores).
+template <typename T>
+__device__ __forceinline__ void load8v(const T* p, float (&v)[8]) {
+  if constexpr (sizeof(T) == 4) {
+    const float4 a = reinterpret_cast<const float4*>(p)[0];
+    const float4 b = reinterpret_cast<const float4*>(p)[1];
+    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+  } else {
+    const uint4 u = *reinterpret_cast<const uint4*>(p);
+    const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[2 * e] = to_f32(__builtin_bit_cast(T, static_cast<uint16_t>(wd[e] & 0xffffu)));
+      v[2 * e + 1] = to_f32(__builtin_bit_cast(T, static_cast<uint16_t>(wd[e] >> 16)));
+    }
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void store8v(T* p, const float (&v)[8]) {
+  if constexpr (sizeof(T) == 4) {
+    reinterpret_cast<float4*>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
+    reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
+  } else {
+    uint32_t wd[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      wd[e] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, from_f32<T>(v[2 * e]))) |
+              (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, from_f32<T>(v[2 * e + 1]))) << 16);
+    *reinterpret_cast<uint4*>(p) = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+  }
+}
+
 // y[b, t, c] = t < L ? a + (z - a) alpha : 0, a = low[b, left[b, t], c],
 // z = low[b, right[b, t], c] (kernels/native.py:_interpolate). One block per row.
 template <typename T>
@@ -161,6 +194,37 @@ __global__ __launch_bounds__(256) void interpolate_kernel(const T* __restrict__ 
       o = a + (z - a) * al;
     }
     y[row * D + c] = from_f32<T>(o);
+  }
+}
+
+// interpolate_kernel through 8-element vectors (D % 8 == 0, 16-byte aligned
+// rows), 128 threads per row. The row's neighbour indices and weight are read
+// whatever the row's length, so the data loads wait for one round trip only.
+template <typename T>
+__global__ __launch_bounds__(128) void interpolate_vec_kernel(const T* __restrict__ low,
+                                                              const int64_t* __restrict__ left,
+                                                              const int64_t* __restrict__ right,
+                                                              const float* __restrict__ alpha,
+                                                              const int64_t* __restrict__ lengths, T* __restrict__ y,
+                                                              int Tn, int LT, int D) {
+  const int64_t row = blockIdx.x;
+  const int b = static_cast<int>(row / Tn);
+  const int t = static_cast<int>(row - static_cast<int64_t>(b) * Tn);
+  const int64_t l0 = left[row], r0 = right[row];
+  const float al0 = alpha[row];
+  const bool valid = t < dev_len(lengths, b, Tn);
+  const int64_t l = valid ? (l0 < 0 ? 0 : (l0 >= LT ? LT - 1 : l0)) : 0;
+  const int64_t r = valid ? (r0 < 0 ? 0 : (r0 >= LT ? LT - 1 : r0)) : 0;
+  const float al = valid ? al0 : 0.f;
+  const T* pa = low + (static_cast<int64_t>(b) * LT + l) * D;
+  const T* pz = low + (static_cast<int64_t>(b) * LT + r) * D;
+  for (int c = 8 * static_cast<int>(threadIdx.x); c < D; c += 8 * static_cast<int>(blockDim.x)) {
+    float a[8], z[8], o[8];
+    load8v(pa + c, a);
+    load8v(pz + c, z);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = valid ? a[e] + (z[e] - a[e]) * al : 0.f;
+    store8v(y + row * D + c, o);
   }
 }
 
@@ -214,38 +278,6 @@ __global__ __launch_bounds__(256) void evidence_norm_kernel(const float* __restr
 
 // evidence_norm_kernel through 8-element vectors: one wave per row, lane holds
 // elements 8 (lane + 64 i) .. +7, i < PER8.
-template <typename T>
-__device__ __forceinline__ void load8v(const T* p, float (&v)[8]) {
-  if constexpr (sizeof(T) == 4) {
-    const float4 a = reinterpret_cast<const float4*>(p)[0];
-    const float4 b = reinterpret_cast<const float4*>(p)[1];
-    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
-  } else {
-    const uint4 u = *reinterpret_cast<const uint4*>(p);
-    const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      v[2 * e] = to_f32(__builtin_bit_cast(T, static_cast<uint16_t>(wd[e] & 0xffffu)));
-      v[2 * e + 1] = to_f32(__builtin_bit_cast(T, static_cast<uint16_t>(wd[e] >> 16)));
-    }
-  }
-}
-
-template <typename T>
-__device__ __forceinline__ void store8v(T* p, const float (&v)[8]) {
-  if constexpr (sizeof(T) == 4) {
-    reinterpret_cast<float4*>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
-    reinterpret_cast<float4*>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
-  } else {
-    uint32_t wd[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      wd[e] = static_cast<uint32_t>(__builtin_bit_cast(uint16_t, from_f32<T>(v[2 * e]))) |
-              (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, from_f32<T>(v[2 * e + 1]))) << 16);
-    *reinterpret_cast<uint4*>(p) = make_uint4(wd[0], wd[1], wd[2], wd[3]);
-  }
-}
-
 template <typename TA, typename TY, int PER8>
 __global__ __launch_bounds__(256) void evidence_norm_vec_kernel(const float* __restrict__ x,
                                                                 const TA* __restrict__ a, const TA* __restrict__ g,
@@ -382,6 +414,14 @@ extern "C" int tf_interpolate(const void* low, int32_t dtype, const int64_t* lef
   if (batch < 0 || time < 0 || low_time < 1 || d < 1 || batch * time > 0x7fffffff) return TF_ERR_SHAPE;
   if (batch * time == 0) return TF_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // 16-byte rows (d % 8 == 0 for every dtype) from 16-byte aligned bases
+  const bool vec = d % 8 == 0 && (reinterpret_cast<uintptr_t>(low) & 15) == 0 && (reinterpret_cast<uintptr_t>(y) & 15) == 0;
+  if (vec)
+    TF_DISPATCH(dtype, T,
+                hipLaunchKernelGGL(tf::interpolate_vec_kernel<T>, TF_ROW_GRID(batch * time), dim3(128), 0, s,
+                                   static_cast<const T*>(low), left, right, alpha, lengths, static_cast<T*>(y),
+                                   static_cast<int>(time), static_cast<int>(low_time), static_cast<int>(d));
+                return tf::launch_status());
   TF_DISPATCH(dtype, T,
               hipLaunchKernelGGL(tf::interpolate_kernel<T>, TF_ROW_GRID(batch * time), dim3(256), 0, s,
                                  static_cast<const T*>(low), left, right, alpha, lengths, static_cast<T*>(y),
