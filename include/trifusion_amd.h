@@ -371,6 +371,18 @@ int tf_interpolate(const void *low, int32_t dtype, const int64_t *left, const in
                    int64_t low_time, int64_t d, void *stream);
 
 /*
+ * tf_interpolate followed by RMSNorm of each output row, in one pass:
+ *   v = dtype(interpolated row), y = dtype(v rsqrt(mean(v^2) + eps) w)
+ * w fp32 [D]; D a multiple of 8 up to 4096; low, y and w 16-byte aligned. The
+ * same values as tf_interpolate then tf_rmsnorm. Replaces self.an(attention(h))
+ * of the TriFusion block, whose attention ends in grids.interpolate
+ * (src/trifusion_l4/model.py:104,160).
+ */
+int tf_interpolate_rmsnorm(const void *low, int32_t dtype, const int64_t *left, const int64_t *right,
+                           const float *alpha, const int64_t *lengths, const float *w, float eps, void *y,
+                           int64_t batch, int64_t time, int64_t low_time, int64_t d, void *stream);
+
+/*
  * Eight frequency bands of a [B, C, T, F] map (strides[4]), written contiguous
  * [B, T, 8, C]: band i averages frequencies floor(i F/8) .. ceil((i+1) F/8) - 1,
  * the adaptive average pool of src/trifusion_l4/front.py:94-101. Replaces

@@ -9,8 +9,11 @@ import pytest
 import torch
 
 from oracle import trifusion as O
+from oracle.elementwise import rms_norm
 from trifusion_amd.kernels import gated_concat
 from trifusion_amd.kernels.buffers import Pool4, RotaryQKV, depthwise_masked, front_norm
+from trifusion_amd.kernels import RMSNorm
+from trifusion_amd.kernels.block import interpolate_rmsnorm
 from trifusion_amd.kernels.native import bands, evidence_norm, interpolate
 
 pytestmark = pytest.mark.gpu
@@ -72,6 +75,31 @@ def test_interpolate_widths(d):
     y = interpolate(low.to(DEV), grids)
     ref = O.interpolate(low, left, right, alpha, lengths)
     close(y, ref, BF)
+    assert not y[1, 57:].float().any() and not y[2, 4:].float().any()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, BF])
+@pytest.mark.parametrize("d", [1024, 520])
+def test_interpolate_rmsnorm(d, dtype):
+    """One pass equals interpolate then the RMSNorm launch bit for bit (same
+    rounding of the interpolated row, same summation order), and the oracle's
+    composition within one rounding."""
+    g = gen(8)
+    lengths = torch.tensor([101, 57, 4])
+    low_lengths, left, right, alpha = O.grids(lengths, 101)
+    low = torch.randn(3, 26, d, generator=g).to(dtype)
+    norm = RMSNorm(d)
+    with torch.no_grad():
+        norm.weight.copy_(torch.rand(d, generator=g) + 0.5)
+    grids = SimpleNamespace(left=left.to(DEV), right=right.to(DEV), alpha=alpha.to(DEV), lengths=lengths.to(DEV))
+    dn = norm.to(DEV)
+    y = interpolate_rmsnorm(low.to(DEV), grids, dn)
+    two = dn(interpolate(low.to(DEV), grids))
+    torch.cuda.synchronize()
+    assert torch.equal(y.cpu(), two.cpu())
+    mid = O.interpolate(low, left, right, alpha, lengths)
+    ref = rms_norm(mid, norm.weight.detach().cpu(), norm.eps)
+    close(y, ref, dtype)
     assert not y[1, 57:].float().any() and not y[2, 4:].float().any()
 
 

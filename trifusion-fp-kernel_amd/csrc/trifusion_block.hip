@@ -228,6 +228,71 @@ __global__ __launch_bounds__(128) void interpolate_vec_kernel(const T* __restric
   }
 }
 
+// interpolate then RMSNorm of each row in one pass: one wave per row, lane
+// holding elements 8 (lane + 64 j) .. +7, j < PER8, the layout and summation
+// order of the RMSNorm kernel (row_norm_vec_kernel), so the result is the one
+// the two launches give. The interpolated value is rounded to T as the
+// interpolation's output is; rows past the length are 0 before the norm.
+template <typename T, int PER8>
+__global__ __launch_bounds__(256) void interp_norm_kernel(const T* __restrict__ low,
+                                                          const int64_t* __restrict__ left,
+                                                          const int64_t* __restrict__ right,
+                                                          const float* __restrict__ alpha,
+                                                          const int64_t* __restrict__ lengths,
+                                                          const float* __restrict__ w, T* __restrict__ y,
+                                                          int64_t rows, int Tn, int LT, int D, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int b = static_cast<int>(row / Tn);
+  const int t = static_cast<int>(row - static_cast<int64_t>(b) * Tn);
+  const int64_t l0 = left[row], r0 = right[row];
+  const float al0 = alpha[row];
+  const bool valid = t < dev_len(lengths, b, Tn);
+  const int64_t l = valid ? (l0 < 0 ? 0 : (l0 >= LT ? LT - 1 : l0)) : 0;
+  const int64_t r = valid ? (r0 < 0 ? 0 : (r0 >= LT ? LT - 1 : r0)) : 0;
+  const float al = valid ? al0 : 0.f;
+  const T* pa = low + (static_cast<int64_t>(b) * LT + l) * D;
+  const T* pz = low + (static_cast<int64_t>(b) * LT + r) * D;
+  float v[PER8][8];
+#pragma unroll
+  for (int j = 0; j < PER8; ++j) {
+    const int i0 = 8 * (lane + 64 * j);
+    if (i0 < D) {
+      float a[8], z[8];
+      load8v(pa + i0, a);
+      load8v(pz + i0, z);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[j][e] = to_f32(from_f32<T>(valid ? a[e] + (z[e] - a[e]) * al : 0.f));
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[j][e] = 0.f;
+    }
+  }
+  // The sum of squares as the RMSNorm kernel's compiled code forms it (its
+  // source adds v * v in element order, contracted): the first two terms as
+  // fma(v0, v0, v1 v1), then one fused multiply-add per element in order.
+  float ss = __builtin_fmaf(v[0][0], v[0][0], v[0][1] * v[0][1]);
+#pragma unroll
+  for (int j = 0; j < PER8; ++j) {
+#pragma unroll
+    for (int e = j == 0 ? 2 : 0; e < 8; ++e) ss = __builtin_fmaf(v[j][e], v[j][e], ss);
+  }
+  ss = wave_sum(ss);
+  const float rn = rsqrtf(ss / static_cast<float>(D) + eps);
+#pragma unroll
+  for (int j = 0; j < PER8; ++j) {
+    const int i0 = 8 * (lane + 64 * j);
+    if (i0 < D) {
+      float wv[8], o[8];
+      load8v(w + i0, wv);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = v[j][e] * rn * wv[e];
+      store8v(y + row * D + i0, o);
+    }
+  }
+}
+
 // [B, C, T, F] (any strides) -> [B, T, 8, C]: band i averages frequencies
 // floor(i F / 8) .. ceil((i + 1) F / 8) - 1 (kernels/native.py:_bands). One
 // thread per output element.
@@ -428,6 +493,35 @@ extern "C" int tf_interpolate(const void* low, int32_t dtype, const int64_t* lef
                                  static_cast<int>(time), static_cast<int>(low_time), static_cast<int>(d));
               return tf::launch_status());
   return TF_ERR_DTYPE;
+}
+
+extern "C" int tf_interpolate_rmsnorm(const void* low, int32_t dtype, const int64_t* left, const int64_t* right,
+                                      const float* alpha, const int64_t* lengths, const float* w, float eps, void* y,
+                                      int64_t batch, int64_t time, int64_t low_time, int64_t d, void* stream) {
+  if (!low || !left || !right || !alpha || !lengths || !w || !y) return TF_ERR_NULL;
+  if (batch < 0 || time < 0 || low_time < 1 || d < 8 || d % 8 || d > 4096 || batch * time > 0x7fffffff)
+    return TF_ERR_SHAPE;
+  if ((reinterpret_cast<uintptr_t>(low) & 15) || (reinterpret_cast<uintptr_t>(y) & 15) ||
+      (reinterpret_cast<uintptr_t>(w) & 15))
+    return TF_ERR_STRIDE;
+  const int64_t rows = batch * time;
+  if (rows == 0) return TF_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<uint32_t>((rows + 3) / 4)), block(256);
+  int per8 = 1;
+  while (per8 * 512 < d) per8 <<= 1;
+#define TF_IN(P)                                                                                                 \
+  if (per8 == P) {                                                                                               \
+    TF_DISPATCH(dtype, T,                                                                                        \
+                hipLaunchKernelGGL((tf::interp_norm_kernel<T, P>), grid, block, 0, s, static_cast<const T*>(low), \
+                                   left, right, alpha, lengths, w, static_cast<T*>(y), rows, static_cast<int>(time), \
+                                   static_cast<int>(low_time), static_cast<int>(d), eps);                        \
+                return tf::launch_status());                                                                     \
+    return TF_ERR_DTYPE;                                                                                         \
+  }
+  TF_IN(1) TF_IN(2) TF_IN(4) TF_IN(8)
+#undef TF_IN
+  return TF_ERR_SHAPE;
 }
 
 extern "C" int tf_bands(const void* x, int32_t dtype, const int64_t* strides, void* y, int64_t batch, int64_t chans,

@@ -256,6 +256,39 @@ def launch_interpolate(low, left, right, alpha, lengths):
     return y
 
 
+def interpolate_rmsnorm_fits(low):
+    """Rows ``tf_interpolate_rmsnorm`` takes: a width that is a multiple of 8 up to 4096."""
+    d = low.shape[-1]
+    return d % 8 == 0 and 8 <= d <= 4096
+
+
+def interpolate_rmsnorm(low, grids, norm):
+    """``norm(interpolate(low, grids))`` in one pass, the values the two
+    launches give (``trifusion_amd::interpolate_rmsnorm``)."""
+    return ops.interpolate_rmsnorm(low, grids.left, grids.right, grids.alpha, grids.lengths, norm.weight,
+                                   float(norm.eps))
+
+
+def launch_interpolate_rmsnorm(low, left, right, alpha, lengths, weight, eps):
+    lib = _lib.load()
+    _lib.require_cuda(low, left, right, alpha, lengths, weight, what="interpolate_rmsnorm")
+    low = _aligned16(low)
+    b, lt, d = low.shape
+    t = left.shape[1]
+    if weight.shape != (d,):
+        raise ValueError(f"interpolate_rmsnorm: weight must be [{d}]")
+    w = _aligned16(weight.float())
+    y = low.new_empty((b, t, d))
+    status = lib.tf_interpolate_rmsnorm(
+        low.data_ptr(), _lib.dtype_code(low, "interpolate_rmsnorm"), left.to(torch.int64).contiguous().data_ptr(),
+        right.to(torch.int64).contiguous().data_ptr(), alpha.float().contiguous().data_ptr(),
+        lengths.to(torch.int64).contiguous().data_ptr(), w.data_ptr(), float(eps), y.data_ptr(), b, t, lt, d,
+        _lib.stream_of(low),
+    )
+    _lib.check(status, "interpolate_rmsnorm")
+    return y
+
+
 def bands(x):
     """``[B, C, T, F]`` -> ``[B, T, 8, C]`` frequency-band means (``trifusion_amd::bands``)."""
     return ops.bands(x)

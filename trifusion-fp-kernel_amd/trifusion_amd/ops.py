@@ -55,6 +55,10 @@ _SCHEMAS = {
     "rotary_qkv": "rotary_qkv(Tensor x, Tensor cos, Tensor sin, int heads) -> Tensor",
     "front_norm": "front_norm(Tensor x, Tensor lengths, Tensor weight, float eps, bool silu) -> Tensor",
     "interpolate": "interpolate(Tensor low, Tensor left, Tensor right, Tensor alpha, Tensor lengths) -> Tensor",
+    "interpolate_rmsnorm": (
+        "interpolate_rmsnorm(Tensor low, Tensor left, Tensor right, Tensor alpha, Tensor lengths, Tensor weight, "
+        "float eps) -> Tensor"
+    ),
     "bands": "bands(Tensor x) -> Tensor",
     "evidence_norm": (
         "evidence_norm(Tensor x, Tensor value, Tensor gate, Tensor weight, Tensor? mask, float eps, "
@@ -308,6 +312,10 @@ def _meta_interpolate(low, left, right, alpha, lengths):
     return low.new_empty((low.shape[0], left.shape[1], low.shape[2]))
 
 
+def _meta_interpolate_rmsnorm(low, left, right, alpha, lengths, weight, eps):
+    return low.new_empty((low.shape[0], left.shape[1], low.shape[2]))
+
+
 def _meta_bands(x):
     b, c, t, f = x.shape
     return x.new_empty((b, t, 8, c))
@@ -417,7 +425,8 @@ _KERNELS = {
     "small_linear": (_cuda_small_linear, _meta_small_linear),
     **{
         name: (_block(name), globals()["_meta_" + name])
-        for name in ("depthwise_masked", "pool4", "rotary_qkv", "front_norm", "interpolate", "bands",
+        for name in ("depthwise_masked", "pool4", "rotary_qkv", "front_norm", "interpolate", "interpolate_rmsnorm",
+                     "bands",
                      "evidence_norm", "gated_concat", "front_conv1", "front_conv2", "block_pre", "norm_silu",
                      "glu_depthwise", "pooled_attention", "merge_gate", "evidence_down", "merge_conv", "query_read",
                      "mask_audio", "log_power", "front_lengths", "grids")

@@ -46,6 +46,8 @@ from .kernels.block import (
     front_stage,
     glu_depthwise,
     interpolate,
+    interpolate_rmsnorm,
+    interpolate_rmsnorm_fits,
     merge_conv,
     merge_gate,
     norm_silu,
@@ -372,7 +374,11 @@ class TriFusionBlock(nn.Module):
         local = self.local
         cn = self.cn(local.out(norm_silu(glu_depthwise(local.up(h), local.dw, lengths), local.norm)))
         att = self.attention
-        an = self.an(grids.interpolate(att.out(pooled_attention(att.qkv(p), grids, att.heads))))
+        low = att.out(pooled_attention(att.qkv(p), grids, att.heads))
+        if interpolate_rmsnorm_fits(low):
+            an = interpolate_rmsnorm(low, grids, self.an)
+        else:
+            an = self.an(grids.interpolate(low))
         if evidence_down_fits(d, self.e_down.out_features):
             z = evidence_down(cn, an, self.e_down)
         else:
