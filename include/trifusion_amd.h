@@ -468,6 +468,16 @@ int tf_glu_depthwise(const void *up, const void *w, const void *bias, const int6
                      int64_t batch, int64_t time, int64_t d, int64_t k, void *stream);
 
 /*
+ * tf_glu_depthwise followed by tf_norm_silu in one launch (d a multiple of 8 up
+ * to 1024, k 3 or 7; norm_w fp32 [d], 16-byte aligned): the values of the two
+ * launches. Replaces the LocalCNN's glu -> depthwise conv -> norm -> silu
+ * (src/trifusion_l4/model.py:73-76, kernels/buffers.py:13-32).
+ */
+int tf_glu_depthwise_norm_silu(const void *up, const void *w, const void *bias, const int64_t *lengths,
+                               const float *norm_w, float eps, void *y, int64_t batch, int64_t time, int64_t d,
+                               int64_t k, void *stream);
+
+/*
  * Attention on the pooled grid: qkv bf16 [B, T, 3, H, D] (D 32 or 64); q and k
  * rotated by interleaved pairs with cos/sin fp32 [T, D/2] (contiguous, 16-byte
  * aligned, as qkv and y are) and rounded to bf16;

@@ -24,6 +24,7 @@ from trifusion_amd.kernels.block import (
     evidence_down,
     evidence_norm,
     glu_depthwise,
+    glu_norm_silu,
     merge_conv,
     merge_gate,
     norm_silu,
@@ -90,6 +91,24 @@ def test_glu_depthwise_and_norm_silu(k):
     s = norm_silu(ref.to(DEV), n.to(DEV))
     close_bf16(s, O.norm_silu(ref, n.weight.detach().cpu()))
     assert torch.equal(s, F.silu(n(ref.to(DEV))))
+
+
+@pytest.mark.parametrize("k", [3, 7])
+@pytest.mark.parametrize("d", [1024, 520, 128])
+def test_glu_norm_silu_equals_two_launches(d, k):
+    """GLU + depthwise + RMSNorm + SiLU in one launch gives the values of
+    glu_depthwise then norm_silu, bit for bit (rows past the length included)."""
+    g = gen(10 + k)
+    up = (torch.randn(3, 101, 2 * d, generator=g) * 2).to(BF).to(DEV)
+    layer = torch.nn.Conv1d(d, d, k, padding=k // 2, groups=d).to(DEV)
+    n = norm(d, g).to(DEV)
+    lengths = LENGTHS.to(DEV)
+    print(f"case glu_norm_silu d={d} k={k}", flush=True)
+    with torch.inference_mode():
+        y = glu_norm_silu(up, layer, lengths, n)
+        two = norm_silu(glu_depthwise(up, layer, lengths), n)
+    torch.cuda.synchronize()
+    assert y.shape == two.shape and torch.equal(y, two)
 
 
 @pytest.mark.parametrize("t,heads,hd", [(26, 16, 64), (101, 8, 32)])

@@ -285,6 +285,117 @@ __global__ __launch_bounds__(256) void glu_depthwise_kernel(const uint16_t* __re
   }
 }
 
+// ---- GLU + masked depthwise conv, then RMSNorm + SiLU of each output row -------
+// glu_depthwise_kernel followed by norm_silu_kernel in one launch: one
+// workgroup per (TW time steps, batch row) owns whole rows (d <= 512 PER8). The
+// GLU rows of the tile go to LDS (bf16) as glu_depthwise forms them; wave w
+// convolves output rows t0 + TO w .. + TO - 1 for every channel (lane = channel
+// groups 8 (lane + 64 j)), rounds them to bf16 as glu_depthwise's output is, and
+// normalises each row as norm_silu does (same per-lane order of the sum of
+// squares), so the values are those of the two launches.
+template <int K, int TW, int PER8>
+__global__ __launch_bounds__(256) void glu_norm_silu_kernel(const uint16_t* __restrict__ up,
+                                                            const uint16_t* __restrict__ w,
+                                                            const uint16_t* __restrict__ bias,
+                                                            const int64_t* __restrict__ lengths,
+                                                            const float* __restrict__ nw, uint16_t* __restrict__ y,
+                                                            int T, int d, float eps) {
+  constexpr int R = TW + K - 1;
+  constexpr int TO = TW / 4;
+  static_assert(TW % 4 == 0, "four waves share the tile's time steps");
+  extern __shared__ uint4 glu_s[];  // [R][d / 8]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int t0 = blockIdx.x * TW, b = blockIdx.y;
+  const int L = clamp_len(lengths, b, T);
+  const int d8 = d / 8;
+  for (int idx = static_cast<int>(threadIdx.x); idx < R * d8; idx += 256) {
+    const int r = idx / d8, c8 = idx - r * d8;
+    const int t = t0 - K / 2 + r;
+    float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (t >= 0 && t < T) {
+      float a[8], g[8];
+      const uint16_t* src = up + (static_cast<int64_t>(b) * T + t) * 2 * d;
+      ld8(src + 8 * c8, a);
+      ld8(src + d + 8 * c8, g);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = a[e] * (1.0f / (1.0f + expf(-g[e])));
+    }
+    uint32_t wd[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      wd[e] = static_cast<uint32_t>(f32_to_bf16(o[2 * e])) | (static_cast<uint32_t>(f32_to_bf16(o[2 * e + 1])) << 16);
+    glu_s[r * d8 + c8] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+  }
+  __syncthreads();
+  float cv[TO][PER8][8];
+#pragma unroll
+  for (int j = 0; j < PER8; ++j) {
+    const int c8 = lane + 64 * j;
+    if (c8 < d8) {
+      float wk[8][K], bb[8];
+      load_taps<K>(w + static_cast<int64_t>(8 * c8) * K, bias + 8 * c8, wk, bb);
+      float win[TO + K - 1][8];
+#pragma unroll
+      for (int r = 0; r < TO + K - 1; ++r) {
+        const uint4 q = glu_s[(wave * TO + r) * d8 + c8];
+        const uint32_t wd[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          win[r][2 * e] = __uint_as_float(wd[e] << 16);
+          win[r][2 * e + 1] = __uint_as_float(wd[e] & 0xffff0000u);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < TO; ++i) {
+        const int t = t0 + wave * TO + i;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float acc = 0.f;
+          if (t < L) {
+#pragma unroll
+            for (int q = 0; q < K; ++q) acc = add_nc(acc, mul_nc(win[i + q][e], wk[e][q]));
+            acc = add_nc(acc, bb[e]);
+          }
+          cv[i][j][e] = round_bf16(acc);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < TO; ++i)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) cv[i][j][e] = 0.f;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < TO; ++i) {
+    const int t = t0 + wave * TO + i;
+    if (t < T) {  // wave-uniform
+      float ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < PER8; ++j) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += cv[i][j][e] * cv[i][j][e];
+      }
+      ss = wave_sum(ss);
+      const float r = rsqrtf(ss / static_cast<float>(d) + eps);
+#pragma unroll
+      for (int j = 0; j < PER8; ++j) {
+        const int c8 = lane + 64 * j;
+        if (c8 < d8) {
+          float wv[8], o[8];
+          ld8(nw + 8 * c8, wv);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float n = round_bf16(cv[i][j][e] * r * wv[e]);
+            o[e] = n / (1.0f + expf(-n));
+          }
+          st8_bf16(y + (static_cast<int64_t>(b) * T + t) * d + 8 * c8, o);
+        }
+      }
+    }
+  }
+}
+
 // ---- rotary + masked attention on the pooled grid -------------------------------
 // One wave per (tile of 16 queries, head, batch row). Each query belongs to four
 // lanes, each holding a quarter of its head dims; together they walk the valid
@@ -592,6 +703,7 @@ int per8_of(int64_t d) {
 
 constexpr int kTT = 4;     // time steps per depthwise tile (merge_conv)
 constexpr int kGluTW = 8;  // time steps per GLU + depthwise workgroup
+constexpr int kGnsTW = 4;  // time steps per GLU + depthwise + norm + SiLU workgroup
 
 }  // namespace
 }  // namespace tf
@@ -641,6 +753,31 @@ extern "C" int tf_norm_silu(const void* x, const float* w, void* y, int64_t rows
       return TF_ERR_SHAPE;
   }
 #undef TF_NS
+}
+
+extern "C" int tf_glu_depthwise_norm_silu(const void* up, const void* w, const void* bias, const int64_t* lengths,
+                                          const float* norm_w, float eps, void* y, int64_t batch, int64_t time,
+                                          int64_t d, int64_t k, void* stream) {
+  if (!up || !w || !bias || !lengths || !norm_w || !y) return TF_ERR_NULL;
+  if (batch < 0 || time < 0 || d < 8 || d % 8 || d > 1024 || batch > 65535 || batch * time > 0x7fffffff ||
+      (time + tf::kGnsTW - 1) / tf::kGnsTW > 65535)
+    return TF_ERR_SHAPE;
+  if (!tf::a16(up) || !tf::a16(y) || !tf::a16(w) || !tf::a16(bias) || !tf::a16(norm_w)) return TF_ERR_SHAPE;
+  if (batch * time == 0) return TF_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<uint32_t>((time + tf::kGnsTW - 1) / tf::kGnsTW), static_cast<uint32_t>(batch));
+  const size_t lds = static_cast<size_t>(tf::kGnsTW + k - 1) * (d / 8) * 16;
+#define TF_GNS(KV, P)                                                                                            \
+  if (k == KV && (d <= 512 * P) && (P == 1 || d > 512 * (P / 2))) {                                              \
+    hipLaunchKernelGGL((tf::glu_norm_silu_kernel<KV, tf::kGnsTW, P>), grid, dim3(256), lds, s,                 \
+                       static_cast<const uint16_t*>(up), static_cast<const uint16_t*>(w),                        \
+                       static_cast<const uint16_t*>(bias), lengths, norm_w, static_cast<uint16_t*>(y),          \
+                       static_cast<int>(time), static_cast<int>(d), eps);                                        \
+    return tf::launch_status();                                                                                  \
+  }
+  TF_GNS(3, 1) TF_GNS(3, 2) TF_GNS(7, 1) TF_GNS(7, 2)
+#undef TF_GNS
+  return TF_ERR_SHAPE;
 }
 
 extern "C" int tf_glu_depthwise(const void* up, const void* w, const void* bias, const int64_t* lengths, void* y,

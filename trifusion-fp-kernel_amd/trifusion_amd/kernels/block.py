@@ -437,6 +437,36 @@ def launch_glu_depthwise(up, weight, bias, lengths):
     return y
 
 
+def glu_norm_silu_fits(up, layer):
+    """Shapes ``tf_glu_depthwise_norm_silu`` takes: d a multiple of 8 up to 1024, k 3 or 7."""
+    d = up.shape[-1] // 2
+    return d % 8 == 0 and 8 <= d <= 1024 and layer.weight.shape[-1] in (3, 7)
+
+
+def glu_norm_silu(up, layer, lengths, norm):
+    """``norm_silu(glu_depthwise(up, layer, lengths), norm)`` in one launch, the
+    values of the two (``trifusion_amd::glu_norm_silu``)."""
+    return ops.glu_norm_silu(up, layer.weight, layer.bias, lengths, norm.weight, float(norm.eps))
+
+
+def launch_glu_norm_silu(up, weight, bias, lengths, norm_weight, eps):
+    lib = _lib.load()
+    _lib.require_cuda(up, weight, bias, lengths, norm_weight, what="glu_norm_silu")
+    uc = _bf16(up, "glu_norm_silu", "up")
+    b, t, d2 = uc.shape
+    d, k = d2 // 2, weight.shape[-1]
+    if weight.numel() != d * k or bias.shape != (d,) or norm_weight.shape != (d,):
+        raise ValueError("glu_norm_silu: weight must be [d, 1, k], bias and norm weight [d]")
+    w = _aligned16(weight.to(torch.bfloat16))
+    bb = _aligned16(bias.to(torch.bfloat16))
+    nw = _aligned16(norm_weight.float())
+    y = torch.empty((b, t, d), device=up.device, dtype=torch.bfloat16)
+    status = lib.tf_glu_depthwise_norm_silu(uc.data_ptr(), w.data_ptr(), bb.data_ptr(), _lengths(lengths).data_ptr(),
+                                            nw.data_ptr(), float(eps), y.data_ptr(), b, t, d, k, _lib.stream_of(up))
+    _lib.check(status, "glu_norm_silu")
+    return y
+
+
 def pooled_attention(qkv, grids, heads):
     """Rotary + masked attention on the pooled grid: ``qkv [B, T, 3 H D]`` bf16 ->
     ``[B, T, H D]`` bf16 (``trifusion_amd::pooled_attention``)."""

@@ -77,6 +77,9 @@ _SCHEMAS = {
         "Tensor gate_bias) -> (Tensor, Tensor)"
     ),
     "evidence_down": "evidence_down(Tensor cn, Tensor an, Tensor weight, Tensor bias) -> Tensor",
+    "glu_norm_silu": (
+        "glu_norm_silu(Tensor up, Tensor weight, Tensor bias, Tensor lengths, Tensor norm_weight, float eps) -> Tensor"
+    ),
     "merge_conv": (
         "merge_conv(Tensor cn, Tensor mn, Tensor an, Tensor g, Tensor weight, Tensor bias, Tensor lengths) -> Tensor"
     ),
@@ -347,6 +350,10 @@ def _meta_merge_gate(cn, mf, mb, an, norm_weight, eps, gate_weight, gate_bias):
     return cn.new_empty(cn.shape, dtype=torch.float32), cn.new_empty((*cn.shape[:-1], 3), dtype=torch.bfloat16)
 
 
+def _meta_glu_norm_silu(up, weight, bias, lengths, norm_weight, eps):
+    return up.new_empty((*up.shape[:-1], up.shape[-1] // 2), dtype=torch.bfloat16)
+
+
 def _meta_evidence_down(cn, an, weight, bias):
     return cn.new_empty((*cn.shape[:-1], weight.shape[0]), dtype=torch.bfloat16)
 
@@ -428,7 +435,7 @@ _KERNELS = {
         for name in ("depthwise_masked", "pool4", "rotary_qkv", "front_norm", "interpolate", "interpolate_rmsnorm",
                      "bands",
                      "evidence_norm", "gated_concat", "front_conv1", "front_conv2", "block_pre", "norm_silu",
-                     "glu_depthwise", "pooled_attention", "merge_gate", "evidence_down", "merge_conv", "query_read",
+                     "glu_depthwise", "glu_norm_silu", "pooled_attention", "merge_gate", "evidence_down", "merge_conv", "query_read",
                      "mask_audio", "log_power", "front_lengths", "grids")
     },
 }

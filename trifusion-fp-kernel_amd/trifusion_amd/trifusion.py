@@ -45,6 +45,8 @@ from .kernels.block import (
     front_norm,
     front_stage,
     glu_depthwise,
+    glu_norm_silu,
+    glu_norm_silu_fits,
     interpolate,
     interpolate_rmsnorm,
     interpolate_rmsnorm_fits,
@@ -372,7 +374,11 @@ class TriFusionBlock(nn.Module):
         b, t, d = x.shape
         x, h, p = block_pre(x, lengths, self.pre)
         local = self.local
-        cn = self.cn(local.out(norm_silu(glu_depthwise(local.up(h), local.dw, lengths), local.norm)))
+        up = local.up(h)
+        if glu_norm_silu_fits(up, local.dw):
+            cn = self.cn(local.out(glu_norm_silu(up, local.dw, lengths, local.norm)))
+        else:
+            cn = self.cn(local.out(norm_silu(glu_depthwise(up, local.dw, lengths), local.norm)))
         att = self.attention
         low = att.out(pooled_attention(att.qkv(p), grids, att.heads))
         if interpolate_rmsnorm_fits(low):
