@@ -453,6 +453,15 @@ int tf_block_pre(const float *x, const int64_t *lengths, const float *w, float e
                  int64_t batch, int64_t time, int64_t d, void *stream);
 
 /*
+ * tf_block_pre of x + addend (addend bf16 [B, T, d], added in fp32 before the
+ * mask): the previous block's closing masked residual add (tf_add of the
+ * residual and the FFN down-projection, src/trifusion_l4/model.py:199) and this
+ * block's start in one launch, the values of the two.
+ */
+int tf_block_pre_add(const float *x, const void *addend, const int64_t *lengths, const float *w, float eps,
+                     float *xm, void *h, void *p, int64_t batch, int64_t time, int64_t d, void *stream);
+
+/*
  * RMSNorm of bf16 rows [rows, d] rounded to bf16, then SiLU rounded to bf16.
  * Replaces F.silu(self.norm(h)) of LocalCNN (src/trifusion_l4/model.py:74).
  */

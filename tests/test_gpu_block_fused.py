@@ -20,6 +20,7 @@ from trifusion_amd.kernels import RMSNorm, gated_concat
 from trifusion_amd.kernels.block import (
     Pool4,
     block_pre,
+    block_pre_add,
     depthwise_masked,
     evidence_down,
     evidence_norm,
@@ -72,6 +73,24 @@ def test_block_pre():
     uh = n(um)
     assert torch.equal(h, uh.to(BF))
     assert torch.equal(p, Pool4.apply(uh, LENGTHS.to(DEV)).to(BF))
+
+
+@pytest.mark.parametrize("d", [1024, 128])
+def test_block_pre_add_equals_add_then_block_pre(d):
+    """The previous block's closing masked add applied by the start kernel: the
+    values of tf_add then tf_block_pre, bit for bit."""
+    g = gen(21)
+    r = torch.randn(3, 101, d, generator=g).to(DEV)
+    down = torch.randn(3, 101, d, generator=g).to(BF).to(DEV)
+    n = norm(d, g).to(DEV)
+    mask = time_mask(LENGTHS, 101).to(DEV)
+    print(f"case block_pre_add d={d}", flush=True)
+    with torch.inference_mode():
+        fused = block_pre_add(r, down, LENGTHS.to(DEV), n)
+        two = block_pre(add(r, down, mask), LENGTHS.to(DEV), n)
+    torch.cuda.synchronize()
+    for a, b in zip(fused, two):
+        assert torch.equal(a, b)
 
 
 @pytest.mark.parametrize("k", [3, 7])

@@ -78,8 +78,9 @@ __device__ __forceinline__ float add_nc(float a, float b) {
 // (t >= L -> 0, written to xm), normalised like the fp32 row norm (wave per row,
 // lane holds elements 8 (lane + 64 i) .. +7) and written as bf16; the fp32 norm
 // rows meet in LDS for the pooled row: sum over valid rows in order, / count.
-template <int PER8>
+template <int PER8, bool ADD>
 __global__ __launch_bounds__(256) void block_pre_kernel(const float* __restrict__ x,
+                                                        const uint16_t* __restrict__ addend,
                                                         const int64_t* __restrict__ lengths,
                                                         const float* __restrict__ w, float* __restrict__ xm,
                                                         uint16_t* __restrict__ h16, uint16_t* __restrict__ p16,
@@ -102,6 +103,13 @@ __global__ __launch_bounds__(256) void block_pre_kernel(const float* __restrict_
       const int i0 = 8 * (lane + 64 * i);
       if (i0 < d) {
         ld8(x + row * d + i0, v[i]);
+        if constexpr (ADD) {
+          // the previous block's closing residual add (masked add kernel: a + b in fp32)
+          float av[8];
+          ld8(addend + row * d + i0, av);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[i][e] = v[i][e] + av[e];
+        }
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[i][e] = keep ? v[i][e] : 0.f;
         st8_f32(xm + row * d + i0, v[i]);
@@ -708,24 +716,52 @@ constexpr int kGnsTW = 4;  // time steps per GLU + depthwise + norm + SiLU workg
 }  // namespace
 }  // namespace tf
 
+namespace tf {
+namespace {
+int launch_block_pre(const float* x, const uint16_t* addend, const int64_t* lengths, const float* w, float eps,
+                     float* xm, void* h, void* p, int64_t batch, int64_t time, int64_t d, hipStream_t s);
+}  // namespace
+}  // namespace tf
+
 extern "C" int tf_block_pre(const float* x, const int64_t* lengths, const float* w, float eps, float* xm, void* h,
                             void* p, int64_t batch, int64_t time, int64_t d, void* stream) {
+  return tf::launch_block_pre(x, nullptr, lengths, w, eps, xm, h, p, batch, time, d,
+                              static_cast<hipStream_t>(stream));
+}
+
+extern "C" int tf_block_pre_add(const float* x, const void* addend, const int64_t* lengths, const float* w,
+                                float eps, float* xm, void* h, void* p, int64_t batch, int64_t time, int64_t d,
+                                void* stream) {
+  if (!addend) return TF_ERR_NULL;
+  if (!tf::a16(addend)) return TF_ERR_SHAPE;
+  return tf::launch_block_pre(x, static_cast<const uint16_t*>(addend), lengths, w, eps, xm, h, p, batch, time, d,
+                              static_cast<hipStream_t>(stream));
+}
+
+namespace tf {
+namespace {
+int launch_block_pre(const float* x, const uint16_t* addend, const int64_t* lengths, const float* w, float eps,
+                     float* xm, void* h, void* p, int64_t batch, int64_t time, int64_t d, hipStream_t s) {
   if (!x || !lengths || !w || !xm || !h || !p) return TF_ERR_NULL;
   if (batch < 0 || time < 0 || d < 8 || d % 8 || d > 4096 || batch > 65535 || batch * time > 0x7fffffff)
     return TF_ERR_SHAPE;
-  if (!tf::a16(x) || !tf::a16(w) || !tf::a16(xm) || !tf::a16(h) || !tf::a16(p)) return TF_ERR_SHAPE;
+  if (!a16(x) || !a16(w) || !a16(xm) || !a16(h) || !a16(p)) return TF_ERR_SHAPE;
   const int64_t lt = (time + 3) / 4;
   if (batch * lt == 0) return TF_OK;
-  hipStream_t s = static_cast<hipStream_t>(stream);
   const dim3 grid(static_cast<uint32_t>(lt), static_cast<uint32_t>(batch));
   const size_t lds = 4 * static_cast<size_t>(d) * sizeof(float);
-  const int per8 = tf::per8_of(d);
+  const int per8 = per8_of(d);
 #define TF_PRE(P)                                                                                                \
   case P:                                                                                                         \
-    hipLaunchKernelGGL(tf::block_pre_kernel<P>, grid, dim3(256), lds, s, x, lengths, w, xm,                      \
-                       static_cast<uint16_t*>(h), static_cast<uint16_t*>(p), static_cast<int>(time),              \
-                       static_cast<int>(lt), static_cast<int>(d), eps);                                           \
-    return tf::launch_status();
+    if (addend)                                                                                                   \
+      hipLaunchKernelGGL((block_pre_kernel<P, true>), grid, dim3(256), lds, s, x, addend, lengths, w, xm,        \
+                         static_cast<uint16_t*>(h), static_cast<uint16_t*>(p), static_cast<int>(time),            \
+                         static_cast<int>(lt), static_cast<int>(d), eps);                                         \
+    else                                                                                                          \
+      hipLaunchKernelGGL((block_pre_kernel<P, false>), grid, dim3(256), lds, s, x, addend, lengths, w, xm,       \
+                         static_cast<uint16_t*>(h), static_cast<uint16_t*>(p), static_cast<int>(time),            \
+                         static_cast<int>(lt), static_cast<int>(d), eps);                                         \
+    return launch_status();
   switch (per8) {
     TF_PRE(1) TF_PRE(2) TF_PRE(4) TF_PRE(8)
     default:
@@ -733,6 +769,8 @@ extern "C" int tf_block_pre(const float* x, const int64_t* lengths, const float*
   }
 #undef TF_PRE
 }
+}  // namespace
+}  // namespace tf
 
 extern "C" int tf_norm_silu(const void* x, const float* w, void* y, int64_t rows, int64_t d, float eps,
                             void* stream) {

@@ -135,6 +135,10 @@ _SIGNATURES = {
         [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_f32, c_ptr, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_ptr],
         c_i32,
     ),
+    "tf_block_pre_add": (
+        [c_ptr, c_ptr, c_ptr, c_ptr, c_f32, c_ptr, c_ptr, c_ptr, c_i64, c_i64, c_i64, c_ptr],
+        c_i32,
+    ),
     "tf_glu_depthwise_norm_silu": (
         [c_ptr, c_ptr, c_ptr, c_ptr, c_ptr, c_f32, c_ptr, c_i64, c_i64, c_i64, c_i64, c_ptr],
         c_i32,

@@ -398,6 +398,34 @@ def launch_block_pre(x, lengths, weight, eps):
     return xm, h, p
 
 
+def block_pre_add_fits(x, addend):
+    """``block_pre_add`` takes an fp32 residual and a bf16 addend of one shape."""
+    return x.dtype == torch.float32 and addend.dtype == torch.bfloat16 and x.shape == addend.shape
+
+
+def block_pre_add(x, addend, lengths, norm):
+    """``block_pre(add(x, addend, mask))`` in one launch, the values of the two
+    (``trifusion_amd::block_pre_add``)."""
+    return ops.block_pre_add(x, addend, lengths, norm.weight, float(norm.eps))
+
+
+def launch_block_pre_add(x, addend, lengths, weight, eps):
+    lib = _lib.load()
+    _lib.require_cuda(x, addend, lengths, weight, what="block_pre_add")
+    if x.dtype != torch.float32 or x.dim() != 3 or not block_pre_add_fits(x, addend):
+        raise TypeError("block_pre_add: x must be fp32 [B, T, d] and addend bf16 of the same shape")
+    b, t, d = x.shape
+    xc, ac, w = _aligned16(x), _aligned16(addend), _aligned16(weight.float())
+    xm = torch.empty_like(xc)
+    h = torch.empty((b, t, d), device=x.device, dtype=torch.bfloat16)
+    p = torch.empty((b, (t + 3) // 4, d), device=x.device, dtype=torch.bfloat16)
+    status = lib.tf_block_pre_add(xc.data_ptr(), ac.data_ptr(), _lengths(lengths).data_ptr(), w.data_ptr(),
+                                  float(eps), xm.data_ptr(), h.data_ptr(), p.data_ptr(), b, t, d,
+                                  _lib.stream_of(x))
+    _lib.check(status, "block_pre_add")
+    return xm, h, p
+
+
 def norm_silu(x, norm):
     """``silu(norm(x))`` of bf16 rows, both rounded to bf16 (``trifusion_amd::norm_silu``)."""
     return ops.norm_silu(x, norm.weight, float(norm.eps))

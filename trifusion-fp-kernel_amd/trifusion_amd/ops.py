@@ -67,6 +67,9 @@ _SCHEMAS = {
     "gated_concat": "gated_concat(Tensor x, Tensor gate) -> Tensor",
     "front_conv1": "front_conv1(Tensor x, Tensor weight, Tensor norm_weight, Tensor lengths, int stride, float eps) -> Tensor",
     "block_pre": "block_pre(Tensor x, Tensor lengths, Tensor weight, float eps) -> (Tensor, Tensor, Tensor)",
+    "block_pre_add": (
+        "block_pre_add(Tensor x, Tensor addend, Tensor lengths, Tensor weight, float eps) -> (Tensor, Tensor, Tensor)"
+    ),
     "norm_silu": "norm_silu(Tensor x, Tensor weight, float eps) -> Tensor",
     "glu_depthwise": "glu_depthwise(Tensor up, Tensor weight, Tensor bias, Tensor lengths) -> Tensor",
     "pooled_attention": (
@@ -334,6 +337,10 @@ def _meta_block_pre(x, lengths, weight, eps):
             x.new_empty((b, (t + 3) // 4, d), dtype=torch.bfloat16))
 
 
+def _meta_block_pre_add(x, addend, lengths, weight, eps):
+    return _meta_block_pre(x, lengths, weight, eps)
+
+
 def _meta_norm_silu(x, weight, eps):
     return torch.empty_like(x, memory_format=torch.contiguous_format)
 
@@ -433,10 +440,9 @@ _KERNELS = {
     **{
         name: (_block(name), globals()["_meta_" + name])
         for name in ("depthwise_masked", "pool4", "rotary_qkv", "front_norm", "interpolate", "interpolate_rmsnorm",
-                     "bands",
-                     "evidence_norm", "gated_concat", "front_conv1", "front_conv2", "block_pre", "norm_silu",
-                     "glu_depthwise", "glu_norm_silu", "pooled_attention", "merge_gate", "evidence_down", "merge_conv", "query_read",
-                     "mask_audio", "log_power", "front_lengths", "grids")
+                     "bands", "evidence_norm", "gated_concat", "front_conv1", "front_conv2", "block_pre",
+                     "block_pre_add", "norm_silu", "glu_depthwise", "glu_norm_silu", "pooled_attention", "merge_gate",
+                     "evidence_down", "merge_conv", "query_read", "mask_audio", "log_power", "front_lengths", "grids")
     },
 }
 

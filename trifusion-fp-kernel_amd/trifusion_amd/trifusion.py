@@ -38,6 +38,8 @@ from .kernels.block import (
     RotaryQKV,
     bands,
     block_pre,
+    block_pre_add,
+    block_pre_add_fits,
     depthwise_masked,
     evidence_down,
     evidence_down_fits,
@@ -331,9 +333,16 @@ class TriFusionBlock(nn.Module):
                 and self.attention.head_dim in (32, 64) and self.merge_dw.kernel_size[0] == 3
                 and self.local.dw.kernel_size[0] in (3, 7))
 
-    def forward(self, x, grids):
+    def forward(self, x, grids, defer=False):
+        """``defer``: the fused forward may return its closing residual add
+        unapplied, as ``(r, down)``, for the next block's start to apply
+        (``forward`` accepts such a pair as ``x``)."""
+        if isinstance(x, tuple):
+            if self.fusable(x[0]):
+                return self.forward_fused(x, grids, defer)
+            x = add(x[0], x[1], grids.mask)
         if self.fusable(x):
-            return self.forward_fused(x, grids)
+            return self.forward_fused(x, grids, defer)
         mask, lengths = grids.mask, grids.lengths
         x = mask_buffer(x, mask)
         h = self.pre(x)
@@ -364,15 +373,21 @@ class TriFusionBlock(nn.Module):
             self._fused_weights[name] = hit
         return hit[1]
 
-    def forward_fused(self, x, grids):
+    def forward_fused(self, x, grids, defer=False):
         """``forward`` with the elementwise runs between the GEMMs fused: the same
         tensors in the same dtypes as the autocast forward, the casts the GEMMs
         would make done by the producing kernels. Layers that read one input run
         as one GEMM: e_value with e_gate, and the in-projections of the two
-        Mamba directions; the two out-projections run as one batched GEMM."""
+        Mamba directions; the two out-projections run as one batched GEMM. ``x``
+        may be the previous block's unapplied closing add ``(r, down)``, which
+        the start kernel applies; with ``defer`` this block returns its own."""
         mask, lengths = grids.mask, grids.lengths
-        b, t, d = x.shape
-        x, h, p = block_pre(x, lengths, self.pre)
+        if isinstance(x, tuple):
+            b, t, d = x[0].shape
+            x, h, p = block_pre_add(x[0], x[1], lengths, self.pre)
+        else:
+            b, t, d = x.shape
+            x, h, p = block_pre(x, lengths, self.pre)
         local = self.local
         up = local.up(h)
         if glu_norm_silu_fits(up, local.dw):
@@ -409,7 +424,10 @@ class TriFusionBlock(nn.Module):
         merged = self.merge(merge_conv(cn, mn, an, g, self.merge_dw, lengths))
         r, f = add_rms(x, merged, self.ff_norm.weight, None, self.ff_norm.eps, torch.bfloat16)
         f = swiglu(self.gate_up(f))
-        return add(r, self.down(f), mask), mf, mb
+        down = self.down(f)
+        if defer and down.dtype == torch.bfloat16 and block_pre_add_fits(r, down):
+            return (r, down), mf, mb
+        return add(r, down, mask), mf, mb
 
 
 _SINPOS = {}
@@ -531,8 +549,10 @@ class TriFusion(nn.Module):
         x = self.front_projection(x).float()
         grids = Grids(main_lengths, x.shape[1], self.config.dim // self.config.heads)
         mf = mb = None
-        for block in self.blocks:
-            x, mf, mb = block(x, grids)
+        last = len(self.blocks) - 1
+        for i, block in enumerate(self.blocks):
+            # a block's closing residual add is applied by the next block's start
+            x, mf, mb = block(x, grids, defer=i < last)
         return x, fine, grids, fine_lengths, mf, mb
 
     def forward(self, audio, lengths, channels):
