@@ -1,6 +1,7 @@
 """The TriFusion-FP model (reference layout) on MI355X against the oracle's CPU
 forward of the same state dict: sigmoid probabilities within 1e-2 (the model
-tolerance), graph replay bitwise equal to eager, and a save/load round trip
+tolerance), graph replay (with its side-stream branches) bitwise equal to the
+one-stream eager forward, and a save/load round trip
 through ``load_student``."""
 
 import pytest
@@ -66,16 +67,37 @@ def test_trifusion_matches_oracle(monkeypatch):
     assert diff <= PROB_TOL
 
 
-def test_trifusion_graph_replay_equals_eager():
+def test_trifusion_graph_replay_equals_eager(monkeypatch):
+    """The captured graph forks the attention branches and the fine reads onto
+    side streams (eager calls do not): every replay, with eager forwards of
+    other inputs between them, equals the one-stream eager forward bitwise."""
     model = make_model(seed=1)
     audio, lengths, channels = (t.to(DEV) for t in inputs(seed=8))
+    other = [t.to(DEV) for t in inputs(seed=10)]
+    forks = []
+    branch = trifusion.branch_stream
+
+    def count_fork(device, slot=0):
+        forks.append(slot)
+        return branch(device, slot)
+
+    monkeypatch.setattr(trifusion, "branch_stream", count_fork)
     eng = runtime.InferenceEngine(model, graphs=True)
     eager = eng.eager(audio, lengths, channels).clone()
+    assert forks == []
+    with trifusion.eager_forks():
+        assert torch.equal(eng.eager(audio, lengths, channels), eager)
+    assert sorted(set(forks)) == [0, 1]
+    forks.clear()
     for _ in range(3):
         graph = eng(audio, lengths, channels)
         torch.cuda.synchronize()
         assert torch.equal(graph, eager)
+        eng.eager(*other)
+        torch.cuda.synchronize()
     assert eng.graph_hits >= 2
+    # two forked warm-ups and the capture
+    assert sorted(set(forks)) == [0, 1] and forks.count(0) == 3 * SMALL["depth"]
 
 
 def test_load_student_round_trip(tmp_path):

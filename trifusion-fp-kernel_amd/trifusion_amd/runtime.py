@@ -28,7 +28,7 @@ from dataclasses import fields
 import torch
 
 from .model import Encoder, ModelConfig
-from .trifusion import TriFusion, TriFusionConfig
+from .trifusion import TriFusion, TriFusionConfig, eager_forks
 
 
 def _model_kind(config):
@@ -166,12 +166,13 @@ class InferenceEngine:
 
     def _capture(self, audio, lengths, channels):
         """Record one forward reading ``audio``/``lengths``/``channels`` into a
-        graph. Two eager forwards on a side stream come first, so kernels are
-        loaded and library handles and workspaces exist before capture."""
+        graph. Two eager forwards on a side stream come first, forking onto the
+        branch streams as the capture will, so kernels are loaded and library
+        handles and workspaces exist on every stream before capture."""
         caller = torch.cuda.current_stream()
         side = torch.cuda.Stream()
         side.wait_stream(caller)
-        with torch.cuda.stream(side):
+        with torch.cuda.stream(side), eager_forks():
             self.eager(audio, lengths, channels)
             self.eager(audio, lengths, channels)
         caller.wait_stream(side)

@@ -24,6 +24,7 @@ The forward runs under bf16 autocast, as the reference's engine runs it
 (``runtime.py:79-82``). Dropout is identity at inference.
 """
 
+import contextlib
 import math
 from dataclasses import dataclass
 
@@ -315,6 +316,7 @@ class TriFusionBlock(nn.Module):
         self.gate_up = nn.Linear(d, 2 * c.ffn_dim, bias=False)
         self.down = nn.Linear(c.ffn_dim, d, bias=False)
         self._fused_weights = {}
+        self.branch_streams = True
         nn.init.zeros_(self.e_gate.weight)
         nn.init.zeros_(self.e_gate.bias)
         nn.init.normal_(self.e_value.weight, std=1e-3)
@@ -373,6 +375,14 @@ class TriFusionBlock(nn.Module):
             self._fused_weights[name] = hit
         return hit[1]
 
+    def _attention_branch(self, p, grids):
+        """Pooled attention, interpolated to frames and normalised: ``an``."""
+        att = self.attention
+        low = att.out(pooled_attention(att.qkv(p), grids, att.heads))
+        if interpolate_rmsnorm_fits(low):
+            return interpolate_rmsnorm(low, grids, self.an)
+        return self.an(grids.interpolate(low))
+
     def forward_fused(self, x, grids, defer=False):
         """``forward`` with the elementwise runs between the GEMMs fused: the same
         tensors in the same dtypes as the autocast forward, the casts the GEMMs
@@ -388,18 +398,28 @@ class TriFusionBlock(nn.Module):
         else:
             b, t, d = x.shape
             x, h, p = block_pre(x, lengths, self.pre)
+        # Under graph capture the attention branch, which reads only p, runs on
+        # the branch stream while the local branch runs here, and rejoins before
+        # the evidence path. Other eager calls stay on one stream: there the
+        # host cost of the fork outweighs the overlap.
+        side = None
+        if self.branch_streams and forking():
+            side = branch_stream(x.device)
+        if side is not None:
+            main = torch.cuda.current_stream(x.device)
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                an = self._attention_branch(p, grids)
+        else:
+            an = self._attention_branch(p, grids)
         local = self.local
         up = local.up(h)
         if glu_norm_silu_fits(up, local.dw):
             cn = self.cn(local.out(glu_norm_silu(up, local.dw, lengths, local.norm)))
         else:
             cn = self.cn(local.out(norm_silu(glu_depthwise(up, local.dw, lengths), local.norm)))
-        att = self.attention
-        low = att.out(pooled_attention(att.qkv(p), grids, att.heads))
-        if interpolate_rmsnorm_fits(low):
-            an = interpolate_rmsnorm(low, grids, self.an)
-        else:
-            an = self.an(grids.interpolate(low))
+        if side is not None:
+            main.wait_stream(side)
         if evidence_down_fits(d, self.e_down.out_features):
             z = evidence_down(cn, an, self.e_down)
         else:
@@ -428,6 +448,42 @@ class TriFusionBlock(nn.Module):
         if defer and down.dtype == torch.bfloat16 and block_pre_add_fits(r, down):
             return (r, down), mf, mb
         return add(r, down, mask), mf, mb
+
+
+_BRANCH_STREAMS = {}
+_EAGER_FORKS = [0]
+
+
+def forking():
+    """Whether forward calls fork onto the branch streams: under graph capture,
+    or inside ``eager_forks``."""
+    return _EAGER_FORKS[0] > 0 or torch.cuda.is_current_stream_capturing()
+
+
+@contextlib.contextmanager
+def eager_forks():
+    """Fork in eager calls too: the warm-ups before a capture run the captured
+    schedule, so the branch streams have their library handles and workspaces
+    before capture begins."""
+    _EAGER_FORKS[0] += 1
+    try:
+        yield
+    finally:
+        _EAGER_FORKS[0] -= 1
+
+
+def branch_stream(device, slot=0):
+    """A second stream for work that forks off the caller's, one per (device,
+    slot), at the default priority: slot 0 takes the fused block's attention
+    branch, slot 1 the decoder's fine reads. Every fork waits for the caller's
+    stream and is joined back before the forked results are used or its inputs
+    dropped, so a tensor either side allocates is freed only after both have
+    consumed it, and graph capture records the two as parallel paths."""
+    index = torch.device(device).index
+    key = (torch.cuda.current_device() if index is None else index, slot)
+    if key not in _BRANCH_STREAMS:
+        _BRANCH_STREAMS[key] = torch.cuda.Stream(device=key[0])
+    return _BRANCH_STREAMS[key]
 
 
 _SINPOS = {}
@@ -486,22 +542,16 @@ class Decoder(nn.Module):
         self.voice_head, self.music_head = nn.Linear(256, 2), nn.Linear(256, 2)
         self.file_head = nn.Sequential(nn.Linear(1536, 256), nn.SiLU(), nn.Linear(256, 1))
 
-    def forward(self, x, fine, grids, fine_lengths, mf, mb):
+    def read_fine(self, fine, fine_lengths):
+        """The reads that depend on the fine features alone: the fine mask, the
+        fine query read, the local logits and the top-k evidence means."""
         b, tf, _, _ = fine.shape
-        dev = x.device
+        dev = fine.device
         fm = time_mask(fine_lengths, tf)
-        deep = self.deep_read(self.query, x, grids.mask, grids.lengths)
         fp = fine + sin_position(tf, 64, dev, fine.dtype)[None, :, None, :] + self.band.to(fine.dtype)[None, None]
         # the fine keys are (frame, band) pairs: valid exactly below 8 * fine_lengths
         fine_q = self.fine_read(self.query, fp.flatten(1, 2), fm[:, :, None].expand(b, tf, 8).reshape(b, -1),
                                 8 * fine_lengths)
-        if x.is_cuda:
-            pooled = masked_mean(x.float(), grids.lengths)
-        else:
-            pooled = (x.float() * grids.mask[..., None]).sum(1) / grids.lengths[:, None]
-        global_feature = self.global_proj(pooled)
-        end = mf[torch.arange(b, device=dev), grids.lengths - 1]
-        memory = self.memory_proj(torch.cat((end, mb[:, 0]), -1))
         flat = fine.flatten(2)
         local, features = self.local_logits(flat), self.local_features(flat)
         k = min(25, tf)
@@ -509,6 +559,22 @@ class Decoder(nn.Module):
         picked = features[:, None].expand(-1, 2, -1, -1).gather(2, idx[..., None].expand(-1, -1, -1, 256))
         valid_k = torch.arange(k, device=dev)[None, :] < fine_lengths.clamp_max(k)[:, None]
         top = (picked.float() * valid_k[:, None, :, None]).sum(2) / valid_k.sum(1)[:, None, None]
+        return fm, fine_q, local.float(), top
+
+    def forward(self, x, fine, grids, fine_lengths, mf, mb, fine_reads=None):
+        """``fine_reads``: ``read_fine(fine, fine_lengths)`` when the caller has
+        already formed it."""
+        b = x.shape[0]
+        dev = x.device
+        fm, fine_q, local, top = fine_reads or self.read_fine(fine, fine_lengths)
+        deep = self.deep_read(self.query, x, grids.mask, grids.lengths)
+        if x.is_cuda:
+            pooled = masked_mean(x.float(), grids.lengths)
+        else:
+            pooled = (x.float() * grids.mask[..., None]).sum(1) / grids.lengths[:, None]
+        global_feature = self.global_proj(pooled)
+        end = mf[torch.arange(b, device=dev), grids.lengths - 1]
+        memory = self.memory_proj(torch.cat((end, mb[:, 0]), -1))
         voice = self.voice_lat(torch.cat((deep[0], fine_q[0], global_feature, top[:, 0], memory), -1))
         music = self.music_lat(torch.cat((deep[1], fine_q[1], global_feature, top[:, 1], memory), -1))
         v, m = self.voice_head(voice), self.music_head(music)
@@ -516,7 +582,7 @@ class Decoder(nn.Module):
         logits = torch.cat((f, v[:, :1], m[:, :1], v[:, 1:], m[:, 1:]), -1).float()
         return {
             "logits": logits,
-            "local_logits": local.float(),
+            "local_logits": local,
             "local_mask": fm,
             "features": x,
             "feature_mask": grids.mask,
@@ -537,6 +603,7 @@ class TriFusion(nn.Module):
         self.blocks = nn.ModuleList([TriFusionBlock(c) for _ in range(c.depth)])
         self.decoder = Decoder(c.dim)
         self.memory_head = nn.Linear(c.dim, 2)
+        self.fork_fine = True
 
     def set_variant(self, variant):
         """Select the recurrence kernel ("auto", "pipe", "mfma" or "generic") of every Mamba."""
@@ -545,7 +612,9 @@ class TriFusion(nn.Module):
                 m.variant = variant
 
     def encode(self, audio, lengths, channels):
-        x, fine, main_lengths, fine_lengths = self.front(audio, lengths, channels)
+        return self._blocks(*self.front(audio, lengths, channels))
+
+    def _blocks(self, x, fine, main_lengths, fine_lengths):
         x = self.front_projection(x).float()
         grids = Grids(main_lengths, x.shape[1], self.config.dim // self.config.heads)
         mf = mb = None
@@ -556,7 +625,19 @@ class TriFusion(nn.Module):
         return x, fine, grids, fine_lengths, mf, mb
 
     def forward(self, audio, lengths, channels):
-        return self.decoder(*self.encode(audio, lengths, channels))
+        front = self.front(audio, lengths, channels)
+        fine, fine_lengths = front[1], front[3]
+        if not (self.fork_fine and fine.is_cuda and forking()):
+            return self.decoder(*self._blocks(*front))
+        # Under graph capture the fine reads, which need only the front end's
+        # fine features, run on their own stream beside the blocks.
+        main, side = torch.cuda.current_stream(fine.device), branch_stream(fine.device, 1)
+        side.wait_stream(main)
+        with torch.cuda.stream(side):
+            reads = self.decoder.read_fine(fine, fine_lengths)
+        encoded = self._blocks(*front)
+        main.wait_stream(side)
+        return self.decoder(*encoded, fine_reads=reads)
 
 
 __all__ = ["TriFusion", "TriFusionConfig", "TriFusionBlock", "Frontend", "Decoder", "Grids"]
