@@ -24,6 +24,16 @@
 namespace tf {
 namespace {
 
+// Eight bf16 values (16 bytes) as floats (exact).
+__device__ __forceinline__ void unpack8(const uint4& u, float (&v)[8]) {
+  const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    v[2 * e] = __uint_as_float(wd[e] << 16);
+    v[2 * e + 1] = __uint_as_float(wd[e] & 0xffff0000u);
+  }
+}
+
 template <typename T>
 __device__ __forceinline__ void ld8(const T* p, float (&v)[8]) {
   if constexpr (sizeof(T) == 4) {
@@ -32,13 +42,7 @@ __device__ __forceinline__ void ld8(const T* p, float (&v)[8]) {
     v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w;
     v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
   } else {
-    const uint4 u = *reinterpret_cast<const uint4*>(p);
-    const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      v[2 * e] = __uint_as_float(wd[e] << 16);
-      v[2 * e + 1] = __uint_as_float(wd[e] & 0xffff0000u);
-    }
+    unpack8(*reinterpret_cast<const uint4*>(p), v);
   }
 }
 
@@ -241,22 +245,37 @@ __global__ __launch_bounds__(256) void glu_depthwise_kernel(const uint16_t* __re
   const int c8 = blockIdx.x * 64 + lane;
   const bool on = c8 < d / 8;
   const int c = 8 * c8;
-  for (int r = wave; r < R; r += 4) {
-    const int t = t0 - K / 2 + r;
-    float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    if (on && t >= 0 && t < T) {
-      float a[8], g[8];
-      const uint16_t* src = up + (static_cast<int64_t>(b) * T + t) * 2 * d;
-      ld8(src + c, a);
-      ld8(src + d + c, g);
+  // The wave's GLU rows r = wave + 4 i: every load is issued before the first
+  // is used, from a clamped row and channel (values outside the tile, [0, T) or
+  // the channels dropped), so no load waits behind the one before.
+  constexpr int NR = (R + 3) / 4;
+  uint4 ra[NR], rg[NR];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = a[e] * (1.0f / (1.0f + expf(-g[e])));
+  for (int i = 0; i < NR; ++i) {
+    const int t = min(max(t0 - K / 2 + wave + 4 * i, 0), T - 1);
+    const uint16_t* src = up + (static_cast<int64_t>(b) * T + t) * 2 * d + (on ? c : 0);
+    ra[i] = *reinterpret_cast<const uint4*>(src);
+    rg[i] = *reinterpret_cast<const uint4*>(src + d);
+  }
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    const int r = wave + 4 * i;
+    if (r < R) {
+      const int t = t0 - K / 2 + r;
+      float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      if (on && t >= 0 && t < T) {
+        float a[8], g[8];
+        unpack8(ra[i], a);
+        unpack8(rg[i], g);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = a[e] * (1.0f / (1.0f + expf(-g[e])));
+      }
+      uint32_t wd[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        wd[e] = static_cast<uint32_t>(f32_to_bf16(o[2 * e])) | (static_cast<uint32_t>(f32_to_bf16(o[2 * e + 1])) << 16);
+      glu[r][lane] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
     }
-    uint32_t wd[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      wd[e] = static_cast<uint32_t>(f32_to_bf16(o[2 * e])) | (static_cast<uint32_t>(f32_to_bf16(o[2 * e + 1])) << 16);
-    glu[r][lane] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
   }
   __syncthreads();
   if (!on) return;
@@ -316,23 +335,41 @@ __global__ __launch_bounds__(256) void glu_norm_silu_kernel(const uint16_t* __re
   const int t0 = blockIdx.x * TW, b = blockIdx.y;
   const int L = clamp_len(lengths, b, T);
   const int d8 = d / 8;
-  for (int idx = static_cast<int>(threadIdx.x); idx < R * d8; idx += 256) {
-    const int r = idx / d8, c8 = idx - r * d8;
-    const int t = t0 - K / 2 + r;
-    float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    if (t >= 0 && t < T) {
-      float a[8], g[8];
-      const uint16_t* src = up + (static_cast<int64_t>(b) * T + t) * 2 * d;
-      ld8(src + 8 * c8, a);
-      ld8(src + d + 8 * c8, g);
+  // All of the thread's GLU-row loads are issued before the first is used, at
+  // most NL of each half (d <= 512 PER8): a slot past the tile or a row outside
+  // [0, T) reads a clamped, valid address and its values are dropped. Loads
+  // consumed inside a runtime-bounded loop would each wait for the one before.
+  constexpr int NL = (R * 64 * PER8 + 255) / 256;
+  uint4 ra[NL], rg[NL];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = a[e] * (1.0f / (1.0f + expf(-g[e])));
+  for (int i = 0; i < NL; ++i) {
+    const int idx = static_cast<int>(threadIdx.x) + 256 * i;
+    const int r = idx / d8, c8 = idx < R * d8 ? idx - r * d8 : 0;
+    const int t = min(max(t0 - K / 2 + r, 0), T - 1);
+    const uint16_t* src = up + (static_cast<int64_t>(b) * T + t) * 2 * d + 8 * c8;
+    ra[i] = *reinterpret_cast<const uint4*>(src);
+    rg[i] = *reinterpret_cast<const uint4*>(src + d);
+  }
+#pragma unroll
+  for (int i = 0; i < NL; ++i) {
+    const int idx = static_cast<int>(threadIdx.x) + 256 * i;
+    if (idx < R * d8) {
+      const int r = idx / d8, c8 = idx - r * d8;
+      const int t = t0 - K / 2 + r;
+      float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      if (t >= 0 && t < T) {
+        float a[8], g[8];
+        unpack8(ra[i], a);
+        unpack8(rg[i], g);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = a[e] * (1.0f / (1.0f + expf(-g[e])));
+      }
+      uint32_t wd[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        wd[e] = static_cast<uint32_t>(f32_to_bf16(o[2 * e])) | (static_cast<uint32_t>(f32_to_bf16(o[2 * e + 1])) << 16);
+      glu_s[r * d8 + c8] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
     }
-    uint32_t wd[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e)
-      wd[e] = static_cast<uint32_t>(f32_to_bf16(o[2 * e])) | (static_cast<uint32_t>(f32_to_bf16(o[2 * e + 1])) << 16);
-    glu_s[r * d8 + c8] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
   }
   __syncthreads();
   float cv[TO][PER8][8];
