@@ -100,6 +100,31 @@ def test_trifusion_graph_replay_equals_eager(monkeypatch):
     assert sorted(set(forks)) == [0, 1] and forks.count(0) == 3 * SMALL["depth"]
 
 
+def test_forks_switched_off(monkeypatch):
+    """With the branch forks switched off the captured forward stays on the
+    caller's stream, and its replays still equal the eager forward bitwise."""
+    model = make_model(seed=3)
+    for blk in model.blocks:
+        blk.branch_streams = False
+    model.fork_fine = False
+    audio, lengths, channels = (t.to(DEV) for t in inputs(seed=11))
+    forks = []
+    branch = trifusion.branch_stream
+
+    def count_fork(device, slot=0):
+        forks.append(slot)
+        return branch(device, slot)
+
+    monkeypatch.setattr(trifusion, "branch_stream", count_fork)
+    eng = runtime.InferenceEngine(model, graphs=True)
+    eager = eng.eager(audio, lengths, channels).clone()
+    for _ in range(2):
+        graph = eng(audio, lengths, channels)
+        torch.cuda.synchronize()
+        assert torch.equal(graph, eager)
+    assert forks == [] and eng.graph_hits >= 1
+
+
 def test_load_student_round_trip(tmp_path):
     torch.manual_seed(2)
     model = TriFusion(TriFusionConfig(**SMALL)).eval()
