@@ -125,6 +125,35 @@ def test_forks_switched_off(monkeypatch):
     assert forks == [] and eng.graph_hits >= 1
 
 
+def test_capture_error_in_a_fork_falls_back(monkeypatch):
+    """An out-of-memory error raised inside the forked attention branch while
+    the graph is captured: the side stream is joined back on the way out, so
+    the capture ends cleanly, the engine sees the error, disables the shape
+    and answers eagerly; the streams stay usable."""
+    model = make_model(seed=4)
+    audio, lengths, channels = (t.to(DEV) for t in inputs(seed=12))
+    eng = runtime.InferenceEngine(model, graphs=True)
+    eager = eng.eager(audio, lengths, channels).clone()
+    cls = type(model.blocks[0])
+    branch = cls._attention_branch
+
+    def fail_in_capture(self, p, grids):
+        if torch.cuda.is_current_stream_capturing():
+            raise torch.cuda.OutOfMemoryError("forced inside the captured attention branch")
+        return branch(self, p, grids)
+
+    monkeypatch.setattr(cls, "_attention_branch", fail_in_capture)
+    out = eng(audio, lengths, channels)
+    torch.cuda.synchronize()
+    assert torch.equal(out, eager)
+    assert len(eng.disabled_shapes) == 1 and eng.graph_hits == 0
+    monkeypatch.setattr(cls, "_attention_branch", branch)
+    with trifusion.eager_forks():
+        forked = eng.eager(audio, lengths, channels)
+    torch.cuda.synchronize()
+    assert torch.equal(forked, eager)
+
+
 def test_load_student_round_trip(tmp_path):
     torch.manual_seed(2)
     model = TriFusion(TriFusionConfig(**SMALL)).eval()

@@ -375,6 +375,15 @@ class TriFusionBlock(nn.Module):
             self._fused_weights[name] = hit
         return hit[1]
 
+    def _local_branch(self, h, lengths):
+        """GLU, masked depthwise conv, norm, SiLU, out-projection and the cn
+        norm: ``cn``."""
+        local = self.local
+        up = local.up(h)
+        if glu_norm_silu_fits(up, local.dw):
+            return self.cn(local.out(glu_norm_silu(up, local.dw, lengths, local.norm)))
+        return self.cn(local.out(norm_silu(glu_depthwise(up, local.dw, lengths), local.norm)))
+
     def _attention_branch(self, p, grids):
         """Pooled attention, interpolated to frames and normalised: ``an``."""
         att = self.attention
@@ -402,24 +411,21 @@ class TriFusionBlock(nn.Module):
         # the branch stream while the local branch runs here, and rejoins before
         # the evidence path. Other eager calls stay on one stream: there the
         # host cost of the fork outweighs the overlap.
-        side = None
         if self.branch_streams and forking():
             side = branch_stream(x.device)
-        if side is not None:
             main = torch.cuda.current_stream(x.device)
             side.wait_stream(main)
-            with torch.cuda.stream(side):
-                an = self._attention_branch(p, grids)
+            try:
+                with torch.cuda.stream(side):
+                    an = self._attention_branch(p, grids)
+                cn = self._local_branch(h, lengths)
+            finally:
+                # joined on every exit: an error inside a capture (out of
+                # memory) must leave no stream forked off it
+                main.wait_stream(side)
         else:
             an = self._attention_branch(p, grids)
-        local = self.local
-        up = local.up(h)
-        if glu_norm_silu_fits(up, local.dw):
-            cn = self.cn(local.out(glu_norm_silu(up, local.dw, lengths, local.norm)))
-        else:
-            cn = self.cn(local.out(norm_silu(glu_depthwise(up, local.dw, lengths), local.norm)))
-        if side is not None:
-            main.wait_stream(side)
+            cn = self._local_branch(h, lengths)
         if evidence_down_fits(d, self.e_down.out_features):
             z = evidence_down(cn, an, self.e_down)
         else:
@@ -633,10 +639,12 @@ class TriFusion(nn.Module):
         # fine features, run on their own stream beside the blocks.
         main, side = torch.cuda.current_stream(fine.device), branch_stream(fine.device, 1)
         side.wait_stream(main)
-        with torch.cuda.stream(side):
-            reads = self.decoder.read_fine(fine, fine_lengths)
-        encoded = self._blocks(*front)
-        main.wait_stream(side)
+        try:
+            with torch.cuda.stream(side):
+                reads = self.decoder.read_fine(fine, fine_lengths)
+            encoded = self._blocks(*front)
+        finally:
+            main.wait_stream(side)
         return self.decoder(*encoded, fine_reads=reads)
 
 
