@@ -130,6 +130,32 @@ def test_glu_norm_silu_equals_two_launches(d, k):
     assert y.shape == two.shape and torch.equal(y, two)
 
 
+@pytest.mark.parametrize("k", [3, 7])
+@pytest.mark.parametrize("t,lengths", [(1, [1, 0]), (3, [3, 2]), (6, [6, 1])])
+def test_glu_short_sequences(t, lengths, k):
+    """Sequences shorter than the kernels' time tiles and the conv halo: GLU
+    rows outside [0, T) are zero (their clamped loads dropped). glu_depthwise
+    against the oracle, the one-launch form bitwise against the two launches,
+    rows past each length exactly zero."""
+    g = gen(20 + 3 * t + k)
+    d = 520
+    up = torch.randn(len(lengths), t, 2 * d, generator=g).to(BF)
+    layer = torch.nn.Conv1d(d, d, k, padding=k // 2, groups=d)
+    w, b = layer.weight.detach().clone(), layer.bias.detach().clone()
+    n = norm(d, g).to(DEV)
+    lens = torch.tensor(lengths)
+    print(f"case glu short t={t} lengths={lengths} k={k}", flush=True)
+    with torch.inference_mode():
+        y = glu_depthwise(up.to(DEV), layer.to(DEV), lens.to(DEV))
+        one = glu_norm_silu(up.to(DEV), layer.to(DEV), lens.to(DEV), n)
+        two = norm_silu(y, n)
+    torch.cuda.synchronize()
+    close_bf16(y, O.glu_depthwise(up, w, b, lens), steps=2)
+    assert torch.equal(one, two)
+    for i, length in enumerate(lengths):
+        assert not y[i, length:].any() and not one[i, length:].any()
+
+
 @pytest.mark.parametrize("t,heads,hd", [(26, 16, 64), (101, 8, 32)])
 def test_pooled_attention(t, heads, hd):
     g = gen(t)
