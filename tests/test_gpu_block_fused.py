@@ -130,6 +130,32 @@ def test_glu_norm_silu_equals_two_launches(d, k):
     assert y.shape == two.shape and torch.equal(y, two)
 
 
+@pytest.mark.parametrize("t,lengths", [(1, [1, 0]), (5, [5, 3]), (9, [9, 0, 6])])
+def test_block_pre_add_short(t, lengths):
+    """Fewer rows than a pooling group, a partial last group and zero-length
+    rows: the start kernel with the previous block's add equals tf_add then
+    tf_block_pre bit for bit, and the oracle's block start."""
+    g = gen(30 + t)
+    d = 256
+    lens = torch.tensor(lengths)
+    r = torch.randn(len(lengths), t, d, generator=g)
+    down = torch.randn(len(lengths), t, d, generator=g).to(BF)
+    n = norm(d, g).to(DEV)
+    mask = time_mask(lens, t).to(DEV)
+    print(f"case block_pre_add short t={t} lengths={lengths}", flush=True)
+    with torch.inference_mode():
+        fused = block_pre_add(r.to(DEV), down.to(DEV), lens.to(DEV), n)
+        summed = add(r.to(DEV), down.to(DEV), mask)
+        two = block_pre(summed, lens.to(DEV), n)
+    torch.cuda.synchronize()
+    for a, b in zip(fused, two):
+        assert torch.equal(a, b)
+    rm, rh, rp = O.block_pre(summed.cpu(), lens, n.weight.detach().cpu())
+    assert torch.equal(fused[0].cpu(), rm)
+    close_bf16(fused[1], rh)
+    close_bf16(fused[2], rp)
+
+
 @pytest.mark.parametrize("k", [3, 7])
 @pytest.mark.parametrize("t,lengths", [(1, [1, 0]), (3, [3, 2]), (6, [6, 1])])
 def test_glu_short_sequences(t, lengths, k):

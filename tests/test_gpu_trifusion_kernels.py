@@ -103,6 +103,31 @@ def test_interpolate_rmsnorm(d, dtype):
     assert not y[1, 57:].float().any() and not y[2, 4:].float().any()
 
 
+@pytest.mark.parametrize("t,lengths", [(1, [1, 1]), (5, [5, 1, 3]), (7, [2, 7])])
+def test_interpolate_rmsnorm_short(t, lengths):
+    """Grids of one or two pooled rows: one pass equals interpolate then the
+    RMSNorm launch bit for bit, rows past each length zero."""
+    g = gen(40 + t)
+    d = 264
+    lens = torch.tensor(lengths)
+    low_lengths, left, right, alpha = O.grids(lens, t)
+    low = torch.randn(len(lengths), (t + 3) // 4, d, generator=g).to(BF)
+    norm = RMSNorm(d)
+    with torch.no_grad():
+        norm.weight.copy_(torch.rand(d, generator=g) + 0.5)
+    grids = SimpleNamespace(left=left.to(DEV), right=right.to(DEV), alpha=alpha.to(DEV), lengths=lens.to(DEV))
+    dn = norm.to(DEV)
+    print(f"case interpolate_rmsnorm short t={t} lengths={lengths}", flush=True)
+    y = interpolate_rmsnorm(low.to(DEV), grids, dn)
+    two = dn(interpolate(low.to(DEV), grids))
+    torch.cuda.synchronize()
+    assert torch.equal(y.cpu(), two.cpu())
+    ref = rms_norm(O.interpolate(low, left, right, alpha, lens), norm.weight.detach().cpu(), norm.eps)
+    close(y, ref, BF)
+    for i, length in enumerate(lengths):
+        assert not y[i, length:].float().any()
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, BF])
 def test_rotary_qkv(dtype):
     g = gen(2)
