@@ -100,6 +100,27 @@ def test_trifusion_graph_replay_equals_eager(monkeypatch):
     assert sorted(set(forks)) == [0, 1] and forks.count(0) == 3 * SMALL["depth"]
 
 
+def test_short_clips_through_the_forked_graph():
+    """0.2 s and 0.1 s clips (a few frames after the front end, one recurrence
+    chunk, grids of one or two pooled rows): eager against the oracle, and the
+    forked graph's replay bitwise against eager."""
+    model = make_model(seed=5)
+    g = torch.Generator().manual_seed(13)
+    audio = torch.randint(-32768, 32768, (2, 1, 3200), generator=g).float() / 32768
+    lengths, channels = torch.tensor([3200, 1600]), torch.tensor([1, 1])
+    eng = runtime.InferenceEngine(model, graphs=True)
+    dev = [t.to(DEV) for t in (audio, lengths, channels)]
+    eager = eng.eager(*dev).clone()
+    ref = trifusion_forward(model.state_dict(), model.config, audio, lengths, channels)
+    diff = (eager.cpu().sigmoid() - ref.sigmoid()).abs().max().item()
+    print(f"short clips prob max diff {diff:.2e}", flush=True)
+    assert torch.isfinite(eager).all() and diff <= PROB_TOL
+    for _ in range(2):
+        graph = eng(*dev)
+        torch.cuda.synchronize()
+        assert torch.equal(graph, eager)
+
+
 def test_forks_switched_off(monkeypatch):
     """With the branch forks switched off the captured forward stays on the
     caller's stream, and its replays still equal the eager forward bitwise."""
