@@ -407,10 +407,11 @@ class TriFusionBlock(nn.Module):
         else:
             b, t, d = x.shape
             x, h, p = block_pre(x, lengths, self.pre)
-        # Under graph capture the attention branch, which reads only p, runs on
-        # the branch stream while the local branch runs here, and rejoins before
-        # the evidence path. Other eager calls stay on one stream: there the
-        # host cost of the fork outweighs the overlap.
+        # Under graph capture (and in the warm-ups before one, see eager_forks)
+        # the attention branch, which reads only p, runs on the branch stream
+        # while the local branch runs here, and rejoins before the evidence
+        # path. Other eager calls stay on one stream: there the host cost of the
+        # fork outweighs the overlap.
         if self.branch_streams and forking():
             side = branch_stream(x.device)
             main = torch.cuda.current_stream(x.device)
@@ -635,8 +636,9 @@ class TriFusion(nn.Module):
         fine, fine_lengths = front[1], front[3]
         if not (self.fork_fine and fine.is_cuda and forking()):
             return self.decoder(*self._blocks(*front))
-        # Under graph capture the fine reads, which need only the front end's
-        # fine features, run on their own stream beside the blocks.
+        # Under graph capture (and in the warm-ups before one) the fine reads,
+        # which need only the front end's fine features, run on their own
+        # stream beside the blocks.
         main, side = torch.cuda.current_stream(fine.device), branch_stream(fine.device, 1)
         side.wait_stream(main)
         try:
