@@ -263,6 +263,10 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
   // loading its rows after phase pass 1, which staggers the two halves' bursts;
   // prefetching both halves, or issuing the next controls before the scan, was
   // slower.
+  // N = 128, P = 64 with one chunk per super-chunk runs at one wave per SIMD
+  // and spills into AGPRs; the next chunk's rows are loaded where used instead
+  // of being held across the chunk.
+  constexpr bool kPrefetch = !(NT == 4 && PT == 2 && CW == 1);
   HalfRows<KS, PS> pre = {};
   for (int g0 = c_begin; g0 < c_stop; g0 += CW) {
     // Lane-derived indices are rebuilt from an index the compiler cannot see
@@ -290,7 +294,7 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
     // wave of each SIMD computes while the other waits.
     HalfRows<KS, PS> rows = {};
     if (active && hf == 0) {
-      if (g0 == c_begin)
+      if (g0 == c_begin || !kPrefetch)
         load_rows<MODE == 0>(P, rows, qbase, kbase, vbase, t0, t, L, hh);
       else
         rows = pre;
@@ -592,7 +596,7 @@ __global__ __launch_bounds__(CW * 128) void mamba_mfma_kernel(const MfmaParams P
     }
     lds_barrier();  // barrier 3: every dS share in LDS
     pre = {};
-    if (hf == 0 && g0 + CW + cw < c_stop) {
+    if (kPrefetch && hf == 0 && g0 + CW + cw < c_stop) {
       const int t0n = (g0 + CW + cw) * kChunk;
       load_rows<MODE == 0>(P, pre, qbase, kbase, vbase, t0n, t0n + c32, L, hh);
     }
